@@ -1,0 +1,407 @@
+"""CPU oracle for the FP4 MoE expert path: a numpy restatement of the reference's algorithm.
+
+THIS IS TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+may import it, and only as the checker. The product path (the HIP library) never calls it.
+
+Each function cites the reference file:line it restates (paths relative to the reference repo).
+How each one is pinned (golden vectors written by the reference's own quant.py, the compiled
+reference CPU library in oracle/_ref, closed forms, brute force) is listed in PINS below and
+checked by tests/test_oracle.py. A function marked "parity unpinned" there has no such check.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+# quant.py:22-24
+FP8_MAX = 448.0
+FP4_MAX = 6.0
+FP4_TABLE = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                      -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0], dtype=F32)
+
+PINS = {
+    "e8m0_to_f32": "golden deq_all (every scale byte) + exp2 identity",
+    "dequant_fp4": "golden deq_all (16 codes x 256 scale bytes) + golden rand_deq",
+    "tile_fp4": "golden rand_w_tiled + round trip",
+    "tile_fp4_scales": "golden rand_s_tiled + round trip",
+    "ceil_log2": "golden cl2 + brute force against log2 on powers of two",
+    "round_e4m3": "torch float8_e4m3fn cast on 2^20 samples (test_fused.py:17 twin) + exhaustive code grid",
+    "fake_quant_fp8": "golden fq8 (bf16 and fp32 inputs, edge groups)",
+    "quant_fp8": "golden qfp8 codes and scales",
+    "permute_x": "closed form: inverse permutation round trip",
+    "swiglu_quant": "compiled reference CPU library (oracle/_ref) layer output + closed form",
+    "gate_topk": "brute force (sort) on random and tied inputs",
+    "moe_dispatch": "invariants + brute force on tiny inputs",
+    "grouped_gemm": "textbook matmul against dense fp64 on tiny inputs",
+    "moe_layer": "compiled reference CPU library (oracle/_ref, bf16 mode) on I = 256",
+}
+
+
+# --------------------------------------------------------------------------- scalar formats
+def f32_bits(a) -> np.ndarray:
+    return np.asarray(a, dtype=F32).view(np.uint32)
+
+
+def bits_f32(u) -> np.ndarray:
+    return np.asarray(u, dtype=np.uint32).view(F32)
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit pattern (torch's `.to(torch.bfloat16)`).
+    NaN follows CPU torch: the sign is kept and the payload saturates (0x7FFF / 0xFFFF)."""
+    u = f32_bits(a).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    nan = np.isnan(np.asarray(a, dtype=F32))
+    r = np.where(nan, (u >> 16).astype(np.uint32) | 0x7FFF, r)
+    return (r & 0xFFFF).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return bits_f32(np.asarray(b, dtype=np.uint32) << 16)
+
+
+def bf16_round(a) -> np.ndarray:
+    """fp32 -> bf16 -> fp32 (the `.to(torch.bfloat16)` rounding point)."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(a))
+
+
+def e8m0_to_f32(b) -> np.ndarray:
+    """E8M0 byte -> fp32 2^(b-127); byte 0 is the subnormal 2^-127 and 255 is +inf (quant.py:27-31)."""
+    b = np.asarray(b, dtype=np.uint32)
+    return np.where(b == 0, bits_f32(np.uint32(0x00400000)), bits_f32(b << 23)).astype(F32)
+
+
+def ceil_log2(a) -> np.ndarray:
+    """ceil(log2(a)) for a > 0 exactly, via frexp (quant.py:34-37)."""
+    m, e = np.frexp(np.asarray(a, dtype=F32))
+    return (e - (m == 0.5)).astype(np.int32)
+
+
+def pow2_scale(amax, qmax: float) -> np.ndarray:
+    """2^ceil(log2(amax / qmax)) (quant.py:40-42); the division is an fp32 RNE division."""
+    return np.ldexp(F32(1.0), ceil_log2(np.asarray(amax, dtype=F32) / F32(qmax))).astype(F32)
+
+
+def round_e4m3(v) -> np.ndarray:
+    """Round fp32 |v| <= 448 to the nearest float8_e4m3fn value, ties to even (fused.py:24-34, the formula
+    test_fused.py:17 checks against torch's float8_e4m3fn cast)."""
+    v = np.asarray(v, dtype=F32)
+    a = np.abs(v)
+    e = ((f32_bits(a) >> 23) & 0xFF).astype(np.int32) - 127
+    e = np.maximum(e, -6)
+    ulp = np.ldexp(F32(1.0), e - 3).astype(F32)
+    r = (np.rint(a / ulp) * ulp).astype(F32)
+    r = np.minimum(r, F32(448.0))
+    # sign from the sign bit: -0.0 stays -0.0 as in torch's cast (quant.py:53); fused.py:34's
+    # `where(v < 0, -r, r)` would give +0.0 there, which quant.py (the spec) does not
+    return np.copysign(r, v).astype(F32)
+
+
+def e4m3_encode(q) -> np.ndarray:
+    """float8_e4m3fn bit pattern of values already on the E4M3 grid (|q| <= 448)."""
+    q = np.asarray(q, dtype=F32)
+    a = np.abs(q)
+    sign = (f32_bits(q) >> 31).astype(np.uint32)
+    ex = ((f32_bits(a) >> 23) & 0xFF).astype(np.int32) - 127
+    normal = a >= F32(2.0 ** -6)
+    man_n = ((f32_bits(a) >> 20) & 7).astype(np.uint32)
+    code_n = (((ex + 7).clip(0, 15).astype(np.uint32)) << 3) | man_n
+    code_s = np.rint(a * F32(512.0)).astype(np.uint32)  # subnormal: multiples of 2^-9
+    code = np.where(normal, code_n, code_s)
+    return ((sign << 7) | code).astype(np.uint8)
+
+
+def e4m3_decode(c) -> np.ndarray:
+    c = np.asarray(c, dtype=np.uint32)
+    s = np.where((c >> 7) & 1, F32(-1.0), F32(1.0))
+    e = ((c >> 3) & 15).astype(np.int32)
+    m = (c & 7).astype(F32)
+    val = np.where(e == 0, m * F32(2.0 ** -9), np.ldexp(F32(1.0) + m / F32(8.0), e - 7)).astype(F32)
+    val = np.where((c & 0x7F) == 0x7F, np.nan, val)
+    return (s * val).astype(F32)
+
+
+# --------------------------------------------------------------------------- FP4 weights
+def unpack_fp4(packed) -> np.ndarray:
+    """uint8 [..., K/2] -> fp32 [..., K] E2M1 values, low nibble = even k (quant.py:98-103)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    lo, hi = p & 0x0F, p >> 4
+    return np.stack([FP4_TABLE[lo], FP4_TABLE[hi]], axis=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+
+
+def dequant_fp4_f32(packed, scale, block: int = 32) -> np.ndarray:
+    """fp32 product E2M1 x 2^(S-127) before the bf16 cast (quant.py:106-110)."""
+    v = unpack_fp4(packed)
+    s = np.repeat(e8m0_to_f32(scale), block, axis=-1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (v * s).astype(F32)
+
+
+def dequant_fp4(packed, scale, block: int = 32) -> np.ndarray:
+    """-> bf16 bit patterns [..., K] (quant.py:106-110)."""
+    return f32_to_bf16_bits(dequant_fp4_f32(packed, scale, block))
+
+
+def dequant_fp4_values(packed, scale) -> np.ndarray:
+    """fp32 values of the bf16 dequant (what the reference's torch oracles multiply with)."""
+    return bf16_bits_to_f32(dequant_fp4(packed, scale))
+
+
+def tile_fp4(w) -> np.ndarray:
+    """[E, N, K/2] row-major -> [E][N/16][K/128][16 rows][64 B] (quant.py:118-122)."""
+    E, N, Kh = w.shape
+    assert N % 16 == 0 and Kh % 64 == 0
+    return np.ascontiguousarray(w.reshape(E, N // 16, 16, Kh // 64, 64).transpose(0, 1, 3, 2, 4).reshape(E, N, Kh))
+
+
+def untile_fp4(w) -> np.ndarray:
+    """inverse of tile_fp4 (quant.py:125-127)."""
+    E, N, Kh = w.shape
+    return np.ascontiguousarray(w.reshape(E, N // 16, Kh // 64, 16, 64).transpose(0, 1, 3, 2, 4).reshape(E, N, Kh))
+
+
+def tile_fp4_scales(s) -> np.ndarray:
+    """[E, N, K/32] -> [E][N/16][K/128][16][4] (quant.py:130-134)."""
+    E, N, Ks = s.shape
+    assert N % 16 == 0 and Ks % 4 == 0
+    return np.ascontiguousarray(s.reshape(E, N // 16, 16, Ks // 4, 4).transpose(0, 1, 3, 2, 4).reshape(E, N, Ks))
+
+
+def untile_fp4_scales(s) -> np.ndarray:
+    """inverse of tile_fp4_scales (quant.py:137-139)."""
+    E, N, Ks = s.shape
+    return np.ascontiguousarray(s.reshape(E, N // 16, Ks // 4, 16, 4).transpose(0, 1, 3, 2, 4).reshape(E, N, Ks))
+
+
+# --------------------------------------------------------------------------- FP8 activations
+def _groups(x, block):
+    x = np.asarray(x, dtype=F32)
+    return x.reshape(-1, block)
+
+
+def quant_fp8_e8m0(x, block: int = 32):
+    """Per-`block` FP8 quantisation (quant.py:57-64) returned as (E4M3 codes uint8 [..., K],
+    E8M0 bytes uint8 [..., K/block]) -- the operand format of the scaled MFMA."""
+    shape = np.shape(x)
+    xg = _groups(x, block)
+    amax = np.maximum(np.abs(xg).max(axis=-1, keepdims=True), F32(1e-4))
+    e = ceil_log2(amax / F32(FP8_MAX))
+    s = np.ldexp(F32(1.0), e).astype(F32)
+    q = round_e4m3(np.clip(xg / s, -FP8_MAX, FP8_MAX))
+    codes = e4m3_encode(q).reshape(shape)
+    scales = (e + 127).astype(np.uint8).reshape(*shape[:-1], shape[-1] // block)
+    return codes, scales
+
+
+def quant_fp8(x, block: int = 32):
+    """(E4M3 values as fp32, fp32 scales [..., K/block]) exactly as quant.quant_fp8 (quant.py:57-64)."""
+    shape = np.shape(x)
+    xg = _groups(x, block)
+    amax = np.maximum(np.abs(xg).max(axis=-1, keepdims=True), F32(1e-4))
+    s = pow2_scale(amax, FP8_MAX)
+    q = round_e4m3(np.clip(xg / s, -FP8_MAX, FP8_MAX))
+    return q.reshape(shape), s.reshape(*shape[:-1], shape[-1] // block)
+
+
+def fake_quant_fp8(x, block: int = 32) -> np.ndarray:
+    """Quantise-dequantise per `block` along the last dim, fp32 result (quant.py:45-54). A bf16 caller
+    casts the result back to bf16, which is exact (4 significant bits times a power of two)."""
+    shape = np.shape(x)
+    q, s = quant_fp8(x, block)
+    return (q.reshape(-1, block) * s.reshape(-1, 1)).astype(F32).reshape(shape)
+
+
+_PERM8 = np.array([0, 4, 2, 6, 1, 5, 3, 7])
+
+
+def permute_x(x) -> np.ndarray:
+    """Within every 8 k: order 0,4,2,6,1,5,3,7 (cukern.py:221-227)."""
+    M, K = x.shape
+    return np.ascontiguousarray(x.reshape(M, K // 8, 8)[:, :, _PERM8].reshape(M, K))
+
+
+def unpermute_x(xp) -> np.ndarray:
+    M, K = xp.shape
+    inv = np.argsort(_PERM8)
+    return np.ascontiguousarray(xp.reshape(M, K // 8, 8)[:, :, inv].reshape(M, K))
+
+
+# --------------------------------------------------------------------------- SwiGLU + quant
+def sigmoid_f32(g) -> np.ndarray:
+    g = np.asarray(g, dtype=F32)
+    with np.errstate(over="ignore"):
+        return (F32(1.0) / (F32(1.0) + np.exp(-g))).astype(F32)
+
+
+def swiglu_quant(gu, weights, inter: int, limit: float, permute: bool = False) -> np.ndarray:
+    """h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) per 32 (fused.py:284-306, 334-345; torch twin
+    model._swiglu model.py:608-613 + quant.fake_quant_fp8, equality test_fused.py:81-88). Returns fp32
+    values of the bf16 output [rows, inter]; permute=True stores the 8-k permuted order (fused.py:303-305)."""
+    gu = np.asarray(gu, dtype=F32)
+    gate, up = gu[:, :inter].copy(), gu[:, inter:2 * inter].copy()
+    if limit > 0:
+        up = np.clip(up, F32(-limit), F32(limit))
+        gate = np.minimum(gate, F32(limit))
+    h = ((gate * sigmoid_f32(gate)).astype(F32) * up).astype(F32)
+    if weights is not None:
+        h = (h * np.asarray(weights, dtype=F32).reshape(-1, 1)).astype(F32)
+    h = bf16_round(h)
+    h = fake_quant_fp8(h, 32)
+    if permute:
+        h = permute_x(h)
+    return h
+
+
+# --------------------------------------------------------------------------- routing
+def gate_topk(scores, bias, temp: float, topk: int, route_scale: float, score_func: str, norm: bool):
+    """MoE gate on precomputed logits (model.py:391-404; fused2.py:419-452): scoring function, + bias for
+    the selection only, top-k with the lowest index winning ties, weights renormalised (+1e-20) and scaled."""
+    s = np.asarray(scores, dtype=F32) / F32(temp)
+    if score_func == "softmax":
+        mx = s.max(axis=-1, keepdims=True)
+        ex = np.exp(s - mx).astype(F32)
+        s = (ex / ex.sum(axis=-1, keepdims=True)).astype(F32)
+    elif score_func == "sigmoid":
+        s = sigmoid_f32(s)
+    else:
+        with np.errstate(over="ignore"):
+            sp = np.where(s > 20.0, s, np.log1p(np.exp(s))).astype(F32)
+        s = np.sqrt(sp).astype(F32)
+    b = (s + (np.zeros(s.shape[-1], F32) if bias is None else np.asarray(bias, F32))).astype(F32)
+    # stable sort of -b: equal values keep ascending index order -> lowest index first
+    idx = np.argsort(-b, axis=-1, kind="stable")[:, :topk].astype(np.int32)
+    w = np.take_along_axis(s, idx, axis=-1).astype(F32)
+    if norm:
+        w = (w / (w.sum(axis=-1, keepdims=True) + F32(1e-20))).astype(F32)
+    w = (w * F32(route_scale)).astype(F32)
+    return idx, w
+
+
+def moe_dispatch(eid, wt, topk: int, n_experts: int, gmax: int):
+    """Expert bucketing (p2p.cu:90-132, cukern.py:323-337) with a deterministic within-expert order
+    (ascending pair index). The reference's order within an expert is arbitrary (atomic cursors,
+    p2p.cu:91-93): tests compare against this through order-free invariants."""
+    eid = np.asarray(eid, dtype=np.int64).reshape(-1)
+    wt = np.asarray(wt, dtype=F32).reshape(-1)
+    n = eid.size
+    order = np.argsort(eid, kind="stable")
+    tok_sorted = (order // topk).astype(np.int32)
+    wt_sorted = wt[order]
+    inv = np.empty(n, np.int32)
+    inv[order] = np.arange(n, dtype=np.int32)
+    counts = np.bincount(eid, minlength=n_experts)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    ge, gs = [], []
+    for e in range(n_experts):
+        for t in range(0, counts[e], gmax):
+            ge.append(e)
+            gs.append(starts[e] + t)
+    G = len(ge)
+    grp_expert = np.full(n, -1, np.int32)
+    grp_start = np.full(n + 1, n, np.int32)
+    grp_expert[:G] = ge
+    grp_start[:G] = gs
+    return tok_sorted, wt_sorted, inv, grp_expert, grp_start, G
+
+
+# --------------------------------------------------------------------------- GEMMs and the layer
+def dense_weights(w, s) -> np.ndarray:
+    """fp32 values of dequant_fp4 (bf16-exact) for [N, K/2] / [N, K/32] (row-major layout)."""
+    return dequant_fp4_values(w, s)
+
+
+def grouped_gemm(x, w, s, grp_expert, grp_start, pair_tok, G: int) -> np.ndarray:
+    """out[p, n] = sum_k x[pair_tok[p], k] * deq(W[grp_expert[g]])[n, k] for the pairs p of group g
+    (cukern.py:238-276 fp4_gemm_tc; test_fp4_tcw.py:55-58), fp32 accumulation (done in fp64 here)."""
+    x = np.asarray(x, dtype=np.float64)
+    n_pairs = int(grp_start[G])
+    N = w.shape[1]
+    out = np.zeros((n_pairs, N), np.float64)
+    cache = {}
+    for g in range(G):
+        e = int(grp_expert[g])
+        if e not in cache:
+            cache[e] = dense_weights(w[e], s[e]).astype(np.float64)
+        a, b = int(grp_start[g]), int(grp_start[g + 1])
+        out[a:b] = x[np.asarray(pair_tok[a:b], dtype=np.int64)] @ cache[e].T
+    return out.astype(F32)
+
+
+def gemv_pairs(x, w, s, row_in, expert, wt) -> np.ndarray:
+    """out[p, n] = wt[p] * x[row_in[p]] . deq(W[expert[p]])[n] (cukern.py:60-77, fp4_gemv.cu:15-66)."""
+    x = np.asarray(x, dtype=np.float64)
+    P = len(row_in)
+    out = np.zeros((P, w.shape[1]), np.float64)
+    for p in range(P):
+        W = dense_weights(w[int(expert[p])], s[int(expert[p])]).astype(np.float64)
+        out[p] = float(wt[p]) * (W @ x[int(row_in[p])])
+    return out.astype(F32)
+
+
+def expert_pair(xq_row, W13, S13, W2, S2, wt: float, inter: int, limit: float):
+    """One (token, expert) pair of the layer (test_cpumoe.py:19-25, fused.py:284-306, decode.py:316-335):
+    gu = xq . deq(W13)^T ; h = swiglu_quant(gu, w) ; y2 = h . deq(W2)^T. fp32 [H]."""
+    gu = (deq64(W13, S13) @ np.asarray(xq_row, np.float64)).astype(F32)
+    h = swiglu_quant(gu.reshape(1, -1), np.array([wt], F32), inter, limit)[0]
+    return (deq64(W2, S2) @ h.astype(np.float64)).astype(F32)
+
+
+def deq64(w, s):
+    return dense_weights(w, s).astype(np.float64)
+
+
+def shared_expert(xq, Ws13, Ws2, inter: int, limit: float) -> np.ndarray:
+    """Shared expert with bf16 weights (model.py:409-412, decode.py:369-371): gu = xq . Ws13^T (fp32),
+    h = swiglu_quant(gu, no weight), ys = bf16(h . Ws2^T). Returns fp32 values of the bf16 ys [M, H]."""
+    Ws13 = bf16_bits_to_f32(Ws13).astype(np.float64)
+    Ws2 = bf16_bits_to_f32(Ws2).astype(np.float64)
+    gu = (np.asarray(xq, np.float64) @ Ws13.T).astype(F32)
+    h = swiglu_quant(gu, None, inter, limit)
+    return bf16_round((h.astype(np.float64) @ Ws2.T).astype(F32))
+
+
+def moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter: int, limit: float) -> np.ndarray:
+    """Routed part of one MoE layer for M tokens (model.py:578-581; decode.py:316-335): fp32 [M, H] =
+    sum over j (fixed order) of the pair outputs, routing weight folded into h before rounding
+    (fused.py:297-302)."""
+    xq = np.asarray(xq, F32)
+    M, k = np.shape(eid)
+    H = W2.shape[1]
+    y = np.zeros((M, H), F32)
+    cache = {}
+    for t in range(M):
+        acc = np.zeros(H, F32)
+        for j in range(k):
+            e = int(eid[t][j])
+            if e not in cache:
+                cache[e] = (deq64(W13[e], S13[e]), deq64(W2[e], S2[e]))
+            A13, A2 = cache[e]
+            gu = (A13 @ xq[t].astype(np.float64)).astype(F32)
+            h = swiglu_quant(gu.reshape(1, -1), np.array([wt[t][j]], F32), inter, limit)[0]
+            acc = (acc + (A2 @ h.astype(np.float64)).astype(F32)).astype(F32)
+        y[t] = acc
+    return y
+
+
+def moe_layer(x_bf16_vals, eid, wt, W13, S13, W2, S2, Ws13, Ws2, inter: int, limit: float) -> np.ndarray:
+    """Whole layer: y = bf16(sum_j y2_j + ys) (model.py:554-591; fused2.py:490-495). Input x is fp32
+    values of a bf16 tensor; it is FP8 fake-quantised first (model.py:565). Returns fp32 values of bf16."""
+    xq = fake_quant_fp8(np.asarray(x_bf16_vals, F32))
+    y = moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter, limit)
+    if Ws13 is not None:
+        y = (y + shared_expert(xq, Ws13, Ws2, inter, limit)).astype(F32)
+    return bf16_round(y)
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def max_abs_over_rms(a, b) -> float:
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    rms = float(np.sqrt(np.mean(b * b)))
+    return float(np.abs(a - b).max() / max(rms, 1e-30))
