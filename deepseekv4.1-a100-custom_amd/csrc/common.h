@@ -1,0 +1,116 @@
+// Shared device helpers of the MI355X (gfx950) FP4 MoE expert path.
+//
+// Formats (the reference's quant.py:6-110):
+//   E2M1 weights, two per byte along k, low nibble = even k; one E8M0 byte per (row, 32 k), value 2^(b-127).
+//   FP8 activations: E4M3 (float8_e4m3fn) codes with one E8M0 byte per 32 k (power-of-two scale).
+// Every rounding helper here is integer/bit based so results do not depend on the FP mode (denormal flush).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dsv41_amd.h"  // the C ABI: definitions below must match these declarations
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+#define DSV41_EINVAL (-1)
+
+#define WAVE 64
+
+// ------------------------------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; every NaN becomes 0xFFFF (torch's vectorised CPU conversion)
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0xFFFFu;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+
+// ------------------------------------------------------------------------------------------ E2M1 x E8M0
+// Exact fp32 bit pattern of E2M1 code c times 2^(b-127), as quant.dequant_fp4 computes it in fp32
+// (quant.py:106-110): byte 0 is the subnormal 2^-127, 255 is +inf (so 0 x inf = NaN). Built from integers:
+// |value| = M * 2^(b-128) with M = 2|v| in {0,1,2,3,4,6,8,12}.
+__device__ __forceinline__ uint32_t e2m1_e8m0_f32_bits(uint32_t c, uint32_t b) {
+    const uint32_t sign = (c & 8u) << 28;
+    const uint32_t mag = c & 7u;
+    const uint32_t M = (mag < 2u) ? mag : ((2u | (mag & 1u)) << ((mag >> 1) - 1u));
+    if (b == 255u) return M ? (sign | 0x7F800000u) : 0xFFC00000u;
+    if (M == 0u) return sign;
+    const uint32_t h = 31u - __builtin_clz(M);            // 0..3
+    const int biased = (int)h + (int)b - 1;                // biased fp32 exponent of M * 2^(b-128)
+    if (biased >= 255) return sign | 0x7F800000u;
+    if (biased >= 1) return sign | ((uint32_t)biased << 23) | ((M << (23u - h)) & 0x7FFFFFu);
+    return sign | (M << (b + 21u));                        // subnormal: M * 2^(b-128) / 2^-149
+}
+
+// E8M0 byte -> fp32 2^(b-127) bit pattern (quant.py:27-31): 0 -> 2^-127 (subnormal), 255 -> +inf
+__device__ __forceinline__ float e8m0_to_f32(uint32_t b) { return __uint_as_float(b ? (b << 23) : 0x00400000u); }
+
+// ------------------------------------------------------------------------------------------ E4M3 (fp8)
+// Round |v| <= 448 to the float8_e4m3fn grid, ties to even, sign kept (-0.0 stays -0.0 as in torch's cast,
+// quant.py:53; the explicit formula is fused.py:24-34). The ulp is a power of two, so v * 2^(3-e) is exact.
+__device__ __forceinline__ float round_e4m3(float v) {
+    const float a = fabsf(v);
+    int e = (int)((__float_as_uint(a) >> 23) & 0xFFu) - 127;
+    e = e < -6 ? -6 : e;
+    const float inv_ulp = __uint_as_float((uint32_t)(127 + 3 - e) << 23);
+    const float ulp = __uint_as_float((uint32_t)(127 - 3 + e) << 23);
+    float r = rintf(a * inv_ulp) * ulp;
+    r = fminf(r, 448.0f);
+    return __uint_as_float(__float_as_uint(r) | (__float_as_uint(v) & 0x80000000u));
+}
+
+// float8_e4m3fn bits of a value already on the E4M3 grid
+__device__ __forceinline__ uint32_t e4m3_encode(float q) {
+    const uint32_t u = __float_as_uint(q);
+    const uint32_t s = (u >> 24) & 0x80u;
+    const float a = __uint_as_float(u & 0x7FFFFFFFu);
+    uint32_t code;
+    if (a >= 0.015625f) code = ((((u >> 23) & 0xFFu) - 120u) << 3) | ((u >> 20) & 7u);
+    else code = (uint32_t)(a * 512.0f);                  // subnormal grid: multiples of 2^-9 (exact)
+    return s | code;
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+    const uint32_t e = (c >> 3) & 15u, m = c & 7u;
+    const float mag = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0.001953125f;
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// Per-32 FP8 block quantisation (quant.py:45-64; fused.py:47-69 MODE 0): given the group's amax, the
+// power-of-two exponent e (scale 2^e, E8M0 byte e + 127). amax is clamped to >= 1e-4 and divided by 448
+// with an IEEE division, then ceil(log2) exactly from the bits (fused.py:10-16).
+__device__ __forceinline__ int fq8_exponent(float amax) {
+    const float r = fmaxf(amax, 1e-4f) / 448.0f;
+    const uint32_t u = __float_as_uint(r);
+    return (int)((u >> 23) & 0xFFu) - 127 + ((u & 0x7FFFFFu) != 0u ? 1 : 0);
+}
+
+// code of v at scale 2^e: RNE_e4m3(clamp(v / 2^e, +-448)); the division by a power of two is exact
+__device__ __forceinline__ uint32_t fq8_code(float v, int e) {
+    const float x = v * __uint_as_float((uint32_t)(127 - e) << 23);
+    return e4m3_encode(round_e4m3(fminf(fmaxf(x, -448.0f), 448.0f)));
+}
+
+__device__ __forceinline__ float fq8_value(uint32_t code, int e) {
+    return e4m3_decode(code) * __uint_as_float((uint32_t)(127 + e) << 23);
+}
+
+// ------------------------------------------------------------------------------------------ waves
+__device__ __forceinline__ float wave_max32(float v) {  // max over each 32-lane half of the wave
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 32));
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------ MFMA
+// D(16x16, fp32) += A(16x128) * B(128x16) with per-32 E8M0 block scales (gfx950 block-scaled MFMA).
+// A = E2M1 weights (format 4): lane l holds 32 k of row l%16 (16 bytes in the low 4 dwords), k-block l/16.
+// B = E4M3 activations (format 0): lane l holds 32 k of column l%16 (32 bytes), k-block l/16.
+// sa / sb: the lane's E8M0 byte (byte 0 of the register). Output: lane l holds D[4*(l/16)+i][l%16].
+__device__ __forceinline__ v4f mfma_fp4w_fp8x(v8i a, v8i b, v4f c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
+}

@@ -1,0 +1,122 @@
+// Format kernels: E2M1 x E8M0 dequantisation (bit-exact with quant.dequant_fp4), per-32 FP8 block
+// quantisation of activations (quant.quant_fp8 / fake_quant_fp8), and the SwiGLU epilogue that turns the
+// fp32 gate/up GEMV output into FP8 codes for the down projection (fused.swiglu_quant).
+// All are HBM-bound element-wise kernels: coalesced loads, one 32-lane half-wave per 32-element FP8 group.
+#include "common.h"
+
+// ------------------------------------------------------------------------------------------ dequant
+// out[n, k] (bf16 bits) = E2M1(code of k in row n) * 2^(S[n, k/32] - 127) rounded to bf16 (quant.py:106-110).
+// tiled: weights/scales in the quant.tile_fp4 / tile_fp4_scales layout (quant.py:118-134); rows % 16 == 0.
+__global__ void __launch_bounds__(256) dequant_fp4_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ s,
+                                                          long long rows, int K, int tiled, uint32_t* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // packed byte index in row-major order
+    const int Kh = K >> 1;
+    if (i >= rows * Kh) return;
+    const long long n = i / Kh;
+    const int j = (int)(i - n * Kh);
+    const int ks = (2 * j) >> 5;
+    long long wi, si;
+    if (tiled) {
+        const long long tile = (n >> 4) * (K >> 7) + (j >> 6);
+        wi = tile * 1024 + (n & 15) * 64 + (j & 63);
+        si = ((n >> 4) * (K >> 7) + (ks >> 2)) * 64 + (n & 15) * 4 + (ks & 3);
+    } else {
+        wi = i;
+        si = n * (K >> 5) + ks;
+    }
+    const uint32_t byte = w[wi], sb = s[si];
+    const uint32_t lo = f32_to_bf16_bits(__uint_as_float(e2m1_e8m0_f32_bits(byte & 15u, sb)));
+    const uint32_t hi = f32_to_bf16_bits(__uint_as_float(e2m1_e8m0_f32_bits(byte >> 4, sb)));
+    out[i] = lo | (hi << 16);
+}
+
+// ------------------------------------------------------------------------------------------ FP8 quant
+// One 32-lane half-wave per 32-element group of a row. Input bf16 or fp32 with row stride ldx (elements);
+// `permuted`: the row is in the 8-k permuted order of cukern.permute_x (within 8 k: 0,4,2,6,1,5,3,7, a
+// bit reversal of k%8), codes/scales are written in natural k order. fq (optional) gets the fake-quantised
+// values in the input's dtype and order (fused.fake_quant_fp8, fused.py:82-83).
+__global__ void __launch_bounds__(256) quant_fp8_kernel(const void* __restrict__ x, int x_f32, long long rows, int K, long long ldx,
+                                                        int permuted, uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
+                                                        void* __restrict__ fq) {
+    const long long gidx = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 5;  // group index
+    const int lane = threadIdx.x & 31;
+    const int gpr = K >> 5;
+    if (gidx >= rows * gpr) return;
+    const long long r = gidx / gpr;
+    const int gk = (int)(gidx - r * gpr) * 32 + lane;  // position in the input row
+    float v;
+    if (x_f32) v = ((const float*)x)[r * ldx + gk];
+    else v = bf16_to_f32(((const uint16_t*)x)[r * ldx + gk]);
+    const float amax = wave_max32(fabsf(v));
+    const int e = fq8_exponent(amax);
+    const uint32_t code = fq8_code(v, e);
+    const int nat = permuted ? ((gk & ~7) | ((gk & 1) << 2) | (gk & 2) | ((gk >> 2) & 1)) : gk;
+    if (codes) codes[r * K + nat] = (uint8_t)code;
+    if (scales && lane == 0) scales[r * gpr + (gk >> 5)] = (uint8_t)(e + 127);
+    if (fq) {
+        const float q = fq8_value(code, e);
+        if (x_f32) ((float*)fq)[r * K + gk] = q;
+        else ((uint16_t*)fq)[r * K + gk] = (uint16_t)f32_to_bf16_bits(q);
+    }
+}
+
+// ------------------------------------------------------------------------------------------ SwiGLU
+// h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) per 32 columns (fused.py:284-306; model.py:608-613).
+// gu: fp32 [rows, ld_gu] with gate in columns [0, I) and up in [I, 2I). Outputs: FP8 codes [rows, I] and E8M0
+// [rows, I/32] (the down-projection operand), and optionally the bf16 values (fused.swiglu_quant's result,
+// 8-k permuted when `permute`, fused.py:303-305).
+__global__ void __launch_bounds__(256) swiglu_quant_kernel(const float* __restrict__ gu, long long ld_gu, const float* __restrict__ wt,
+                                                           int rows, int inter, float limit, uint8_t* __restrict__ codes,
+                                                           uint8_t* __restrict__ scales, uint16_t* __restrict__ hb, int permute) {
+    const long long gidx = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+    const int lane = threadIdx.x & 31;
+    const int gpr = inter >> 5;
+    if (gidx >= (long long)rows * gpr) return;
+    const int r = (int)(gidx / gpr);
+    const int c = (int)(gidx - (long long)r * gpr) * 32 + lane;
+    float g = gu[(long long)r * ld_gu + c];
+    float u = gu[(long long)r * ld_gu + inter + c];
+    if (limit > 0.f) {
+        u = fminf(fmaxf(u, -limit), limit);
+        g = fminf(g, limit);
+    }
+    float h = g * (1.0f / (1.0f + expf(-g))) * u;
+    if (wt) h = h * wt[r];
+    h = bf16_round(h);
+    const float amax = wave_max32(fabsf(h));
+    const int e = fq8_exponent(amax);
+    const uint32_t code = fq8_code(h, e);
+    if (codes) codes[(long long)r * inter + c] = (uint8_t)code;
+    if (scales && lane == 0) scales[(long long)r * gpr + (c >> 5)] = (uint8_t)(e + 127);
+    if (hb) {
+        const int cc = permute ? ((c & ~7) | ((c & 1) << 2) | (c & 2) | ((c >> 2) & 1)) : c;
+        hb[(long long)r * inter + cc] = (uint16_t)f32_to_bf16_bits(fq8_value(code, e));
+    }
+}
+
+// ------------------------------------------------------------------------------------------ C ABI
+extern "C" int dsv41_dequant_fp4(const uint8_t* w, const uint8_t* s, long long rows, int K, int tiled, uint16_t* out, void* stream) {
+    if (!w || !s || !out || rows < 0 || K <= 0 || (K & 31) || (tiled && ((rows & 15) || (K & 127)))) return DSV41_EINVAL;
+    const long long n = rows * (K / 2);
+    if (n == 0) return 0;
+    dequant_fp4_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(w, s, rows, K, tiled, (uint32_t*)out);
+    return (int)hipGetLastError();
+}
+
+extern "C" int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, long long ldx, int permuted,
+                               uint8_t* codes, uint8_t* scales, void* fq, void* stream) {
+    if (!x || rows < 0 || K <= 0 || (K & 31) || ldx < K || (!codes && !scales && !fq)) return DSV41_EINVAL;
+    const long long groups = rows * (K / 32);
+    if (groups == 0) return 0;
+    quant_fp8_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(x, x_f32, rows, K, ldx, permuted, codes, scales, fq);
+    return (int)hipGetLastError();
+}
+
+extern "C" int dsv41_swiglu_quant(const float* gu, long long ld_gu, const float* wt, int rows, int inter, float limit,
+                                  uint8_t* codes, uint8_t* scales, uint16_t* h_bf16, int permute, void* stream) {
+    if (!gu || rows < 0 || inter <= 0 || (inter & 31) || ld_gu < 2LL * inter || (!codes && !scales && !h_bf16)) return DSV41_EINVAL;
+    const long long groups = (long long)rows * (inter / 32);
+    if (groups == 0) return 0;
+    swiglu_quant_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(gu, ld_gu, wt, rows, inter, limit, codes, scales, h_bf16, permute);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,119 @@
+"""FP4 expert kernels with the call surface of the reference's cukern.py (fp4_gemv_pairs, fp4_gemm_tc,
+permute_x, moe_dispatch), on the HIP library instead of libcuda-launched cubins.
+
+Activations arrive as bf16 tensors already on the FP8 grid (fake_quant_fp8 / swiglu_quant outputs, exactly what
+the reference passes). The wrappers convert them to the MFMA operand format (E4M3 codes + E8M0 bytes per 32);
+for FP8-grid input that conversion is exact, so the products equal the reference's bf16 products.
+Outputs are allocated with torch.empty on the input's device (cukern.py:67, 251, 328-332); kernels never
+allocate. All launches go to torch's current stream and can be captured in a hipGraph.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _lib
+from .quant import quant_fp8_e8m0
+
+FP4_TILED = os.environ.get("DSV41_FP4_TILED", "1") == "1"  # experts stored in the tile_fp4 layout (cukern.py:231)
+FP4_W_MAX = 64                                              # tokens per group of the dispatch (cukern.py:232)
+
+_PERM8 = [0, 4, 2, 6, 1, 5, 3, 7]
+
+
+def permute_x(x: torch.Tensor) -> torch.Tensor:
+    """bf16 [M, K] -> the 8-k permuted layout fp4_gemm_tc accepts (within every 8 k: 0,4,2,6,1,5,3,7),
+    cukern.py:224-227. A layout view, kept for drop-in compatibility (the HIP kernels take natural order)."""
+    M, K = x.shape
+    return x.view(M, K // 8, 8)[:, :, _PERM8].reshape(M, K).contiguous()
+
+
+def _quant_x(x: torch.Tensor, permuted: bool):
+    codes, scales = quant_fp8_e8m0(x, permuted=permuted)
+    return codes, scales
+
+
+def grouped_gemm_codes(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: torch.Tensor,
+                       grp_start: torch.Tensor, pair_tok: torch.Tensor, out: torch.Tensor, max_tokens: int, tiled: bool,
+                       pair_wt: torch.Tensor | None = None, out_row: torch.Tensor | None = None, accum: int = 0,
+                       shard_start: int = 0, shard_n: int = 1 << 30, zero_out: bool = False, n_cols: int | None = None,
+                       min_tok: int = 0, max_tok: int = 1 << 30) -> torch.Tensor:
+    """Core launcher: out[out_row[p], :N] (=, +=, atomic +=) wt[p] * codes(x)[pair_tok[p]] . deq(W[e_g])^T.
+    xc/xs: FP8 codes [rows, K] / E8M0 [rows, K/32]; w/s: [E, N, K/2] / [E, N, K/32] (may be a column slice)."""
+    dev = _lib.require_cuda(xc, xs, w, s, grp_expert, grp_start, pair_tok, out)
+    E, N, Kh = w.shape
+    K = Kh * 2
+    if n_cols is not None:
+        N = n_cols
+    assert w.stride(2) == 1 and w.stride(1) == Kh and s.stride(2) == 1 and s.stride(1) == K // 32, "weights must be row-contiguous"
+    assert xc.dtype == torch.uint8 and xs.dtype == torch.uint8 and xc.shape[-1] == K and xs.shape[-1] == K // 32
+    assert out.dtype == torch.float32 and out.stride(-1) == 1
+    for t in (grp_expert, grp_start, pair_tok):
+        assert t.dtype == torch.int32 and t.is_contiguous()
+    G = grp_expert.numel()
+    _lib.call("dsv41_fp4_grouped_gemm", _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 1 if tiled else 0, N, K,
+              _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(grp_expert), _lib.ptr(grp_start), G, _lib.ptr(pair_tok),
+              _lib.ptr(out), out.stride(0), _lib.ptr(out_row), _lib.ptr(pair_wt), accum, max(1, int(max_tokens)),
+              shard_start, min(shard_n, E), 1 if zero_out else 0, min_tok, max_tok, _lib.stream(dev))
+    return out
+
+
+def fp4_gemv_pairs(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, row_in: torch.Tensor, expert: torch.Tensor,
+                   wt: torch.Tensor, n_pairs: int, tiled: bool = False) -> torch.Tensor:
+    """x: bf16 [rows_in, K]; w: uint8 [E, N, K/2]; s: uint8 [E, N, K/32]; row_in/expert: int32 [pairs];
+    wt: fp32 [pairs]. Returns fp32 [pairs, N] = wt * x[row_in] @ W[expert]^T, one output row per pair, no atomics
+    (cukern.py:60-77). The reference kernel reads the row-major layout; `tiled` selects tile_fp4 instead."""
+    dev = _lib.require_cuda(x, w, s, row_in, expert, wt)
+    assert x.dtype == torch.bfloat16 and x.stride(1) == 1
+    E, N, Kh = w.shape
+    out = torch.empty(n_pairs, N, device=dev, dtype=torch.float32)
+    if n_pairs == 0:
+        return out
+    xc, xs = _quant_x(x, False)
+    starts = torch.arange(n_pairs + 1, device=dev, dtype=torch.int32)
+    grouped_gemm_codes(xc, xs, w, s, expert.to(torch.int32).contiguous(), starts, row_in.to(torch.int32).contiguous(), out, 1, tiled,
+                       pair_wt=wt.to(torch.float32).contiguous())
+    return out
+
+
+def fp4_gemm_tc(xp: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: torch.Tensor, grp_start: torch.Tensor,
+                pair_tok: torch.Tensor, n_pairs: int, max_tokens: int, shard_start: int = 0, shard_n: int = 1 << 30,
+                zero_out: bool = False, out: torch.Tensor | None = None, out_col: int = 0) -> torch.Tensor:
+    """xp: permuted bf16 [rows, K] (permute_x); w: uint8 [E, N, K/2]; s: uint8 [E, N, K/32]; groups g: expert
+    grp_expert[g] with pairs grp_start[g]..grp_start[g+1]-1, pair p uses x row pair_tok[p]. Returns fp32
+    [n_pairs, N] (cukern.py:238-276). Groups of other shards are skipped (zero_out: rows zeroed); `out`/`out_col`
+    write into columns [out_col, out_col + N) of a wider buffer. Any group size is accepted (passes of 64)."""
+    dev = _lib.require_cuda(xp, w, s)
+    E, N, Kh = w.shape
+    K = Kh * 2
+    assert xp.dtype == torch.bfloat16 and xp.is_contiguous() and K % 128 == 0 and N % 16 == 0
+    if out is None:
+        out = torch.empty(n_pairs, N, device=dev, dtype=torch.float32)
+    assert out.shape[1] >= out_col + N
+    xc, xs = _quant_x(xp, True)
+    target = out[:, out_col:] if out_col else out
+    grouped_gemm_codes(xc, xs, w, s, grp_expert.to(torch.int32).contiguous(), grp_start.to(torch.int32).contiguous(),
+                       pair_tok.to(torch.int32).contiguous(), target, max_tokens, FP4_TILED, shard_start=shard_start,
+                       shard_n=shard_n, zero_out=zero_out, n_cols=N)
+    return out
+
+
+def moe_dispatch(eid: torch.Tensor, wt: torch.Tensor, topk: int, n_experts: int, gmax: int, device: torch.device,
+                 n_groups: torch.Tensor | None = None):
+    """One-launch expert bucketing (cukern.py:323-337): eid int32 [n], wt fp32 [n] ->
+    (tok_sorted int32 [n], wt_sorted fp32 [n], inv int32 [n], grp_expert int32 [n], grp_start int32 [n+1]).
+    Within an expert pairs keep ascending pair order (the reference's order is arbitrary)."""
+    n = eid.numel()
+    assert n_experts <= 512
+    eid = eid.reshape(-1).to(torch.int32).contiguous()
+    wt = wt.reshape(-1).to(torch.float32).contiguous()
+    _lib.require_cuda(eid, wt)
+    tok_sorted = torch.empty(n, dtype=torch.int32, device=device)
+    wt_sorted = torch.empty(n, dtype=torch.float32, device=device)
+    inv = torch.empty(n, dtype=torch.int32, device=device)
+    grp_expert = torch.empty(n, dtype=torch.int32, device=device)
+    grp_start = torch.empty(n + 1, dtype=torch.int32, device=device)
+    _lib.call("dsv41_moe_dispatch", _lib.ptr(eid), _lib.ptr(wt), n, topk, n_experts, gmax, _lib.ptr(tok_sorted), _lib.ptr(wt_sorted),
+              _lib.ptr(inv), _lib.ptr(grp_expert), _lib.ptr(grp_start), _lib.ptr(n_groups), _lib.stream(device))
+    return tok_sorted, wt_sorted, inv, grp_expert, grp_start

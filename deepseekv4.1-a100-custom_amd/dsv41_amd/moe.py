@@ -1,0 +1,229 @@
+"""The FP4 MoE expert path of one layer on MI355X: routed experts (decode, M <= 16 tokens), the bf16 shared
+expert, routing and the combine, as HIP kernels launched on torch's current stream.
+
+Decode (decode.py:316-372 experts_tc / moe2; model.py:554-591 MoE.__call__ for <= 16 tokens):
+  1. xq (bf16, FP8 grid) -> E4M3 codes + E8M0 per 32 (exact)                       quant_fp8 kernel
+  2. pairs bucketed by expert on the device (M > 1; M = 1 uses constant tables,
+     decode.py:304-314)                                                             moe_dispatch kernel
+  3. gu[p] = x[tok(p)] . deq(W13[e(p)])^T, each selected expert read once          grouped MFMA kernel
+  4. h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) as FP8 codes          swiglu_quant kernel
+     (routing weight folded in before rounding, fused.py:297-302)
+  5. y[t] = sum over t's experts of h . deq(W2)^T in one MFMA accumulator,
+     out = bf16(y + ys) (fused2.py:490-495)                                         moe_down_sum kernel
+Only the selected experts' weight bytes are read from HBM.
+
+Workspaces are allocated once per (device, shape) and reused, so a captured graph replays without allocating.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .fused import swiglu_quant_codes
+from .hipkern import grouped_gemm_codes, moe_dispatch
+from .quant import quant_fp8_e8m0
+
+
+@dataclass
+class ExpertWeights:
+    """One layer's routed experts in the checkpoint format (load.py:128-148): w13 uint8 [E, 2I, H/2] (w1 rows then
+    w3 rows), s13 uint8 [E, 2I, H/32], w2 uint8 [E, H, I/2], s2 uint8 [E, H, I/32]; `tiled`: tile_fp4 layout."""
+    w13: torch.Tensor
+    s13: torch.Tensor
+    w2: torch.Tensor
+    s2: torch.Tensor
+    tiled: bool = True
+
+    @property
+    def E(self) -> int:
+        return self.w13.shape[0]
+
+    @property
+    def H(self) -> int:
+        return self.w2.shape[1]
+
+    @property
+    def I(self) -> int:
+        return self.w2.shape[2] * 2
+
+    def check(self):
+        E, H, I = self.E, self.H, self.I
+        assert self.w13.shape == (E, 2 * I, H // 2) and self.s13.shape == (E, 2 * I, H // 32)
+        assert self.w2.shape == (E, H, I // 2) and self.s2.shape == (E, H, I // 32)
+        for t in (self.w13, self.s13, self.w2, self.s2):
+            assert t.dtype == torch.uint8 and t.is_contiguous() and t.is_cuda
+        assert H % 128 == 0 and I % 128 == 0 and (2 * I) % 16 == 0 and H % 16 == 0
+
+    def expert_bytes(self) -> int:
+        """Packed bytes of one expert (weights + scales of w13 and w2)."""
+        per = lambda t: t[0].numel() * t.element_size()
+        return per(self.w13) + per(self.s13) + per(self.w2) + per(self.s2)
+
+
+class _Workspace:
+    def __init__(self, dev, M, k, H, I):
+        P = M * k
+        u8, i32, f32 = torch.uint8, torch.int32, torch.float32
+        self.M, self.k, self.P = M, k, P
+        self.xc = torch.empty(M, H, dtype=u8, device=dev)
+        self.xs = torch.empty(M, H // 32, dtype=u8, device=dev)
+        self.gu = torch.empty(P, 2 * I, dtype=f32, device=dev)
+        self.hc = torch.empty(P, I, dtype=u8, device=dev)
+        self.hs = torch.empty(P, I // 32, dtype=u8, device=dev)
+        self.y = torch.empty(M, H, dtype=f32, device=dev)
+        self.tok_sorted = torch.empty(P, dtype=i32, device=dev)
+        self.wt_sorted = torch.empty(P, dtype=f32, device=dev)
+        self.inv = torch.empty(P, dtype=i32, device=dev)
+        self.grp_expert = torch.empty(P, dtype=i32, device=dev)
+        self.grp_start = torch.empty(P + 1, dtype=i32, device=dev)
+        self.n_groups = torch.empty(1, dtype=i32, device=dev)
+        # M = 1: one group per pair, in pair order (decode.py:304-314)
+        self.const_start = torch.arange(P + 1, dtype=i32, device=dev)
+        self.const_tok = torch.zeros(P, dtype=i32, device=dev)
+
+
+_WS: dict = {}
+
+
+def _workspace(dev, M, k, H, I) -> _Workspace:
+    key = (dev, M, k, H, I)
+    ws = _WS.get(key)
+    if ws is None:
+        ws = _WS[key] = _Workspace(dev, M, k, H, I)
+    return ws
+
+
+def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
+                ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed experts of one layer for M <= 16 tokens.
+    xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int32 [M, k]; wt fp32 [M, k].
+    Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
+    or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None)."""
+    dev = _lib.require_cuda(xq, eid, wt)
+    M, H = xq.shape
+    k = eid.shape[-1]
+    assert 1 <= M <= 16, "decode path: at most 16 tokens (use the prefill path beyond)"
+    assert H == ex.H and xq.dtype == torch.bfloat16
+    ws = _workspace(dev, M, k, H, ex.I)
+    quant_fp8_e8m0(xq, codes=ws.xc, scales=ws.xs)
+    eid32 = eid.reshape(-1)
+    wt32 = wt.reshape(-1)
+    if eid32.dtype != torch.int32:
+        eid32 = eid32.to(torch.int32)
+    if wt32.dtype != torch.float32:
+        wt32 = wt32.float()
+    eid32 = eid32.contiguous()
+    wt32 = wt32.contiguous()
+    if M == 1:
+        grp_expert, grp_start, tok, wts = eid32, ws.const_start, ws.const_tok, wt32
+    else:
+        _lib.call("dsv41_moe_dispatch", _lib.ptr(eid32), _lib.ptr(wt32), ws.P, k, ex.E, 64, _lib.ptr(ws.tok_sorted), _lib.ptr(ws.wt_sorted),
+                  _lib.ptr(ws.inv), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.n_groups), _lib.stream(dev))
+        grp_expert, grp_start, tok, wts = ws.grp_expert, ws.grp_start, ws.tok_sorted, ws.wt_sorted
+    grouped_gemm_codes(ws.xc, ws.xs, ex.w13, ex.s13, grp_expert, grp_start, tok, ws.gu, M, ex.tiled)
+    swiglu_quant_codes(ws.gu, wts, ex.I, limit, codes=ws.hc, scales=ws.hs)
+    y = ws.y if y32 is None else y32
+    want_y = out is None or y32 is not None
+    _lib.call("dsv41_moe_down_sum", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H, ex.I,
+              _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), _lib.ptr(grp_expert), _lib.ptr(grp_start), _lib.ptr(tok),
+              ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
+              _lib.ptr(out), H if out is None else out.stride(0), 0, 1 << 30, _lib.stream(dev))
+    return out if out is not None else y
+
+
+# --------------------------------------------------------------------------- dense bf16 (shared expert, router)
+def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, out_bf16: bool = False) -> torch.Tensor:
+    """out[t, n] = sum_k x[t, k] W[n, k] for M <= 16 rows of bf16 x and bf16 W [N, K] (fp32 accumulation);
+    fp32 output, or bf16 (round to nearest even) when out_bf16."""
+    dev = _lib.require_cuda(W, x)
+    M, K = x.shape
+    N = W.shape[0]
+    assert W.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and W.shape[1] == K and W.stride(1) == 1 and x.stride(1) == 1
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=dev)
+    is_b = out.dtype == torch.bfloat16
+    _lib.call("dsv41_dense_gemv_bf16", _lib.ptr(W), W.stride(0), N, K, _lib.ptr(x), x.stride(0), M,
+              None if is_b else _lib.ptr(out), out.stride(0), _lib.ptr(out) if is_b else None, out.stride(0), _lib.stream(dev))
+    return out
+
+
+class _SharedWs:
+    def __init__(self, dev, M, H, I):
+        self.gu = torch.empty(M, 2 * I, dtype=torch.float32, device=dev)
+        self.h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
+        self.ys = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+
+
+_SWS: dict = {}
+
+
+def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit: float, ys: torch.Tensor | None = None) -> torch.Tensor:
+    """Shared expert with bf16 weights (model.py:409-412, decode.py:369-371): gu = xq . Ws13^T (fp32),
+    h = swiglu_quant(gu, no weight) (bf16 on the FP8 grid), ys = bf16(h . Ws2^T). Ws13 = [w1; w3] bf16 [2I, H]."""
+    dev = _lib.require_cuda(xq, Ws13, Ws2)
+    M, H = xq.shape
+    I = Ws2.shape[1]
+    key = (dev, M, H, I)
+    sw = _SWS.get(key)
+    if sw is None:
+        sw = _SWS[key] = _SharedWs(dev, M, H, I)
+    dense_gemv(Ws13, xq, out=sw.gu)
+    _lib.call("dsv41_swiglu_quant", _lib.ptr(sw.gu), sw.gu.stride(0), None, M, I, float(limit), None, None, _lib.ptr(sw.h), 0, _lib.stream(dev))
+    out = sw.ys if ys is None else ys
+    dense_gemv(Ws2, sw.h, out=out)
+    return out
+
+
+class MoEDecodeLayer:
+    """One MoE layer at decode (M <= 16 tokens): router logits (given, or x . G^T with bf16 router weights G),
+    gate_topk, the shared expert and the routed FP4 experts, combined as y = bf16(sum_j y2_j + ys)
+    (model.py:554-591; decode.py:354-372; fused2.py:474-508)."""
+
+    def __init__(self, experts: ExpertWeights, Ws13: torch.Tensor | None, Ws2: torch.Tensor | None, limit: float,
+                 topk: int = 8, score_func: str = "softmax", route_scale: float = 1.0, norm: bool = True,
+                 router: torch.Tensor | None = None, bias: torch.Tensor | None = None, temp: float = 1.0):
+        experts.check()
+        self.ex, self.Ws13, self.Ws2, self.limit = experts, Ws13, Ws2, float(limit)
+        self.topk, self.score_func, self.route_scale, self.norm = topk, score_func, route_scale, norm
+        self.router, self.bias, self.temp = router, bias, temp
+        self._bufs: dict = {}
+
+    def _buf(self, dev, M):
+        b = self._bufs.get(M)
+        if b is None:
+            E, H = self.ex.E, self.ex.H
+            b = self._bufs[M] = {
+                "xq": torch.empty(M, H, dtype=torch.bfloat16, device=dev),
+                "logits": torch.empty(M, E, dtype=torch.float32, device=dev),
+                "eid": torch.empty(M, self.topk, dtype=torch.int32, device=dev),
+                "wt": torch.empty(M, self.topk, dtype=torch.float32, device=dev),
+                "ys": torch.empty(M, H, dtype=torch.bfloat16, device=dev),
+                "out": torch.empty(M, H, dtype=torch.bfloat16, device=dev),
+            }
+        return b
+
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        from .fused2 import gate_topk
+        dev = _lib.require_cuda(x)
+        M, H = x.shape
+        b = self._buf(dev, M)
+        # xq = fake_quant_fp8(x) (model.py:565): one pass writes the bf16 values; the routed path re-derives the
+        # codes from them exactly
+        _lib.call("dsv41_quant_fp8", _lib.ptr(x), 0, M, H, x.stride(0), 0, None, None, _lib.ptr(b["xq"]), _lib.stream(dev))
+        if logits is None:
+            assert self.router is not None, "router weights or logits are required"
+            logits = dense_gemv(self.router, x, out=b["logits"])
+        gate_topk(logits, self.bias, self.temp, self.topk, self.route_scale, self.score_func, self.norm and self.topk > 1,
+                  eid=b["eid"], wt=b["wt"])
+        ys = None
+        if self.Ws13 is not None:
+            ys = shared_expert(b["xq"], self.Ws13, self.Ws2, self.limit, ys=b["ys"])
+        o = b["out"] if out is None else out
+        moe_experts(b["xq"], b["eid"], b["wt"], self.ex, self.limit, ys=ys, out=o)
+        return o
+
+    @property
+    def last_routing(self):
+        return {M: (v["eid"], v["wt"]) for M, v in self._bufs.items()}

@@ -1,0 +1,93 @@
+/* C ABI of libdsv41_amd.so: the MI355X (gfx950) FP4 MoE expert path.
+ *
+ * Every entry point takes raw device pointers, sizes, and the HIP stream to launch on (hipStream_t passed as
+ * void*), launches its kernels on that stream and returns immediately (stream-ordered, capturable in a
+ * hipGraph). Return value: 0 ok, -1 invalid arguments (nothing launched), > 0 the hipError_t of the launch.
+ * No entry point allocates device memory; callers own every buffer.
+ *
+ * Formats (reference dsv41/quant.py:6-110):
+ *   FP4 weights  uint8 [E][N][K/2], E2M1 nibbles, low nibble = even k; scales uint8 [E][N][K/32] E8M0 (2^(b-127)).
+ *   tiled = 1: weights/scales in the reference's tile_fp4 / tile_fp4_scales layout (quant.py:113-139):
+ *                [E][N/16][K/128][16 rows][64 B] and [E][N/16][K/128][16][4]; tiled = 0: row-major as above.
+ *   FP8 activations: E4M3 (float8_e4m3fn) codes uint8 [rows][K] + E8M0 bytes uint8 [rows][K/32].
+ *   bf16 tensors are passed as uint16_t bit patterns.
+ */
+#ifndef DSV41_AMD_H
+#define DSV41_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 [rows][K] = E2M1 x 2^(S-127), bit-exact with quant.dequant_fp4 (quant.py:98-110). */
+int dsv41_dequant_fp4(const uint8_t* w, const uint8_t* s, long long rows, int K, int tiled, uint16_t* out, void* stream);
+
+/* Per-32 FP8 quantisation of bf16 (x_f32 = 0) or fp32 rows: E4M3 codes + E8M0 scales in natural k order, and/or
+ * the fake-quantised values in the input dtype (fq). Replaces quant.fake_quant_fp8 / quant.quant_fp8
+ * (quant.py:45-64) and fused.fake_quant_fp8 (fused.py:82-83). permuted = 1: x is in cukern.permute_x order
+ * (cukern.py:221-227). Any of codes / scales / fq may be NULL (not all). */
+int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, long long ldx, int permuted,
+                    uint8_t* codes, uint8_t* scales, void* fq, void* stream);
+
+/* h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) per 32 (fused.swiglu_quant, fused.py:283-345).
+ * gu: fp32 [rows][ld_gu], gate columns [0, inter), up [inter, 2 inter). wt: fp32 [rows] or NULL. Outputs (any
+ * may be NULL, not all): FP8 codes [rows][inter] + E8M0 [rows][inter/32]; bf16 values [rows][inter]
+ * (8-k permuted when permute = 1, fused.py:303-305). */
+int dsv41_swiglu_quant(const float* gu, long long ld_gu, const float* wt, int rows, int inter, float limit,
+                       uint8_t* codes, uint8_t* scales, uint16_t* h_bf16, int permute, void* stream);
+
+/* Grouped FP4 x FP8 GEMM on block-scaled MFMA: for each group g (expert grp_expert[g], pairs
+ * grp_start[g] .. grp_start[g+1]-1) and pair p: out[out_row ? out_row[p] : p][0:N] (=, +=, atomic += for
+ * accum 0 / 1 / 2) (pair_wt ? pair_wt[p] : 1) * sum_k x[pair_tok[p]][k] * deq(W[e])[n][k].
+ * Replaces cukern.fp4_gemm_tc (cukern.py:238-276, fp4_tcw.cu / fp4_tc.cu), cukern.fp4_gemv_pairs
+ * (cukern.py:60-77, fp4_gemv.cu) and moe_kernels.grouped_fp4_gemm (moe_kernels.py:127-200).
+ * Groups of any size (max_tokens selects the pass width); groups whose expert is outside
+ * [shard_start, shard_start + shard_n) are skipped and, with zero_out, their rows zeroed (cukern.py:244-246);
+ * groups with fewer than min_tok or more than max_tok pairs are skipped. N % 16 == 0, K % 128 == 0. */
+int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
+                           int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs,
+                           const int* grp_expert, const int* grp_start, int G, const int* pair_tok,
+                           float* out, long long ldo, const int* out_row, const float* pair_wt, int accum, int max_tokens,
+                           int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
+
+/* Decode down projection and per-token combine: y[t][n] = sum over groups g and their pair p of token t of
+ * h_p . deq(W2[e_g])[n]  (M <= 16 tokens, n_slots <= 256 group slots; slots with expert -1 are unused).
+ * Optional outputs: y fp32 [M][ldy]; yb bf16 = bf16(y + ys) with ys the bf16 shared-expert output or NULL.
+ * Replaces the w2 call of decode.DecodeRuntime.experts_tc (decode.py:316-335) plus the sum of the k rows in
+ * fused2.hc_post2_ (fused2.py:490-495) and model.MoE.__call__ (model.py:581, 590-591). */
+int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
+                       int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs,
+                       const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
+                       float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
+                       int shard_start, int shard_n, void* stream);
+
+/* out[t][n] = sum_k x[t][k] * W[n][k], bf16 W [N][ldw], bf16 x [M][ldx], M <= 16, fp32 and/or bf16 output.
+ * The bf16 shared expert's two GEMVs (model.MoE.shared_expert, model.py:409-412; decode.py:369-371) and the
+ * router logits (decode.py:357, model.py:391-392). */
+int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int N, int K, const uint16_t* x, long long ldx, int M,
+                          float* out, long long ldo, uint16_t* outb, long long ldob, void* stream);
+
+/* MoE gate on logits: score_func 0 sqrt(softplus), 1 sigmoid, 2 softmax; top-k of scores + bias (lowest index
+ * wins ties); weights renormalised when norm, times route_scale. fused2.gate_topk (fused2.py:418-471),
+ * model.MoE.gate (model.py:391-404). */
+int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B, int E, float temp, int topk, float route_scale,
+                    int score_func, int norm, int* eid, float* wt, void* stream);
+
+/* Expert bucketing of n = tokens * topk pairs: tok_sorted, wt_sorted, inv, grp_expert (-1 padded), grp_start
+ * (n padded), groups of <= gmax pairs per expert; n_groups (optional) receives the group count. Pairs keep
+ * ascending order within an expert. cukern.moe_dispatch (cukern.py:323-337, p2p.cu:90-132); E <= 512. */
+int dsv41_moe_dispatch(const int* eid, const float* wt, int n, int topk, int E, int gmax, int* tok_sorted, float* wt_sorted,
+                       int* inv, int* grp_expert, int* grp_start, int* n_groups, void* stream);
+
+/* Diagnostics (no reference counterpart): one wave runs one matrix instruction on caller-given operands so a
+ * test can check the lane layouts the kernels rely on. a, b: [64][8] dwords; sa, sb: [64]; c: [64][4] fp32. */
+int dsv41_selftest_mfma_scale(const int* a, const int* b, const int* sa, const int* sb, float* c, int fmt_a, int fmt_b, void* stream);
+int dsv41_selftest_mfma_bf16(const uint16_t* a, const uint16_t* b, float* c, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV41_AMD_H */

@@ -49,11 +49,11 @@ def bits_f32(u) -> np.ndarray:
 
 def f32_to_bf16_bits(a) -> np.ndarray:
     """Round-to-nearest-even fp32 -> bf16 bit pattern (torch's `.to(torch.bfloat16)`).
-    NaN follows CPU torch: the sign is kept and the payload saturates (0x7FFF / 0xFFFF)."""
+    Every NaN becomes 0xFFFF, as torch's vectorised CPU conversion writes it."""
     u = f32_bits(a).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
     nan = np.isnan(np.asarray(a, dtype=F32))
-    r = np.where(nan, (u >> 16).astype(np.uint32) | 0x7FFF, r)
+    r = np.where(nan, np.uint32(0xFFFF), r)
     return (r & 0xFFFF).astype(np.uint16)
 
 
@@ -144,7 +144,12 @@ def dequant_fp4(packed, scale, block: int = 32) -> np.ndarray:
 
 
 def dequant_fp4_values(packed, scale) -> np.ndarray:
-    """fp32 values of the bf16 dequant (what the reference's torch oracles multiply with)."""
+    """fp32 values of the bf16 dequant (what the reference's torch oracles multiply with). When every scale
+    byte is in [2, 250] the fp32 product already has <= 2 significant bits inside bf16's exponent range, so the
+    bf16 rounding is the identity and is skipped (test_oracle checks this shortcut against the full path)."""
+    sc = np.asarray(scale)
+    if sc.size and sc.min() >= 2 and sc.max() <= 250:
+        return dequant_fp4_f32(packed, scale)
     return bf16_bits_to_f32(dequant_fp4(packed, scale))
 
 
@@ -341,10 +346,10 @@ def gemv_pairs(x, w, s, row_in, expert, wt) -> np.ndarray:
 
 def expert_pair(xq_row, W13, S13, W2, S2, wt: float, inter: int, limit: float):
     """One (token, expert) pair of the layer (test_cpumoe.py:19-25, fused.py:284-306, decode.py:316-335):
-    gu = xq . deq(W13)^T ; h = swiglu_quant(gu, w) ; y2 = h . deq(W2)^T. fp32 [H]."""
-    gu = (deq64(W13, S13) @ np.asarray(xq_row, np.float64)).astype(F32)
+    gu = xq . deq(W13)^T ; h = swiglu_quant(gu, w) ; y2 = h . deq(W2)^T. fp32 [H], fp32 accumulation."""
+    gu = (dense_weights(W13, S13) @ np.asarray(xq_row, F32)).astype(F32)
     h = swiglu_quant(gu.reshape(1, -1), np.array([wt], F32), inter, limit)[0]
-    return (deq64(W2, S2) @ h.astype(np.float64)).astype(F32)
+    return (dense_weights(W2, S2) @ h.astype(F32)).astype(F32)
 
 
 def deq64(w, s):
@@ -354,11 +359,11 @@ def deq64(w, s):
 def shared_expert(xq, Ws13, Ws2, inter: int, limit: float) -> np.ndarray:
     """Shared expert with bf16 weights (model.py:409-412, decode.py:369-371): gu = xq . Ws13^T (fp32),
     h = swiglu_quant(gu, no weight), ys = bf16(h . Ws2^T). Returns fp32 values of the bf16 ys [M, H]."""
-    Ws13 = bf16_bits_to_f32(Ws13).astype(np.float64)
-    Ws2 = bf16_bits_to_f32(Ws2).astype(np.float64)
-    gu = (np.asarray(xq, np.float64) @ Ws13.T).astype(F32)
+    Ws13 = bf16_bits_to_f32(Ws13)
+    Ws2 = bf16_bits_to_f32(Ws2)
+    gu = (np.asarray(xq, F32) @ Ws13.T).astype(F32)
     h = swiglu_quant(gu, None, inter, limit)
-    return bf16_round((h.astype(np.float64) @ Ws2.T).astype(F32))
+    return bf16_round((h @ Ws2.T).astype(F32))
 
 
 def moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter: int, limit: float) -> np.ndarray:
@@ -369,17 +374,26 @@ def moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter: int, limit: float) ->
     M, k = np.shape(eid)
     H = W2.shape[1]
     y = np.zeros((M, H), F32)
-    cache = {}
+    # fp32 BLAS products (fp32 accumulation, as the reference's kernels); experts dequantised once each
+    experts = sorted({int(e) for e in np.asarray(eid).reshape(-1)})
+    gu_all = {}
+    for e in experts:
+        A13 = dense_weights(W13[e], S13[e])
+        toks = [t for t in range(M) if e in [int(v) for v in eid[t]]]
+        gu_all[e] = {t: (A13 @ xq[t]).astype(F32) for t in toks}
+        del A13
+    y2 = {}
+    for e in experts:
+        A2 = dense_weights(W2[e], S2[e])
+        for t, gu in gu_all[e].items():
+            j = [int(v) for v in eid[t]].index(e)
+            h = swiglu_quant(gu.reshape(1, -1), np.array([wt[t][j]], F32), inter, limit)[0]
+            y2[(t, j)] = (A2 @ h).astype(F32)
+        del A2
     for t in range(M):
         acc = np.zeros(H, F32)
         for j in range(k):
-            e = int(eid[t][j])
-            if e not in cache:
-                cache[e] = (deq64(W13[e], S13[e]), deq64(W2[e], S2[e]))
-            A13, A2 = cache[e]
-            gu = (A13 @ xq[t].astype(np.float64)).astype(F32)
-            h = swiglu_quant(gu.reshape(1, -1), np.array([wt[t][j]], F32), inter, limit)[0]
-            acc = (acc + (A2 @ h.astype(np.float64)).astype(F32)).astype(F32)
+            acc = (acc + y2[(t, j)]).astype(F32)
         y[t] = acc
     return y
 

@@ -1,0 +1,85 @@
+"""Format kernels against the golden vectors written by the reference's quant.py and against the oracle:
+dequant_fp4 bit-exact over every (code, scale byte) and both layouts; fake_quant_fp8 / quant_fp8 bit-exact;
+swiglu_quant against the oracle (identical up to an E4M3 ulp where fp32 evaluation order flips a rounding)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "quant_golden.npz")
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def gold():
+    return np.load(GOLD, allow_pickle=False)
+
+
+def u16(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_dequant_every_code_and_scale(gold):
+    from dsv41_amd import quant
+    p = torch.from_numpy(gold["deq_all_packed"]).to(DEV)
+    s = torch.from_numpy(gold["deq_all_scale"]).to(DEV)
+    # K = 32 per row: one scale byte per row, all 256 bytes and all 16 codes
+    out = u16(quant.dequant_fp4(p, s))
+    assert np.array_equal(out, gold["deq_all_bf16"])
+
+
+def test_dequant_random_row_major_and_tiled(gold):
+    from dsv41_amd import quant
+    w = torch.from_numpy(gold["rand_w"]).to(DEV)
+    s = torch.from_numpy(gold["rand_s"]).to(DEV)
+    assert np.array_equal(u16(quant.dequant_fp4(w, s)), gold["rand_deq_bf16"])
+    wt = torch.from_numpy(gold["rand_w_tiled"]).to(DEV)
+    st = torch.from_numpy(gold["rand_s_tiled"]).to(DEV)
+    assert np.array_equal(u16(quant.dequant_fp4(wt, st, tiled=True)), gold["rand_deq_bf16"])
+    # torch-side tiling helpers agree with the reference's layout
+    assert torch.equal(quant.tile_fp4(w), wt) and torch.equal(quant.tile_fp4_scales(s), st)
+
+
+def test_fake_quant_fp8_golden(gold):
+    from dsv41_amd import quant
+    xb = torch.from_numpy(gold["fq8_in_bf16"].view(np.int16)).view(torch.bfloat16).to(DEV)
+    assert np.array_equal(u16(quant.fake_quant_fp8(xb)), gold["fq8_out_bf16"])
+    xf = torch.from_numpy(gold["fq8_in_f32"]).to(DEV)
+    assert np.array_equal(quant.fake_quant_fp8(xf).cpu().numpy().view(np.uint32), gold["fq8_out_f32"].view(np.uint32))
+    q, s = quant.quant_fp8(xb)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), gold["qfp8_codes_bf16in"])
+    assert np.array_equal(s.cpu().numpy(), gold["qfp8_scales_bf16in"])
+
+
+def test_quant_permuted_input_gives_natural_codes():
+    from dsv41_amd import hipkern, quant
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 1024, generator=g).to(torch.bfloat16).to(DEV)
+    c0, s0 = quant.quant_fp8_e8m0(x)
+    c1, s1 = quant.quant_fp8_e8m0(hipkern.permute_x(x), permuted=True)
+    assert torch.equal(c0, c1) and torch.equal(s0, s1)
+    codes, e8 = O.quant_fp8_e8m0(O.bf16_bits_to_f32(u16(x)))
+    assert np.array_equal(c0.cpu().numpy(), codes) and np.array_equal(s0.cpu().numpy(), e8)
+
+
+@pytest.mark.parametrize("limit,weighted,permute", [(10.0, True, False), (0.0, True, True), (10.0, False, False)])
+def test_swiglu_quant(limit, weighted, permute):
+    from dsv41_amd import fused
+    g = torch.Generator().manual_seed(4)
+    rows, inter = 9, 1664
+    gu = torch.randn(rows, 2 * inter, generator=g) * 5
+    wt = torch.rand(rows, generator=g)
+    h = fused.swiglu_quant(gu.to(DEV), wt.to(DEV) if weighted else None, inter, limit, permute=permute)
+    ref = O.swiglu_quant(gu.numpy(), wt.numpy() if weighted else None, inter, limit, permute=permute)
+    got = O.bf16_bits_to_f32(u16(h))
+    # identical except where an ulp-level difference of silu/exp flips a bf16 or E4M3 rounding
+    assert (got == ref).mean() > 0.995
+    assert O.rel_l2(got, ref) < 2e-3
+    # the codes output decodes to exactly the bf16 output's values
+    c, s = fused.swiglu_quant_codes(gu.to(DEV), wt.to(DEV) if weighted else None, inter, limit)
+    vals = O.e4m3_decode(c.cpu().numpy()) * np.repeat(O.e8m0_to_f32(s.cpu().numpy()), 32, axis=-1)
+    assert np.array_equal(vals, got if not permute else O.unpermute_x(got))

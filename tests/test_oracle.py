@@ -182,3 +182,10 @@ def test_grouped_gemm_textbook():
             code = (w[e, n, kk // 2] >> (4 * (kk % 2))) & 15
             acc += float(x[tok[p], kk]) * float(O.FP4_TABLE[code]) * 2.0 ** (int(s[e, n, kk // 32]) - 127)
         assert abs(out[p, n] - acc) <= 1e-5 * max(1.0, abs(acc))
+
+
+def test_dequant_shortcut_matches_full_path():
+    rng = np.random.default_rng(12)
+    w = rng.integers(0, 256, (64, 128), dtype=np.uint8)
+    s = rng.integers(2, 251, (64, 8), dtype=np.uint8)
+    assert np.array_equal(O.dequant_fp4_values(w, s), O.bf16_bits_to_f32(O.dequant_fp4(w, s)))
