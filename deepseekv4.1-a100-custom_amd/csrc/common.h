@@ -108,9 +108,11 @@ __device__ __forceinline__ float wave_max32(float v) {  // max over each 32-lane
 
 // ------------------------------------------------------------------------------------------ MFMA
 // D(16x16, fp32) += A(16x128) * B(128x16) with per-32 E8M0 block scales (gfx950 block-scaled MFMA).
-// A = E2M1 weights (format 4): lane l holds 32 k of row l%16 (16 bytes in the low 4 dwords), k-block l/16.
-// B = E4M3 activations (format 0): lane l holds 32 k of column l%16 (32 bytes), k-block l/16.
-// sa / sb: the lane's E8M0 byte (byte 0 of the register). Output: lane l holds D[4*(l/16)+i][l%16].
+// Lane layouts (measured on gfx950 by tests/test_gpu_mfma_layout.py), g = l/16:
+// A = E2M1 weights (format 4): lane l holds row l%16, k [32g, 32g+32) contiguous: 16 bytes in the low 4 dwords,
+//     low nibble first. B = E4M3 activations (format 0): lane l holds column l%16, bytes 0-15 = k [16g, 16g+16)
+//     and bytes 16-31 = k [64+16g, 64+16g+16). sa / sb: byte 0 of the lane's register, the E8M0 scale of
+//     32-k block g of row / column l%16. Output: lane l holds D[4g+i][l%16], i = 0..3.
 __device__ __forceinline__ v4f mfma_fp4w_fp8x(v8i a, v8i b, v4f c, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
 }

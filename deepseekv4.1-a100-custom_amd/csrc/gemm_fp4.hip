@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
             const int q = base + c * 16 + col;
             ok[c] = q < p1;
             const long long r = ok[c] ? a.pair_tok[q] : 0;
-            xp[c] = a.xc + r * a.ldx + kb * 32;
+            xp[c] = a.xc + r * a.ldx + kb * 16;
             xsp[c] = a.xs + r * a.ldxs + kb;
         }
         v4f acc[NCH];
@@ -101,9 +101,9 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 if (ok[c]) {
-                    const v4i* p = (const v4i*)(xp[c] + kc * 128);
-                    B0[c][slot] = p[0];
-                    B1[c][slot] = p[1];
+                    const uint8_t* p = xp[c] + kc * 128;
+                    B0[c][slot] = *(const v4i*)p;
+                    B1[c][slot] = *(const v4i*)(p + 64);
                     SB[c][slot] = xsp[c][kc * 4];
                 } else {
                     B0[c][slot] = v4i{0, 0, 0, 0};
@@ -208,9 +208,9 @@ __global__ void __launch_bounds__(256) moe_down_sum_kernel(const DownSumArgs a) 
         A[slot] = __builtin_nontemporal_load((const v4i*)(a.W + (long long)e * a.stride_we + w0 + lkc * ws));
         SA[slot] = a.S[(long long)e * a.stride_se + s0 + lkc * ss];
         if (q >= 0) {
-            const v4i* p = (const v4i*)(a.hc + (long long)q * a.ldh + lkc * 128 + kb * 32);
-            B0[slot] = p[0];
-            B1[slot] = p[1];
+            const uint8_t* p = a.hc + (long long)q * a.ldh + lkc * 128 + kb * 16;
+            B0[slot] = *(const v4i*)p;
+            B1[slot] = *(const v4i*)(p + 64);
             SB[slot] = a.hs[(long long)q * a.ldhs + lkc * 4 + kb];
         } else {
             B0[slot] = v4i{0, 0, 0, 0};

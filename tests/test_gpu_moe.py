@@ -49,6 +49,7 @@ def host_subset(ws, ids):
     class View:
         def __init__(self, a):
             self.a = a
+            self.shape = (None,) + a.shape[1:]
 
         def __getitem__(self, e):
             return self.a[pos[int(e)]]
@@ -233,7 +234,8 @@ def test_decode_full_batched_equals_single(full_layer, M):
 
 def test_decode_layer_with_shared_expert_and_router(full_layer):
     """Whole layer: router GEMV (bf16 [384, 7168]) -> softmax top-8 -> shared bf16 SwiGLU + routed experts ->
-    bf16(sum + ys), against the oracle's layer."""
+    bf16(sum + ys). Each stage against the oracle in fp32 (the tolerance is defined on fp32 outputs), and the
+    final bf16 rounding bit-exactly against the composition of the stages."""
     from dsv41_amd import moe
     E, H, I, ws, ex = full_layer
     g = torch.Generator(device=DEV).manual_seed(77)
@@ -242,15 +244,31 @@ def test_decode_layer_with_shared_expert_and_router(full_layer):
     G = (torch.randn(E, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16)
     layer = moe.MoEDecodeLayer(ex, Ws13, Ws2, 10.0, topk=8, score_func="softmax", router=G)
     x = rand_x(1, H, 78).to(DEV)
-    y = layer(x)
+    y = layer(x).clone()
+    b = layer._bufs[1]
+    # routing
     logits = (x.float().cpu() @ G.float().cpu().T).numpy()
+    assert np.allclose(b["logits"].cpu().numpy(), logits, rtol=1e-4, atol=1e-4)
     eid, wt = O.gate_topk(logits, None, 1.0, 8, 1.0, "softmax", True)
-    got_eid, got_wt = layer.last_routing[1]
-    assert np.array_equal(got_eid.cpu().numpy(), eid)
-    W13, S13, W2, S2 = host_subset(ws, set(eid.reshape(-1).tolist()))
+    assert np.array_equal(b["eid"].cpu().numpy(), eid)
+    assert np.allclose(b["wt"].cpu().numpy(), wt, rtol=1e-4)
+    # shared expert (bf16 output)
     u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    ref = O.moe_layer(bf16_vals(x), eid, got_wt.cpu().numpy(), W13, S13, W2, S2, u16(Ws13), u16(Ws2), I, 10.0)
-    close(bf16_vals(y), ref, "decode layer with shared expert")
+    xq = bf16_vals(b["xq"])
+    assert np.array_equal(xq, O.fake_quant_fp8(bf16_vals(x)))
+    ys_ref = O.shared_expert(xq, u16(Ws13), u16(Ws2), I, 10.0)
+    close(bf16_vals(b["ys"]), ys_ref, "shared expert")
+    # routed experts in fp32
+    y32 = torch.empty(1, H, device=DEV)
+    out = torch.empty(1, H, dtype=torch.bfloat16, device=DEV)
+    moe.moe_experts(b["xq"], b["eid"], b["wt"], ex, 10.0, ys=b["ys"], out=out, y32=y32)
+    W13, S13, W2, S2 = host_subset(ws, set(eid.reshape(-1).tolist()))
+    routed_ref = O.moe_layer_routed(xq, eid, b["wt"].cpu().numpy(), W13, S13, W2, S2, I, 10.0)
+    close(y32.cpu().numpy(), routed_ref, "routed experts fp32")
+    close(y32.cpu().numpy() + bf16_vals(b["ys"]), routed_ref + ys_ref, "layer fp32 (routed + shared)")
+    # final rounding: out = bf16(y32 + ys) exactly, and the layer call produced the same bits
+    comp = O.f32_to_bf16_bits((y32.cpu().numpy() + bf16_vals(b["ys"])).astype(np.float32))
+    assert np.array_equal(u16(out), comp) and torch.equal(out, y)
 
 
 def test_graph_capture_replay(full_layer):
