@@ -66,6 +66,7 @@ def make_layers(torch, dev, n, seed):
 def graph_time(torch, fn_steps, steps, warmup):
     """Capture `steps` calls (fn_steps(i) for i in range(steps)) in one graph; replay warmup then timed."""
     s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())   # inputs were produced on the current stream
     with torch.cuda.stream(s):
         for i in range(min(steps, 4)):
             fn_steps(i)                       # eager warm-up: workspaces allocated outside capture
@@ -95,7 +96,7 @@ def routing_stream(torch, dev, steps, M, seed):
 
 
 def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared=None, seed=7):
-    from dsv41_amd import fused2, moe, quant
+    from dsv41_amd import moe, quant
     logits = routing_stream(torch, dev, steps, M, seed)
     gx = torch.Generator(device=dev).manual_seed(seed + 1)
     x = torch.randn(M, H, generator=gx, device=dev).to(torch.bfloat16)
@@ -107,9 +108,8 @@ def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared
 
     def step(i):
         ex = layers[i % len(layers)]
-        fused2.gate_topk(logits[i], None, 1.0, TOPK, 1.0, "softmax", True, eid=eid[i], wt=wt[i])
         y_s = moe.shared_expert(xq, shared[0], shared[1], LIMIT, ys=ys) if with_shared else None
-        moe.moe_experts(xq, eid[i], wt[i], ex, LIMIT, ys=y_s, out=out)
+        moe.moe_route_experts(xq, logits[i], None, 1.0, TOPK, 1.0, "softmax", True, ex, LIMIT, ys=y_s, out=out, eid_out=eid[i], wt_out=wt[i])
 
     t, g = graph_time(torch, step, steps, warmup)
     # unique experts per step (selected-expert bytes: each unique expert is read once)
@@ -117,24 +117,15 @@ def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared
     return t, statistics.mean(uniq)
 
 
-def bench_w13_kernel(torch, dev, layers, steps, warmup):
-    """The dominant kernel alone (w13 grouped GEMV, M = 1): average launch duration from HIP events on the
-    launch stream, over the same rotating inputs."""
-    from dsv41_amd import fused2, hipkern, moe, quant
+def bench_up_kernel(torch, dev, layers, steps, warmup):
+    """The dominant kernel alone (dsv41_moe_decode_up at M = 1: routing + w13 + SwiGLU): average launch duration
+    from HIP events on its launch stream, over the same rotating layers and fresh logits."""
+    from dsv41_amd import moe, quant
     logits = routing_stream(torch, dev, steps, 1, 11)
-    eid = torch.empty(steps, 1, TOPK, dtype=torch.int32, device=dev)
-    wt = torch.empty(steps, 1, TOPK, dtype=torch.float32, device=dev)
-    for i in range(steps):
-        fused2.gate_topk(logits[i], None, 1.0, TOPK, 1.0, "softmax", True, eid=eid[i], wt=wt[i])
-    x = torch.randn(1, H, device=dev).to(torch.bfloat16)
-    xc, xs = quant.quant_fp8_e8m0(quant.fake_quant_fp8(x))
-    gs = torch.arange(TOPK + 1, dtype=torch.int32, device=dev)
-    tok = torch.zeros(TOPK, dtype=torch.int32, device=dev)
-    gu = torch.empty(TOPK, 2 * I, dtype=torch.float32, device=dev)
+    xq = quant.fake_quant_fp8(torch.randn(1, H, device=dev).to(torch.bfloat16))
 
     def step(i):
-        ex = layers[i % len(layers)]
-        hipkern.grouped_gemm_codes(xc, xs, ex.w13, ex.s13, eid[i].view(-1), gs, tok, gu, 1, True)
+        moe.decode_up(xq, layers[i % len(layers)], LIMIT, TOPK, logits=logits[i], gate=(None, 1.0, 1.0, "softmax", True))
 
     t, _ = graph_time(torch, step, steps, warmup)
     return t
@@ -216,12 +207,14 @@ def main():
     t_routed, _ = bench_decode(torch, dev, layers, K, W, 1)
     value = sel_bytes / t_routed / 1e12
     extra = {}
-    # dominant kernel roofline: w13 grouped GEMV at M = 1 (8 experts x (W13 + S13) bytes per launch)
+    # dominant kernel roofline: the fused up kernel at M = 1 (8 experts x (W13 + S13) bytes per launch; the
+    # logits and activations it also reads are < 0.03 % of that and not counted)
     w13_bytes = TOPK * (2 * I * (H // 2) + 2 * I * (H // 32))
-    t_w13 = bench_w13_kernel(torch, dev, layers, K, W)
-    roof = {"bound": "hbm", "kernel": "fp4_grouped_kernel<1,1,8> (w13, M=1)", "achieved": round(w13_bytes / t_w13 / 1e9, 1),
-            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(w13_bytes / t_w13 / HBM_PEAK, 4), "traffic": None,
-            "avg_launch_us": round(t_w13 * 1e6, 2), "algorithmic_bytes": w13_bytes}
+    t_up = bench_up_kernel(torch, dev, layers, K, W)
+    roof = {"bound": "hbm", "kernel": "moe_decode_up_kernel<1,8,8> (routing + w13 + SwiGLU, M=1)", "achieved": round(w13_bytes / t_up / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(w13_bytes / t_up / HBM_PEAK, 4), "traffic": None,
+            "avg_launch_us": round(t_up * 1e6, 2), "algorithmic_bytes": w13_bytes}
+    extra["down_sum_us_est"] = round((t_routed - t_up) * 1e6, 2)
     if not args.quick:
         g = torch.Generator(device=dev).manual_seed(5)
         Ws13 = (torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)

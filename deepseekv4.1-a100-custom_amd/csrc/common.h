@@ -106,6 +106,73 @@ __device__ __forceinline__ float wave_max32(float v) {  // max over each 32-lane
     return v;
 }
 
+// Full-wave reductions on DPP row operations (a few cycles per step, no LDS crossbar round trips): the classic
+// row_shr 1/2/3, row_shr 4/8 (bank masked), row_bcast 15/31 sequence leaves the result in lane 63, which
+// readlane broadcasts. Lanes a DPP step has no source for keep their own value (update_dpp with old = self).
+#define DPP_STEP(T, x, op, ctrl, rmask, bmask)                                                                 \
+    x = op(x, __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, x),                    \
+                                                                __builtin_bit_cast(int, x), ctrl, rmask, bmask, false)))
+__device__ __forceinline__ float fmax2(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float fadd2(float a, float b) { return a + b; }
+
+__device__ __forceinline__ float wave_reduce_max(float x) {
+    DPP_STEP(float, x, fmax2, 0x111, 0xF, 0xF);   // row_shr:1
+    DPP_STEP(float, x, fmax2, 0x112, 0xF, 0xF);   // row_shr:2
+    DPP_STEP(float, x, fmax2, 0x113, 0xF, 0xF);   // row_shr:3
+    DPP_STEP(float, x, fmax2, 0x114, 0xF, 0xE);   // row_shr:4
+    DPP_STEP(float, x, fmax2, 0x118, 0xF, 0xC);   // row_shr:8
+    DPP_STEP(float, x, fmax2, 0x142, 0xA, 0xF);   // row_bcast:15
+    DPP_STEP(float, x, fmax2, 0x143, 0xC, 0xF);   // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// wave sum in a fixed order (the same DPP tree every call): deterministic. Steps 1-3 add the ORIGINAL values of
+// lanes i-1, i-2, i-3 (a running source would count elements twice); steps 4-7 combine partial sums. Lanes a
+// step has no source for add 0 (update_dpp with old = 0).
+__device__ __forceinline__ float wave_reduce_sum(float x) {
+#define DPP_SRC(v, ctrl, rmask, bmask) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rmask, bmask, false))
+    float t = x;
+    t += DPP_SRC(x, 0x111, 0xF, 0xF);   // row_shr:1
+    t += DPP_SRC(x, 0x112, 0xF, 0xF);   // row_shr:2
+    t += DPP_SRC(x, 0x113, 0xF, 0xF);   // row_shr:3
+    t += DPP_SRC(t, 0x114, 0xF, 0xE);   // row_shr:4, lanes 4..15 of each row
+    t += DPP_SRC(t, 0x118, 0xF, 0xC);   // row_shr:8, lanes 8..15
+    t += DPP_SRC(t, 0x142, 0xA, 0xF);   // row_bcast:15 into rows 1, 3
+    t += DPP_SRC(t, 0x143, 0xC, 0xF);   // row_bcast:31 into rows 2, 3
+#undef DPP_SRC
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 63));
+}
+
+// wave max of 64-bit unsigned keys (two 32-bit DPP moves per step)
+__device__ __forceinline__ unsigned long long wave_reduce_max_u64(unsigned long long x) {
+#define DPP_MAX64(ctrl, rmask, bmask)                                                                          \
+    {                                                                                                          \
+        const unsigned lo = (unsigned)x, hi = (unsigned)(x >> 32);                                             \
+        const unsigned nlo = (unsigned)__builtin_amdgcn_update_dpp((int)lo, (int)lo, ctrl, rmask, bmask, false); \
+        const unsigned nhi = (unsigned)__builtin_amdgcn_update_dpp((int)hi, (int)hi, ctrl, rmask, bmask, false); \
+        const unsigned long long n = ((unsigned long long)nhi << 32) | nlo;                                    \
+        x = n > x ? n : x;                                                                                     \
+    }
+    DPP_MAX64(0x111, 0xF, 0xF);
+    DPP_MAX64(0x112, 0xF, 0xF);
+    DPP_MAX64(0x113, 0xF, 0xF);
+    DPP_MAX64(0x114, 0xF, 0xE);
+    DPP_MAX64(0x118, 0xF, 0xC);
+    DPP_MAX64(0x142, 0xA, 0xF);
+    DPP_MAX64(0x143, 0xC, 0xF);
+#undef DPP_MAX64
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)x, 63);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(x >> 32), 63);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// float -> uint32 whose unsigned order is the float order (NaN excluded by the caller)
+__device__ __forceinline__ unsigned float_order_key(float f) {
+    const unsigned u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // ------------------------------------------------------------------------------------------ MFMA
 // D(16x16, fp32) += A(16x128) * B(128x16) with per-32 E8M0 block scales (gfx950 block-scaled MFMA).
 // Lane layouts (measured on gfx950 by tests/test_gpu_mfma_layout.py), g = l/16:
@@ -115,4 +182,113 @@ __device__ __forceinline__ float wave_max32(float v) {  // max over each 32-lane
 //     32-k block g of row / column l%16. Output: lane l holds D[4g+i][l%16], i = 0..3.
 __device__ __forceinline__ v4f mfma_fp4w_fp8x(v8i a, v8i b, v4f c, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
+}
+
+// ------------------------------------------------------------------------------------------ weight tiles
+// Byte offset of lane `lane`'s 16 weight bytes for 16-row block nb, k-chunk kc (128 k), and of its scale byte.
+// Lane l: row nb*16 + l%16, k [kc*128 + 32*(l/16), +32).
+template <int TILED>
+__device__ __forceinline__ long long wtile_off(int nb, int kc, int nk, int Kh, int lane) {
+    if (TILED) return ((long long)nb * nk + kc) * 1024 + (lane & 15) * 64 + (lane >> 4) * 16;   // quant.py:118-122
+    return ((long long)nb * 16 + (lane & 15)) * Kh + kc * 64 + (lane >> 4) * 16;
+}
+template <int TILED>
+__device__ __forceinline__ long long stile_off(int nb, int kc, int nk, int Ks, int lane) {
+    if (TILED) return ((long long)nb * nk + kc) * 64 + (lane & 15) * 4 + (lane >> 4);           // quant.py:130-134
+    return ((long long)nb * 16 + (lane & 15)) * Ks + kc * 4 + (lane >> 4);
+}
+
+// weight tiles are streamed once: non-temporal loads keep them from displacing reused data in the caches
+#ifndef DSV41_WEIGHT_NT
+#define DSV41_WEIGHT_NT 1
+#endif
+__device__ __forceinline__ v4i load_weight_tile(const uint8_t* p) {
+#if DSV41_WEIGHT_NT
+    return __builtin_nontemporal_load((const v4i*)p);
+#else
+    return *(const v4i*)p;
+#endif
+}
+// Buffer loads: a 128-bit descriptor in scalar registers holds the base address and the byte count, the lane
+// supplies a 32-bit offset and the loop a scalar one. Per-lane 64-bit addresses (two VGPRs per in-flight slot)
+// disappear, and an offset at or beyond `bytes` reads 0 instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i buffer_load_tile(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, DSV41_WEIGHT_NT ? 2 : 0));
+}
+__device__ __forceinline__ int buffer_load_byte(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
+}
+#ifndef DSV41_PF_UP
+#define DSV41_PF_UP 8
+#endif
+
+// ------------------------------------------------------------------------------------------ load pipeline
+// Software pipeline over n iterations with PF register slots: load(slot, it) fills a slot, use(slot) consumes
+// it. The steady-state loop has no guards (every load in bounds); only the peeled drain has uniform (scalar)
+// guards, so the compiler can keep PF loads in flight with exact vmcnt waits instead of draining the queue.
+template <int PF, typename LoadF>
+__device__ __forceinline__ void pipeline_start(int n, LoadF&& load) {
+    // unconditional prologue: the loop is entered with exactly PF slots in flight, in slot order, so the
+    // waitcnt pass can wait for the oldest slot only (a conditional prologue makes it drain the queue);
+    // sched_barrier(0) keeps each consume/refill pair in program order
+    if (n < PF) return;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+        load(i, i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int PF, typename LoadF, typename UseF>
+__device__ __forceinline__ void pipeline_finish(int n, LoadF&& load, UseF&& use) {
+    if (n < PF) {  // short: no pipeline
+        for (int i = 0; i < n; ++i) {
+            load(0, i);
+            use(0);
+        }
+        return;
+    }
+    int it = 0;
+    for (; it + 2 * PF <= n; it += PF) {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            use(i);
+            load(i, it + PF + i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+        use(i);
+        if (it + PF + i < n) load(i, it + PF + i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    it += PF;
+#pragma unroll
+    for (int i = 0; i < PF; ++i)
+        if (it + i < n) use(i);
+}
+
+template <int PF, typename LoadF, typename UseF>
+__device__ __forceinline__ void pipelined(int n, LoadF&& load, UseF&& use) {
+    pipeline_start<PF>(n, load);
+    pipeline_finish<PF>(n, load, use);
+}
+
+// The same pipeline over a compile-time trip count NK, fully unrolled: straight-line code lets the waitcnt pass
+// emit exact rolling waits (wait for the oldest slot only) instead of draining the queue at a loop head.
+template <int PF, int NK, typename LoadF, typename UseF>
+__device__ __forceinline__ void pipelined_fixed(LoadF&& load, UseF&& use) {
+#pragma unroll
+    for (int i = 0; i < (PF < NK ? PF : NK); ++i) load(i, i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < NK; ++it) {
+        use(it % PF);
+        if (it + PF < NK) load(it % PF, it + PF);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }

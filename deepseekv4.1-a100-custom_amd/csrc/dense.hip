@@ -25,29 +25,20 @@ __global__ void __launch_bounds__(WPG * 64) dense_gemv_bf16_kernel(const DenseAr
     const int col = lane & 15, kb = lane >> 4;
     const int nk = a.K >> 5;                               // 32-k chunks
     const int c0 = (int)((long long)nk * wave / WPG), c1 = (int)((long long)nk * (wave + 1) / WPG);
-    const uint16_t* wrow = a.W + ((long long)nb * 16 + col) * a.ldw + kb * 8;
+    const uint16_t* wrow = a.W + ((long long)nb * 16 + col) * a.ldw + kb * 8 + (long long)c0 * 32;
     const bool ok = col < a.M;
-    const uint16_t* xrow = a.x + (long long)(ok ? col : 0) * a.ldx + kb * 8;
+    // columns without a token read row 0 (their outputs are not stored): no divergent loads
+    const uint16_t* xrow = a.x + (long long)(ok ? col : 0) * a.ldx + kb * 8 + (long long)c0 * 32;
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
     v4i A[PF], B[PF];
-    const int n = c1 - c0;
-    auto load = [&](int slot, int c) {
-        A[slot] = __builtin_nontemporal_load((const v4i*)(wrow + (long long)c * 32));
-        B[slot] = ok ? *(const v4i*)(xrow + (long long)c * 32) : v4i{0, 0, 0, 0};
-    };
-#pragma unroll
-    for (int i = 0; i < PF; ++i)
-        if (i < n) load(i, c0 + i);
-    for (int k0 = 0; k0 < n; k0 += PF) {
-#pragma unroll
-        for (int i = 0; i < PF; ++i) {
-            const int it = k0 + i;
-            if (it < n) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, A[i]), __builtin_bit_cast(v8bf, B[i]), acc, 0, 0, 0);
-                if (it + PF < n) load(i, c0 + it + PF);
-            }
-        }
-    }
+    pipelined<PF>(c1 - c0,
+        [&](int slot, int c) {
+            A[slot] = __builtin_nontemporal_load((const v4i*)(wrow + (long long)c * 32));
+            B[slot] = *(const v4i*)(xrow + (long long)c * 32);
+        },
+        [&](int slot) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, A[slot]), __builtin_bit_cast(v8bf, B[slot]), acc, 0, 0, 0);
+        });
     s_red[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;

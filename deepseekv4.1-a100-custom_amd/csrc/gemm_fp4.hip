@@ -17,20 +17,6 @@
 //                      every selected expert's w2 is read once. Optional epilogue: bf16(y + shared-expert ys).
 #include "common.h"
 
-// ------------------------------------------------------------------------------------------ weight tiles
-// Byte offset of lane `lane`'s 16 weight bytes for 16-row block nb, k-chunk kc (128 k), and of its scale byte.
-// Lane l: row nb*16 + l%16, k [kc*128 + 32*(l/16), +32).
-template <int TILED>
-__device__ __forceinline__ long long wtile_off(int nb, int kc, int nk, int Kh, int lane) {
-    if (TILED) return ((long long)nb * nk + kc) * 1024 + (lane & 15) * 64 + (lane >> 4) * 16;   // quant.py:118-122
-    return ((long long)nb * 16 + (lane & 15)) * Kh + kc * 64 + (lane >> 4) * 16;
-}
-template <int TILED>
-__device__ __forceinline__ long long stile_off(int nb, int kc, int nk, int Ks, int lane) {
-    if (TILED) return ((long long)nb * nk + kc) * 64 + (lane & 15) * 4 + (lane >> 4);           // quant.py:130-134
-    return ((long long)nb * 16 + (lane & 15)) * Ks + kc * 4 + (lane >> 4);
-}
-
 __device__ __forceinline__ v8i widen(v4i a) { return v8i{a.x, a.y, a.z, a.w, 0, 0, 0, 0}; }
 __device__ __forceinline__ v8i join(v4i a, v4i b) { return v8i{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}; }
 
@@ -46,22 +32,62 @@ struct GroupedArgs {
     const float* pair_wt;                    // optional per-pair factor
     int shard_start, shard_n, zero_out, min_tok, max_tok, vec_store;
     int accum;                               // 0 store, 1 add (distinct rows), 2 atomic add (rows may repeat)
+    int lds_rows;                            // B_LDS: activation rows staged per pass (<= 16)
+    // B_LDS only: bf16 activations on the FP8 grid, quantised to E4M3 + E8M0 while staging (xc / xs unused)
+    const uint16_t* xbf; long long ldxb;
+    // fused SwiGLU epilogue (cnt != null): the last workgroup of group g turns the group's gate/up rows of out
+    // into h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) codes (fused.py:284-306); cnt[g] is reset to 0
+    int* cnt; const float* sw_wt; float limit; int inter;
+    uint8_t* hc; long long ldhc; uint8_t* hs; long long ldhs;
 };
 
-template <int NCH, int TILED, int PF>
+// SwiGLU + routing weight + bf16 + per-32 FP8 for rows [p0, p1) of gu (one 32-lane half-wave per 32 columns)
+__device__ __forceinline__ void swiglu_rows(const float* gu, long long ld_gu, const float* wt, int p0, int p1, int inter, float limit,
+                                            uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs) {
+    const int lane = threadIdx.x & 31, hw = threadIdx.x >> 5, nhw = blockDim.x >> 5;
+    const int gpr = inter >> 5;
+    for (int idx = hw; idx < (p1 - p0) * gpr; idx += nhw) {
+        const int r = p0 + idx / gpr;
+        const int c = (idx % gpr) * 32 + lane;
+        float g = __builtin_nontemporal_load(gu + (long long)r * ld_gu + c);
+        float u = __builtin_nontemporal_load(gu + (long long)r * ld_gu + inter + c);
+        if (limit > 0.f) {
+            u = fminf(fmaxf(u, -limit), limit);
+            g = fminf(g, limit);
+        }
+        float h = g * (1.0f / (1.0f + expf(-g))) * u;
+        if (wt) h = h * wt[r];
+        h = bf16_round(h);
+        const int e = fq8_exponent(wave_max32(fabsf(h)));
+        hc[(long long)r * ldhc + c] = (uint8_t)fq8_code(h, e);
+        if (lane == 0) hs[(long long)r * ldhs + (c >> 5)] = (uint8_t)(e + 127);
+    }
+}
+
+// LDS row stride for staged activation codes: +16 bytes so 16 rows fall in different banks
+__device__ __forceinline__ int lds_stride(int K) { return K + 16; }
+
+// One wave = one (group, 16-row block); 4 waves per workgroup on consecutive row blocks of one group. A pass
+// covers up to 16 pairs of the group (one MFMA column each); larger groups take several passes.
+// B_LDS: the pass's activation rows are staged once per workgroup in LDS and read from there, so the vector
+// memory queue holds only weight tiles (PF in flight per wave); otherwise B is read from global memory
+// (L1/L2-resident) with non-divergent loads. Lanes whose column has no pair read row 0: their output
+// column is never stored.
+template <int TILED, int PF, int B_LDS, int NKC>
 __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = blockIdx.x * 4 + wave;
     const int g = blockIdx.y;
-    if (nb * 16 >= a.N) return;
+    const bool active = nb * 16 < a.N;
     const int p0 = a.grp_start[g], p1 = a.grp_start[g + 1];
     const int m = p1 - p0;
-    if (m <= 0 || m < a.min_tok || m > a.max_tok) return;
+    if (m <= 0 || m < a.min_tok || m > a.max_tok) return;       // uniform over the workgroup
     const int col = lane & 15, kb = lane >> 4;
     const int row0 = nb * 16 + 4 * kb;   // this lane's 4 output rows
     const int e = a.grp_expert[g] - a.shard_start;
     if (e < 0 || e >= a.shard_n) {       // another GPU's expert (cukern.py:244-246): skip, optionally zero
-        if (a.zero_out && a.accum == 0)
+        if (active && a.zero_out && a.accum == 0)
             for (int q = p0 + col; q < p1; q += 16) {
                 const long long orow = a.out_row ? a.out_row[q] : q;
 #pragma unroll
@@ -69,71 +95,98 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
             }
         return;
     }
-    const int nk = a.K >> 7, Kh = a.K >> 1, Ks = a.K >> 5;
-    const uint8_t* wbase = a.W + (long long)e * a.stride_we;
-    const uint8_t* sbase = a.S + (long long)e * a.stride_se;
-    const long long w0 = wtile_off<TILED>(nb, 0, nk, Kh, lane), ws = TILED ? 1024 : 64;
-    const long long s0 = stile_off<TILED>(nb, 0, nk, Ks, lane), ss = TILED ? 64 : 4;
+    const int K = a.K, nk = K >> 7, Kh = K >> 1, Ks = K >> 5;
+    const uint8_t* wl = a.W + (long long)e * a.stride_we + wtile_off<TILED>(nb, 0, nk, Kh, lane);
+    const uint8_t* sl = a.S + (long long)e * a.stride_se + stile_off<TILED>(nb, 0, nk, Ks, lane);
+    const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
+    const int LS = lds_stride(K);
+    uint8_t* lds_s = smem + (size_t)a.lds_rows * LS;
 
-    for (int base = p0; base < p1; base += 16 * NCH) {
-        const uint8_t* xp[NCH];
-        const uint8_t* xsp[NCH];
-        bool ok[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int q = base + c * 16 + col;
-            ok[c] = q < p1;
-            const long long r = ok[c] ? a.pair_tok[q] : 0;
-            xp[c] = a.xc + r * a.ldx + kb * 16;
-            xsp[c] = a.xs + r * a.ldxs + kb;
-        }
-        v4f acc[NCH];
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
-
-        v4i A[PF];
-        int SA[PF];
-        v4i B0[NCH][PF], B1[NCH][PF];
-        int SB[NCH][PF];
+    const int PW = B_LDS ? a.lds_rows : 16;   // pairs per pass: never more rows than the LDS holds
+    v4i A[PF];
+    int SA[PF];
+    v4i B0[B_LDS ? 1 : PF], B1[B_LDS ? 1 : PF];
+    int SB[B_LDS ? 1 : PF];
+    for (int base = p0; base < p1; base += PW) {
+        const int mp = min(PW, p1 - base);
+        const int brow = col < mp ? col : 0;
+        const uint8_t* xg = a.xc + (long long)a.pair_tok[base + brow] * a.ldx + kb * 16;
+        const uint8_t* xsg = a.xs + (long long)a.pair_tok[base + brow] * a.ldxs + kb;
+        const uint8_t* xl = smem + brow * LS + kb * 16;
+        const uint8_t* xsl = lds_s + brow * Ks + kb;
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
         auto load = [&](int slot, int kc) {
-            A[slot] = __builtin_nontemporal_load((const v4i*)(wbase + w0 + kc * ws));
-            SA[slot] = sbase[s0 + kc * ss];
-#pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                if (ok[c]) {
-                    const uint8_t* p = xp[c] + kc * 128;
-                    B0[c][slot] = *(const v4i*)p;
-                    B1[c][slot] = *(const v4i*)(p + 64);
-                    SB[c][slot] = xsp[c][kc * 4];
-                } else {
-                    B0[c][slot] = v4i{0, 0, 0, 0};
-                    B1[c][slot] = v4i{0, 0, 0, 0};
-                    SB[c][slot] = 127;
-                }
+            A[slot] = load_weight_tile(wl + (long long)kc * ws);
+            SA[slot] = sl[(long long)kc * ss];
+            if (!B_LDS) {
+                B0[slot] = *(const v4i*)(xg + kc * 128);
+                B1[slot] = *(const v4i*)(xg + kc * 128 + 64);
+                SB[slot] = xsg[kc * 4];
             }
         };
+        auto use = [&](int slot) {
+            // B_LDS reads the k-chunk of this slot by counter: slots are consumed in k order
+            if (B_LDS) {
+                const v4i b0 = *(const v4i*)(xl);
+                const v4i b1 = *(const v4i*)(xl + 64);
+                const int sb = *xsl;
+                xl += 128;
+                xsl += 4;
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
+            } else {
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
+            }
+        };
+        // the first weight tiles go out before the activations are staged: staging overlaps their latency
+        if (active) pipeline_start<PF>(nk, load);
+        if (B_LDS) {
+            __syncthreads();
+            if (a.xbf) {
+                // stage rows base .. base+mp-1 from bf16, one thread per 32-element group: E4M3 codes + E8M0
+                for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
+                    const int r = i / Ks, v = i - r * Ks;
+                    const uint16_t* src = a.xbf + (long long)a.pair_tok[base + r] * a.ldxb + v * 32;
+                    v4i raw[4];
 #pragma unroll
-        for (int i = 0; i < PF; ++i)
-            if (i < nk) load(i, i);
-        for (int k0 = 0; k0 < nk; k0 += PF) {
+                    for (int j = 0; j < 4; ++j) raw[j] = ((const v4i*)src)[j];
+                    const uint16_t* hv = (const uint16_t*)raw;
+                    float amax = 0.f;
 #pragma unroll
-            for (int i = 0; i < PF; ++i) {
-                const int kc = k0 + i;
-                if (kc < nk) {
-                    const v8i av = widen(A[i]);
+                    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(hv[j])));
+                    const int e = fq8_exponent(amax);
+                    uint32_t w[8];
 #pragma unroll
-                    for (int c = 0; c < NCH; ++c) acc[c] = mfma_fp4w_fp8x(av, join(B0[c][i], B1[c][i]), acc[c], SA[i], SB[c][i]);
-                    if (kc + PF < nk) load(i, kc + PF);
+                    for (int j = 0; j < 8; ++j) {
+                        w[j] = 0;
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) w[j] |= fq8_code(bf16_to_f32(hv[4 * j + b]), e) << (8 * b);
+                    }
+                    *(v4i*)(smem + r * LS + v * 32) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+                    *(v4i*)(smem + r * LS + v * 32 + 16) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+                    lds_s[r * Ks + v] = (uint8_t)(e + 127);
+                }
+            } else {
+                // stage rows base .. base+mp-1: codes as 16-byte vectors, then the E8M0 bytes
+                const int vpr = K >> 4;
+                for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
+                    const int r = i / vpr, v = i - r * vpr;
+                    const long long src = (long long)a.pair_tok[base + r] * a.ldx + v * 16;
+                    *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.xc + src);
+                }
+                for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
+                    const int r = i / Ks, v = i - r * Ks;
+                    lds_s[r * Ks + v] = a.xs[(long long)a.pair_tok[base + r] * a.ldxs + v];
                 }
             }
+            __syncthreads();
         }
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            if (!ok[c]) continue;
-            const int q = base + c * 16 + col;
+        if (!active) continue;
+        pipeline_finish<PF>(nk, load, use);
+        if (col < mp) {
+            const int q = base + col;
             const float f = a.pair_wt ? a.pair_wt[q] : 1.f;
             float* o = a.out + (a.out_row ? (long long)a.out_row[q] : (long long)q) * a.ldo + row0;
-            const v4f v = acc[c] * f;
+            const v4f v = acc * f;
             if (a.accum == 2) {
                 atomicAdd(o + 0, v.x); atomicAdd(o + 1, v.y); atomicAdd(o + 2, v.z); atomicAdd(o + 3, v.w);
             } else if (a.accum == 1) {
@@ -145,6 +198,22 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
             }
         }
     }
+    if (a.cnt) {
+        // completion count of group g over its gridDim.x workgroups; the last one runs the SwiGLU epilogue
+        // (release: every workgroup's gate/up stores are made visible before its increment; acquire: the last
+        // workgroup fences after observing the final count). The count is reset for the next launch.
+        __shared__ int s_last;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();
+            s_last = atomicAdd(a.cnt + g, 1) == (int)gridDim.x - 1;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
+        swiglu_rows(a.out, a.ldo, a.sw_wt, p0, p1, a.inter, a.limit, a.hc, a.ldhc, a.hs, a.ldhs);
+        if (threadIdx.x == 0) atomicExch(a.cnt + g, 0);
+    }
 }
 
 // ------------------------------------------------------------------------------------------ decode w2 + sum
@@ -152,8 +221,9 @@ struct DownSumArgs {
     const uint8_t* W; long long stride_we;
     const uint8_t* S; long long stride_se;
     int N, K;                                 // N = hidden (output rows), K = intermediate
-    const uint8_t* hc; long long ldh;         // FP8 codes of h, pairs in expert-sorted order
+    const uint8_t* hc; long long ldh;         // FP8 codes of h, pairs in expert-sorted order; row `zero_row` is 0
     const uint8_t* hs; long long ldhs;
+    int zero_row;                             // an all-zero row of hc / hs (absent token columns read it)
     const int* grp_expert; const int* grp_start; const int* tok_sorted;
     int n_slots;                              // group slots to scan (= pairs); unused slots have expert -1
     int M;                                    // tokens (<= 16)
@@ -164,84 +234,106 @@ struct DownSumArgs {
 };
 
 #define DS_MAX_SLOTS 256
+#define DS_WAVES 8
 
-template <int TILED, int PF>
-__global__ void __launch_bounds__(256) moe_down_sum_kernel(const DownSumArgs a) {
-    __shared__ int s_exp[DS_MAX_SLOTS];
+// One workgroup per 16-row block of the output; its 8 waves split the selected experts (group slots g = wave,
+// wave + 8, ...), each accumulating sum over its experts and k of W2[e] . h in one MFMA accumulator whose
+// column t is token t; a token absent from a group reads the zero row. The partial accumulators are summed in
+// a fixed order through LDS. The (group, k-chunk) space of a wave is flattened so the weight pipeline runs
+// across expert boundaries. H_LDS: all h rows (+ the zero row) are staged in LDS, so the vector memory queue
+// holds only weight tiles.
+template <int TILED, int PF, int NKC, int H_LDS>
+__global__ void __launch_bounds__(DS_WAVES * 64) moe_down_sum_kernel(const DownSumArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ short s_exp[DS_MAX_SLOTS];
     __shared__ short s_pair[DS_MAX_SLOTS][16];
-    __shared__ int s_ngroups;
-    __shared__ v4f s_red[4][64];
+    __shared__ short s_we[DS_WAVES][DS_MAX_SLOTS / DS_WAVES + 1];        // per wave: expert of its j-th group
+    __shared__ short s_wq[DS_WAVES][DS_MAX_SLOTS / DS_WAVES + 1][16];    // per wave: pair row of token t in it
+    __shared__ int s_cnt[DS_WAVES];
+    __shared__ v4f s_red[DS_WAVES][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = blockIdx.x;
-    // per-group table: expert (shard-local, -1 = skip) and, per token column, the group's pair (-1 = none)
-    if (threadIdx.x == 0) s_ngroups = 0;
-    __syncthreads();
+    const int K = a.K, Ks = K >> 5, LS = K + 16;
     for (int g = threadIdx.x; g < a.n_slots; g += blockDim.x) {
         const int ge = a.grp_expert[g];
         int e = ge < 0 ? -1 : ge - a.shard_start;
         if (e >= a.shard_n) e = -1;
-        s_exp[g] = e;
+        s_exp[g] = (short)e;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) s_pair[g][t] = -1;
-        if (ge >= 0) {
-            atomicMax(&s_ngroups, g + 1);
+        for (int t = 0; t < 16; ++t) s_pair[g][t] = (short)a.zero_row;
+        if (e >= 0)
             for (int q = a.grp_start[g]; q < a.grp_start[g + 1]; ++q) s_pair[g][a.tok_sorted[q] & 15] = (short)q;
+    }
+    if (H_LDS) {  // rows 0 .. zero_row of h (codes, 16-byte vectors) and their E8M0 bytes
+        uint8_t* hs_l = smem + (size_t)(a.zero_row + 1) * LS;
+        const int vpr = K >> 4;
+        for (int i = threadIdx.x; i < (a.zero_row + 1) * vpr; i += blockDim.x) {
+            const int r = i / vpr, v = i - r * vpr;
+            *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.hc + (long long)r * a.ldh + v * 16);
+        }
+        for (int i = threadIdx.x; i < (a.zero_row + 1) * Ks; i += blockDim.x) {
+            const int r = i / Ks, v = i - r * Ks;
+            hs_l[r * Ks + v] = a.hs[(long long)r * a.ldhs + v];
         }
     }
     __syncthreads();
-    const int G = s_ngroups;
-    const int col = lane & 15, kb = lane >> 4;
-    const int nk = a.K >> 7, Kh = a.K >> 1, Ks = a.K >> 5;
-    const long long w0 = wtile_off<TILED>(nb, 0, nk, Kh, lane), ws = TILED ? 1024 : 64;
-    const long long s0 = stile_off<TILED>(nb, 0, nk, Ks, lane), ss = TILED ? 64 : 4;
-
-    // this wave's iteration space: groups g = wave, wave + 4, ... (valid ones) x k-chunks, flattened so the
-    // load pipeline runs across group boundaries
-    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-    v4i A[PF], B0[PF], B1[PF];
-    int SA[PF], SB[PF];
-    int lg = wave, lkc = 0;                   // load cursor: group slot, k-chunk
-    while (lg < G && s_exp[lg] < 0) lg += 4;
-    auto load = [&](int slot) {
-        const int e = s_exp[lg];
-        const int q = s_pair[lg][col];
-        A[slot] = __builtin_nontemporal_load((const v4i*)(a.W + (long long)e * a.stride_we + w0 + lkc * ws));
-        SA[slot] = a.S[(long long)e * a.stride_se + s0 + lkc * ss];
-        if (q >= 0) {
-            const uint8_t* p = a.hc + (long long)q * a.ldh + lkc * 128 + kb * 16;
-            B0[slot] = *(const v4i*)p;
-            B1[slot] = *(const v4i*)(p + 64);
-            SB[slot] = a.hs[(long long)q * a.ldhs + lkc * 4 + kb];
-        } else {
-            B0[slot] = v4i{0, 0, 0, 0};
-            B1[slot] = v4i{0, 0, 0, 0};
-            SB[slot] = 127;
-        }
-        if (++lkc == nk) {
-            lkc = 0;
-            lg += 4;
-            while (lg < G && s_exp[lg] < 0) lg += 4;
-        }
-    };
-    int total = 0;
-    for (int g = wave; g < G; g += 4) total += s_exp[g] >= 0 ? nk : 0;
+    if (lane == 0) {  // this wave's valid groups, in slot order
+        int c = 0;
+        for (int g = wave; g < a.n_slots; g += DS_WAVES)
+            if (s_exp[g] >= 0) {
+                s_we[wave][c] = s_exp[g];
 #pragma unroll
-    for (int i = 0; i < PF; ++i)
-        if (i < total) load(i);
-    for (int k0 = 0; k0 < total; k0 += PF) {
-#pragma unroll
-        for (int i = 0; i < PF; ++i) {
-            const int it = k0 + i;
-            if (it < total) {
-                acc = mfma_fp4w_fp8x(widen(A[i]), join(B0[i], B1[i]), acc, SA[i], SB[i]);
-                if (it + PF < total) load(i);
+                for (int t = 0; t < 16; ++t) s_wq[wave][c][t] = s_pair[g][t];
+                ++c;
             }
-        }
+        s_cnt[wave] = c;
     }
+    __syncthreads();
+    const int col = lane & 15, kb = lane >> 4;
+    const int nk = NKC > 0 ? NKC : (K >> 7), Kh = K >> 1;
+    const long long w0 = wtile_off<TILED>(nb, 0, nk, Kh, lane), s0 = stile_off<TILED>(nb, 0, nk, Ks, lane);
+    const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
+    const int total = s_cnt[wave] * nk;
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    v4i A[PF], B0[H_LDS ? 1 : PF], B1[H_LDS ? 1 : PF];
+    int SA[PF], SB[H_LDS ? 1 : PF];
+    int uit = 0;   // consume-side iteration (H_LDS reads B when the slot is consumed)
+    const uint8_t* hs_l = smem + (size_t)(a.zero_row + 1) * LS;
+    // flattened (group, k-chunk) iteration: addresses computed without branches so the pipeline stays exact
+    pipelined<PF>(total,
+        [&](int slot, int it) {
+            const int j = it / nk, kc = it - j * nk;
+            const long long e = s_we[wave][j];
+            A[slot] = load_weight_tile(a.W + e * a.stride_we + w0 + (long long)kc * ws);
+            SA[slot] = a.S[e * a.stride_se + s0 + (long long)kc * ss];
+            if (!H_LDS) {
+                const long long q = s_wq[wave][j][col];
+                const uint8_t* hb = a.hc + q * a.ldh + kc * 128 + kb * 16;
+                B0[slot] = *(const v4i*)hb;
+                B1[slot] = *(const v4i*)(hb + 64);
+                SB[slot] = a.hs[q * a.ldhs + kc * 4 + kb];
+            }
+        },
+        [&](int slot) {
+            if (H_LDS) {
+                const int j = uit / nk, kc = uit - j * nk;
+                ++uit;
+                const int q = s_wq[wave][j][col];
+                const uint8_t* hb = smem + q * LS + kc * 128 + kb * 16;
+                const v4i b0 = *(const v4i*)hb;
+                const v4i b1 = *(const v4i*)(hb + 64);
+                const int sb = hs_l[q * Ks + kc * 4 + kb];
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
+            } else {
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
+            }
+        });
     s_red[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
-    const v4f sum = ((s_red[0][lane] + s_red[1][lane]) + s_red[2][lane]) + s_red[3][lane];
+    v4f sum = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < DS_WAVES; ++w) sum += s_red[w][lane];
     if (col >= a.M) return;
     const int row0 = nb * 16 + 4 * kb;
     if (a.y) {
@@ -249,7 +341,7 @@ __global__ void __launch_bounds__(256) moe_down_sum_kernel(const DownSumArgs a) 
         o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
     }
     if (a.yb) {
-        float v[4] = {sum.x, sum.y, sum.z, sum.w};
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float t = v[i];
@@ -260,11 +352,13 @@ __global__ void __launch_bounds__(256) moe_down_sum_kernel(const DownSumArgs a) 
 }
 
 // ------------------------------------------------------------------------------------------ C ABI
-template <int NCH, int TILED>
-static void launch_grouped(const GroupedArgs& a, int G, hipStream_t st) {
+#define B_LDS_MAX_BYTES (48 * 1024)
+
+template <int TILED, int B_LDS>
+static void launch_grouped(const GroupedArgs& a, int G, size_t lds, hipStream_t st) {
     dim3 grid((unsigned)((a.N / 16 + 3) / 4), (unsigned)G);
-    constexpr int PF = NCH == 1 ? 8 : (NCH == 2 ? 4 : 2);
-    fp4_grouped_kernel<NCH, TILED, PF><<<grid, 256, 0, st>>>(a);
+    constexpr int PF = B_LDS ? DSV41_PF_UP : 8;
+    fp4_grouped_kernel<TILED, PF, B_LDS, 0><<<grid, 256, lds, st>>>(a);
 }
 
 extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
@@ -274,32 +368,73 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
                                       int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream) {
     if (!W || !S || !xc || !xs || !grp_expert || !grp_start || !pair_tok || !out) return DSV41_EINVAL;
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || G < 0 || ldo < N || ldx < K || ldxs < K / 32 || max_tokens < 1) return DSV41_EINVAL;
-    if (accum < 0 || accum > 2) return DSV41_EINVAL;
+    if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15)) return DSV41_EINVAL;
     if (G == 0) return 0;
     GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, grp_expert, grp_start, pair_tok, out, ldo, out_row, pair_wt,
-                  shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum};
+                  shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0,
+                  nullptr, 0, nullptr, nullptr, 0.f, 0, nullptr, 0, nullptr, 0};
     a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
-    const int nch = max_tokens <= 16 ? 1 : (max_tokens <= 32 ? 2 : 4);
+    const int rows = max_tokens < 16 ? max_tokens : 16;
+    const size_t lds = (size_t)rows * (K + 16) + (size_t)rows * (K / 32);
+    const bool use_lds = lds <= B_LDS_MAX_BYTES;
+    a.lds_rows = use_lds ? rows : 0;
     if (tiled) {
-        if (nch == 1) launch_grouped<1, 1>(a, G, st); else if (nch == 2) launch_grouped<2, 1>(a, G, st); else launch_grouped<4, 1>(a, G, st);
+        if (use_lds) launch_grouped<1, 1>(a, G, lds, st); else launch_grouped<1, 0>(a, G, 0, st);
     } else {
-        if (nch == 1) launch_grouped<1, 0>(a, G, st); else if (nch == 2) launch_grouped<2, 0>(a, G, st); else launch_grouped<4, 0>(a, G, st);
+        if (use_lds) launch_grouped<0, 1>(a, G, lds, st); else launch_grouped<0, 0>(a, G, 0, st);
     }
     return (int)hipGetLastError();
 }
 
+extern "C" int dsv41_moe_up_swiglu(const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se, int tiled,
+                                   int N, int K, int E, const uint16_t* x, long long ldx, const int* grp_expert, const int* grp_start,
+                                   int G, const int* pair_tok, int max_tokens, float* gu, long long ldgu, int* counters, const float* wt,
+                                   float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs, void* stream) {
+    if (!W13 || !S13 || !x || !grp_expert || !grp_start || !pair_tok || !gu || (counters && (!hc || !hs || !wt))) return DSV41_EINVAL;
+    if (N <= 0 || (N & 63) || K <= 0 || (K & 127) || G < 0 || ldgu < N || ldx < K || (ldx & 7) || (((uintptr_t)x) & 15) ||
+        max_tokens < 1 || E < 1)
+        return DSV41_EINVAL;
+    if (G == 0) return 0;
+    const int inter = N / 2;
+    GroupedArgs a{W13, stride_we, S13, stride_se, N, K, nullptr, 0, nullptr, 0, grp_expert, grp_start, pair_tok, gu, ldgu, nullptr, nullptr,
+                  0, E, 0, 0, 1 << 30, 0, 0, 0,   // expert ids outside [0, E) are skipped, never dereferenced
+                  x, ldx, counters, wt, limit, inter, hc, ldhc, hs, ldhs};
+    a.vec_store = ((ldgu & 3) == 0 && (((uintptr_t)gu) & 15) == 0) ? 1 : 0;
+    // activation rows staged per pass: as many as fit in 64 KiB of LDS (<= 16)
+    const size_t row_bytes = (size_t)(K + 16) + (size_t)(K / 32);
+    int rows = (int)((64 * 1024) / row_bytes);
+    rows = rows > 16 ? 16 : rows;
+    rows = rows > max_tokens ? max_tokens : rows;
+    if (rows < 1) return DSV41_EINVAL;
+    a.lds_rows = rows;
+    hipStream_t st = (hipStream_t)stream;
+    if (tiled) launch_grouped<1, 1>(a, G, rows * row_bytes, st); else launch_grouped<0, 1>(a, G, rows * row_bytes, st);
+    return (int)hipGetLastError();
+}
+
 extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
-                                  int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs,
+                                  int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                                   const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                                   float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                                   int shard_start, int shard_n, void* stream) {
     if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb)) return DSV41_EINVAL;
-    if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16) return DSV41_EINVAL;
-    DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, grp_expert, grp_start, tok_sorted, n_slots, M,
+    if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0) return DSV41_EINVAL;
+    if ((ldh & 15) || (((uintptr_t)hc) & 15)) return DSV41_EINVAL;
+    DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n};
     hipStream_t st = (hipStream_t)stream;
-    if (tiled) moe_down_sum_kernel<1, 8><<<N / 16, 256, 0, st>>>(a);
-    else moe_down_sum_kernel<0, 8><<<N / 16, 256, 0, st>>>(a);
+    const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
+    const bool h_lds = lds <= 32 * 1024;
+    const dim3 grid(N / 16), block(DS_WAVES * 64);
+#define DS_LAUNCH(T, PF, NK, HL) moe_down_sum_kernel<T, PF, NK, HL><<<grid, block, HL ? lds : 0, st>>>(a)
+    if (K == 1664) {   // the decode shape: k-chunk count known at compile time
+        if (h_lds) { if (tiled) DS_LAUNCH(1, 13, 13, 1); else DS_LAUNCH(0, 13, 13, 1); }
+        else { if (tiled) DS_LAUNCH(1, 8, 13, 0); else DS_LAUNCH(0, 8, 13, 0); }
+    } else {
+        if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1); else DS_LAUNCH(0, 12, 0, 1); }
+        else { if (tiled) DS_LAUNCH(1, 8, 0, 0); else DS_LAUNCH(0, 8, 0, 0); }
+    }
+#undef DS_LAUNCH
     return (int)hipGetLastError();
 }

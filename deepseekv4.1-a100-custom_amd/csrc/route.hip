@@ -9,97 +9,33 @@
 // p2p.cu:91-93; a stable order makes the tables reproducible). Rounds of blockDim pairs; within a wave the rank
 // among same-expert lanes comes from ballots, across waves from per-wave counts in LDS.
 #include "common.h"
+#include "gate.h"
 
-#define GATE_THREADS 256
-#define GATE_MAX_E 2048
+#define GATE_MAX_PER_LANE 32   // E <= 2048 scores per row, held in registers (32 per lane)
 
-__device__ __forceinline__ void argmax_pair(float& v, int& i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
-}
-
-__global__ void __launch_bounds__(GATE_THREADS) gate_topk_kernel(const float* __restrict__ scores, long long lds, const float* __restrict__ bias,
-                                                                 int E, float temp, int topk, float route_scale, int mode, int norm,
-                                                                 int* __restrict__ eid, float* __restrict__ wt) {
-    __shared__ float s_s[GATE_MAX_E], s_b[GATE_MAX_E];
-    __shared__ float s_rv[GATE_THREADS / WAVE];
-    __shared__ int s_ri[GATE_THREADS / WAVE];
-    __shared__ float s_w[32];
-    __shared__ int s_i[32];
-    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float* S = scores + (long long)row * lds;
-    // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440
-    float lmax = -INFINITY;
-    for (int e = tid; e < E; e += GATE_THREADS) {
-        const float s = S[e] / temp;
-        s_s[e] = s;
-        lmax = fmaxf(lmax, s);
-    }
-    __syncthreads();
-    if (mode == 2) {
-        for (int o = 32; o > 0; o >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, o));
-        if (lane == 0) s_rv[wave] = lmax;
-        __syncthreads();
-        float mx = s_rv[0];
-        for (int w = 1; w < GATE_THREADS / WAVE; ++w) mx = fmaxf(mx, s_rv[w]);
-        __syncthreads();
-        float lsum = 0.f;
-        for (int e = tid; e < E; e += GATE_THREADS) {
-            const float ex = expf(s_s[e] - mx);
-            s_s[e] = ex;
-            lsum += ex;
-        }
-        for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
-        if (lane == 0) s_rv[wave] = lsum;
-        __syncthreads();
-        float tot = 0.f;
-        for (int w = 0; w < GATE_THREADS / WAVE; ++w) tot += s_rv[w];
-        for (int e = tid; e < E; e += GATE_THREADS) s_s[e] = s_s[e] / tot;
-    } else {
-        for (int e = tid; e < E; e += GATE_THREADS) {
-            const float s = s_s[e];
-            s_s[e] = mode == 1 ? 1.0f / (1.0f + expf(-s)) : sqrtf(s > 20.f ? s : log1pf(expf(s)));
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += GATE_THREADS) s_b[e] = s_s[e] + (bias ? bias[e] : 0.f);
-    __syncthreads();
-    for (int k = 0; k < topk; ++k) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-        for (int e = tid; e < E; e += GATE_THREADS) argmax_pair(bv, bi, s_b[e], e);
-        for (int o = 32; o > 0; o >>= 1) {
-            const float v2 = __shfl_xor(bv, o);
-            const int i2 = __shfl_xor(bi, o);
-            argmax_pair(bv, bi, v2, i2);
-        }
-        if (lane == 0) { s_rv[wave] = bv; s_ri[wave] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            float v = s_rv[0];
-            int i = s_ri[0];
-            for (int w = 1; w < GATE_THREADS / WAVE; ++w) argmax_pair(v, i, s_rv[w], s_ri[w]);
-            s_i[k] = i;
-            s_w[k] = s_s[i];
-            s_b[i] = -INFINITY;
-        }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        float sum = 0.f;
-        for (int k = 0; k < topk; ++k) sum += s_w[k];
-        for (int k = 0; k < topk; ++k) {
-            eid[(long long)row * topk + k] = s_i[k];
-            wt[(long long)row * topk + k] = norm ? s_w[k] / (sum + 1e-20f) * route_scale : s_w[k] * route_scale;
-        }
+template <int PER>
+__global__ void __launch_bounds__(64) gate_topk_kernel(const float* __restrict__ scores, long long lds, const float* __restrict__ bias,
+                                                       int E, float temp, int topk, float route_scale, int mode, int norm,
+                                                       int* __restrict__ eid, float* __restrict__ wt) {
+    int ki;
+    float kw;
+    gate_row_wave<PER>(scores + (long long)blockIdx.x * lds, bias, E, temp, topk, route_scale, mode, norm, &ki, &kw);
+    if (threadIdx.x < topk) {
+        eid[(long long)blockIdx.x * topk + threadIdx.x] = ki;
+        wt[(long long)blockIdx.x * topk + threadIdx.x] = kw;
     }
 }
 
 extern "C" int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B, int E, float temp, int topk, float route_scale,
                                int score_func, int norm, int* eid, float* wt, void* stream) {
-    if (!scores || !eid || !wt || B < 0 || E < 1 || E > GATE_MAX_E || topk < 1 || topk > 32 || topk > E || score_func < 0 || score_func > 2 || lds < E)
+    if (!scores || !eid || !wt || B < 0 || E < 1 || E > 64 * GATE_MAX_PER_LANE || topk < 1 || topk > 64 || topk > E || score_func < 0 ||
+        score_func > 2 || lds < E)
         return DSV41_EINVAL;
     if (B == 0) return 0;
-    gate_topk_kernel<<<B, GATE_THREADS, 0, (hipStream_t)stream>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
+    hipStream_t st = (hipStream_t)stream;
+    if (E <= 64 * 4) gate_topk_kernel<4><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
+    else if (E <= 64 * 8) gate_topk_kernel<8><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
+    else gate_topk_kernel<GATE_MAX_PER_LANE><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
     return (int)hipGetLastError();
 }
 

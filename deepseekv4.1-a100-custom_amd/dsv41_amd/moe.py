@@ -1,15 +1,14 @@
 """The FP4 MoE expert path of one layer on MI355X: routed experts (decode, M <= 16 tokens), the bf16 shared
 expert, routing and the combine, as HIP kernels launched on torch's current stream.
 
-Decode (decode.py:316-372 experts_tc / moe2; model.py:554-591 MoE.__call__ for <= 16 tokens):
-  1. xq (bf16, FP8 grid) -> E4M3 codes + E8M0 per 32 (exact)                       quant_fp8 kernel
-  2. pairs bucketed by expert on the device (M > 1; M = 1 uses constant tables,
-     decode.py:304-314)                                                             moe_dispatch kernel
-  3. gu[p] = x[tok(p)] . deq(W13[e(p)])^T, each selected expert read once          grouped MFMA kernel
-  4. h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) as FP8 codes          swiglu_quant kernel
-     (routing weight folded in before rounding, fused.py:297-302)
-  5. y[t] = sum over t's experts of h . deq(W2)^T in one MFMA accumulator,
-     out = bf16(y + ys) (fused2.py:490-495)                                         moe_down_sum kernel
+Decode (decode.py:316-372 experts_tc / moe2; model.py:554-591 MoE.__call__ for <= 16 tokens), two launches:
+  1. dsv41_moe_decode_up: routing from the logits (gate_topk, fused2.py:418-452) or given ids / weights, the
+     (token, expert) pairs bucketed by expert (moe_dispatch order), xq (bf16 on the FP8 grid) re-encoded as
+     E4M3 + E8M0 in LDS (exact), gu = x . deq(W13[e])^T for 32 SwiGLU columns per workgroup and
+     h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) written as FP8 codes (routing weight folded in before
+     rounding, fused.py:297-302); gate/up never leave the chip
+  2. dsv41_moe_down_sum: y[t] = sum over t's experts of h . deq(W2)^T in one MFMA accumulator,
+     out = bf16(y + ys) (fused2.py:490-495)
 Only the selected experts' weight bytes are read from HBM.
 
 Workspaces are allocated once per (device, shape) and reused, so a captured graph replays without allocating.
@@ -21,9 +20,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .fused import swiglu_quant_codes
-from .hipkern import grouped_gemm_codes, moe_dispatch
-from .quant import quant_fp8_e8m0
+from .fused2 import _MODES
 
 
 @dataclass
@@ -67,21 +64,14 @@ class _Workspace:
         P = M * k
         u8, i32, f32 = torch.uint8, torch.int32, torch.float32
         self.M, self.k, self.P = M, k, P
-        self.xc = torch.empty(M, H, dtype=u8, device=dev)
-        self.xs = torch.empty(M, H // 32, dtype=u8, device=dev)
-        self.gu = torch.empty(P, 2 * I, dtype=f32, device=dev)
-        self.hc = torch.empty(P, I, dtype=u8, device=dev)
-        self.hs = torch.empty(P, I // 32, dtype=u8, device=dev)
+        # row P of hc / hs stays zero: the down projection reads it for tokens a group does not contain
+        self.hc = torch.zeros(P + 1, I, dtype=u8, device=dev)
+        self.hs = torch.zeros(P + 1, I // 32, dtype=u8, device=dev)
         self.y = torch.empty(M, H, dtype=f32, device=dev)
         self.tok_sorted = torch.empty(P, dtype=i32, device=dev)
         self.wt_sorted = torch.empty(P, dtype=f32, device=dev)
-        self.inv = torch.empty(P, dtype=i32, device=dev)
         self.grp_expert = torch.empty(P, dtype=i32, device=dev)
         self.grp_start = torch.empty(P + 1, dtype=i32, device=dev)
-        self.n_groups = torch.empty(1, dtype=i32, device=dev)
-        # M = 1: one group per pair, in pair order (decode.py:304-314)
-        self.const_start = torch.arange(P + 1, dtype=i32, device=dev)
-        self.const_tok = torch.zeros(P, dtype=i32, device=dev)
 
 
 _WS: dict = {}
@@ -95,42 +85,73 @@ def _workspace(dev, M, k, H, I) -> _Workspace:
     return ws
 
 
-def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
-                ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None) -> torch.Tensor:
-    """Routed experts of one layer for M <= 16 tokens.
-    xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int32 [M, k]; wt fp32 [M, k].
-    Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
-    or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None)."""
-    dev = _lib.require_cuda(xq, eid, wt)
+def _as(t: torch.Tensor, dtype) -> torch.Tensor:
+    t = t.reshape(-1)
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=None, eid=None, wt=None, eid_out=None, wt_out=None):
+    """The first of the two decode launches (dsv41_moe_decode_up): routing (from `logits` with gate = (bias,
+    temp, route_scale, score_func, norm), or the given eid / wt), bucketing, up projection and SwiGLU.
+    Returns the workspace holding h (codes + E8M0, expert-sorted pair rows) and the tables for decode_down."""
+    dev = _lib.require_cuda(xq, logits, eid, wt)
     M, H = xq.shape
-    k = eid.shape[-1]
     assert 1 <= M <= 16, "decode path: at most 16 tokens (use the prefill path beyond)"
-    assert H == ex.H and xq.dtype == torch.bfloat16
+    assert H == ex.H and xq.dtype == torch.bfloat16 and 1 <= k <= 16 and ex.E <= 512
+    if xq.stride(1) != 1 or xq.stride(0) % 8 or xq.data_ptr() % 16:
+        xq = xq.contiguous()
     ws = _workspace(dev, M, k, H, ex.I)
-    quant_fp8_e8m0(xq, codes=ws.xc, scales=ws.xs)
-    eid32 = eid.reshape(-1)
-    wt32 = wt.reshape(-1)
-    if eid32.dtype != torch.int32:
-        eid32 = eid32.to(torch.int32)
-    if wt32.dtype != torch.float32:
-        wt32 = wt32.float()
-    eid32 = eid32.contiguous()
-    wt32 = wt32.contiguous()
-    if M == 1:
-        grp_expert, grp_start, tok, wts = eid32, ws.const_start, ws.const_tok, wt32
+    if logits is not None:
+        bias, temp, route_scale, score_func, norm = gate
+        lg = logits if (logits.dtype == torch.float32 and logits.stride(-1) == 1) else logits.float().contiguous()
+        b = None if bias is None else _as(bias, torch.float32)
+        assert lg.shape[-1] == ex.E and (b is None or b.numel() == ex.E)
+        route = (_lib.ptr(lg), lg.stride(0), _lib.ptr(b), float(temp), float(route_scale), _MODES[score_func], 1 if norm else 0, None, None)
     else:
-        _lib.call("dsv41_moe_dispatch", _lib.ptr(eid32), _lib.ptr(wt32), ws.P, k, ex.E, 64, _lib.ptr(ws.tok_sorted), _lib.ptr(ws.wt_sorted),
-                  _lib.ptr(ws.inv), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.n_groups), _lib.stream(dev))
-        grp_expert, grp_start, tok, wts = ws.grp_expert, ws.grp_start, ws.tok_sorted, ws.wt_sorted
-    grouped_gemm_codes(ws.xc, ws.xs, ex.w13, ex.s13, grp_expert, grp_start, tok, ws.gu, M, ex.tiled)
-    swiglu_quant_codes(ws.gu, wts, ex.I, limit, codes=ws.hc, scales=ws.hs)
+        eid32, wt32 = _as(eid, torch.int32), _as(wt, torch.float32)
+        route = (None, ex.E, None, 1.0, 1.0, 0, 0, _lib.ptr(eid32), _lib.ptr(wt32))
+    _lib.call("dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
+              ex.s13.stride(0), 1 if ex.tiled else 0, H, ex.I, float(limit), _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0),
+              _lib.ptr(eid_out), _lib.ptr(wt_out), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.tok_sorted),
+              _lib.ptr(ws.wt_sorted), _lib.stream(dev))
+    return ws
+
+
+def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None):
+    """The second decode launch (dsv41_moe_down_sum): y[t] = sum over t's groups of h . deq(W2[e])^T (fp32, into
+    y32 or the workspace) and/or out = bf16(y + ys)."""
+    dev = _lib.require_cuda(ws.hc, ys, out, y32)
+    M, H = ws.M, ex.H
     y = ws.y if y32 is None else y32
     want_y = out is None or y32 is not None
     _lib.call("dsv41_moe_down_sum", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H, ex.I,
-              _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), _lib.ptr(grp_expert), _lib.ptr(grp_start), _lib.ptr(tok),
-              ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
-              _lib.ptr(out), H if out is None else out.stride(0), 0, 1 << 30, _lib.stream(dev))
+              _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), ws.P, _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start),
+              _lib.ptr(ws.tok_sorted), ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
+              _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.stream(dev))
     return out if out is not None else y
+
+
+def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
+                ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed experts of one layer for M <= 16 tokens with given routing.
+    xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int [M, k] (distinct per token); wt fp32 [M, k].
+    Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
+    or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None);
+    y32 (fp32 [M, H]) additionally receives y."""
+    ws = decode_up(xq, ex, limit, eid.shape[-1], eid=eid, wt=wt)
+    return decode_down(ws, ex, ys, out, y32)
+
+
+def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None, temp: float, topk: int, route_scale: float,
+                      score_func: str, norm: bool, ex: ExpertWeights, limit: float, ys: torch.Tensor | None = None,
+                      out: torch.Tensor | None = None, y32: torch.Tensor | None = None, eid_out: torch.Tensor | None = None,
+                      wt_out: torch.Tensor | None = None) -> torch.Tensor:
+    """gate_topk (fused2.py:418-452) fused into the routed experts: logits fp32 [M, E] -> routing (written to
+    eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts."""
+    ws = decode_up(xq, ex, limit, topk, logits=logits, gate=(bias, temp, route_scale, score_func, norm), eid_out=eid_out, wt_out=wt_out)
+    return decode_down(ws, ex, ys, out, y32)
 
 
 # --------------------------------------------------------------------------- dense bf16 (shared expert, router)
@@ -205,7 +226,6 @@ class MoEDecodeLayer:
         return b
 
     def __call__(self, x: torch.Tensor, logits: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-        from .fused2 import gate_topk
         dev = _lib.require_cuda(x)
         M, H = x.shape
         b = self._buf(dev, M)
@@ -215,13 +235,12 @@ class MoEDecodeLayer:
         if logits is None:
             assert self.router is not None, "router weights or logits are required"
             logits = dense_gemv(self.router, x, out=b["logits"])
-        gate_topk(logits, self.bias, self.temp, self.topk, self.route_scale, self.score_func, self.norm and self.topk > 1,
-                  eid=b["eid"], wt=b["wt"])
         ys = None
         if self.Ws13 is not None:
             ys = shared_expert(b["xq"], self.Ws13, self.Ws2, self.limit, ys=b["ys"])
         o = b["out"] if out is None else out
-        moe_experts(b["xq"], b["eid"], b["wt"], self.ex, self.limit, ys=ys, out=o)
+        moe_route_experts(b["xq"], logits, self.bias, self.temp, self.topk, self.route_scale, self.score_func, self.norm and self.topk > 1,
+                          self.ex, self.limit, ys=ys, out=o, eid_out=b["eid"], wt_out=b["wt"])
         return o
 
     @property

@@ -52,13 +52,44 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
                            float* out, long long ldo, const int* out_row, const float* pair_wt, int accum, int max_tokens,
                            int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
 
+/* Decode up projection with its epilogue fused: x bf16 [rows][ldx] on the FP8 grid (fake_quant_fp8 output) is
+ * quantised to E4M3 + E8M0 while staged in LDS, gu[p] = x[pair_tok[p]] . deq(W13[e_g])^T (fp32 [pairs][ldgu],
+ * N = 2 * inter rows: w1 then w3), and the last workgroup of each group writes h = fq8(bf16(wt[p] *
+ * silu(min(g, L)) * clamp(u, +-L))) as FP8 codes hc [pairs][ldhc] + E8M0 hs [pairs][ldhs]. E: experts in W13;
+ * groups whose expert id is outside [0, E) are skipped (their rows are not written). counters: int [G],
+ * zero before the first call; every call leaves them zero. counters = NULL: no epilogue (gu only). Replaces the w13 fp4_gemm_tc call and swiglu_quant
+ * of decode.DecodeRuntime.experts_tc (decode.py:316-335; cukern.py:238-276; fused.py:283-345). */
+int dsv41_moe_up_swiglu(const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se, int tiled,
+                        int N, int K, int E, const uint16_t* x, long long ldx, const int* grp_expert, const int* grp_start,
+                        int G, const int* pair_tok, int max_tokens, float* gu, long long ldgu, int* counters, const float* wt,
+                        float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs, void* stream);
+
+/* Decode routing + up projection + SwiGLU in one launch (M <= 16 tokens, topk <= 16, E <= 512):
+ * routing from fp32 logits [M][ldl] (gate_topk semantics, score_func 0 sqrt(softplus) / 1 sigmoid / 2 softmax;
+ * bias may be NULL) or, with logits = NULL, from given eid_in / wt_in [M][topk]; the (token, expert) pairs are
+ * bucketed by expert (groups in ascending expert id, tokens ascending inside a group); x bf16 [M][ldx] on the
+ * FP8 grid is quantised to E4M3 + E8M0 in LDS, and h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) of
+ * gu = x . deq(W13[e])^T (2 * I rows: w1 then w3) is written as FP8 codes hc [P][ldhc] + E8M0 hs [P][ldhs],
+ * P = M * topk pair slots in sorted order. Outputs for dsv41_moe_down_sum: grp_expert [P] (-1 past the last
+ * group), grp_start [P + 1], tok_sorted [P], wt_sorted [P]; routing eid_out / wt_out [M][topk] (optional).
+ * Expert ids outside [0, E) are dropped. Replaces gate_topk + moe_dispatch + the w13 fp4_gemm_tc + swiglu_quant
+ * of decode.DecodeRuntime.moe2 / experts_tc (decode.py:354-361, 316-335; fused2.py:418-452; cukern.py:238-276;
+ * fused.py:283-345; p2p.cu:90-132). */
+int dsv41_moe_decode_up(const float* logits, long long ldl, const float* bias, float temp, float route_scale, int score_func,
+                        int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
+                        long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
+                        int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
+                        int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
+                        void* stream);
+
 /* Decode down projection and per-token combine: y[t][n] = sum over groups g and their pair p of token t of
  * h_p . deq(W2[e_g])[n]  (M <= 16 tokens, n_slots <= 256 group slots; slots with expert -1 are unused).
+ * zero_row: index of an all-zero row of hc and hs (read for tokens a group does not contain).
  * Optional outputs: y fp32 [M][ldy]; yb bf16 = bf16(y + ys) with ys the bf16 shared-expert output or NULL.
  * Replaces the w2 call of decode.DecodeRuntime.experts_tc (decode.py:316-335) plus the sum of the k rows in
  * fused2.hc_post2_ (fused2.py:490-495) and model.MoE.__call__ (model.py:581, 590-591). */
 int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
-                       int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs,
+                       int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                        const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                        float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                        int shard_start, int shard_n, void* stream);

@@ -167,9 +167,19 @@ def test_gate_topk(func):
     ref_i, ref_w = O.gate_topk(sc, bias, 1.0, 8, 2.5, func, True)
     assert np.array_equal(eid.cpu().numpy(), ref_i)
     assert np.allclose(wt.cpu().numpy(), ref_w, rtol=2e-6, atol=0)
+    # without renormalisation the raw scores (softmax denominators included) are checked too
+    eid2, wt2 = fused2.gate_topk(torch.from_numpy(sc).to(DEV), torch.from_numpy(bias).to(DEV), 1.3, 8, 1.0, func, False)
+    ref_i2, ref_w2 = O.gate_topk(sc, bias, 1.3, 8, 1.0, func, False)
+    assert np.array_equal(eid2.cpu().numpy(), ref_i2)
+    assert np.allclose(wt2.cpu().numpy(), ref_w2, rtol=4e-6, atol=0)
     tied = torch.zeros(1, 64, device=DEV)
     e1, _ = fused2.gate_topk(tied, None, 1.0, 4, 1.0, "softmax", True)
     assert e1.tolist() == [0, 1, 2, 3]
+    # NaN scores never win and no index is ever out of range
+    nanrow = torch.full((1, 384), float("nan"), device=DEV)
+    nanrow[0, 7] = 1.0
+    e2, _ = fused2.gate_topk(nanrow, None, 1.0, 8, 1.0, "sigmoid", True)
+    assert e2[0].item() == 7 and int(e2.max()) < 384 and int(e2.min()) >= 0
 
 
 # ------------------------------------------------------------------------------------------ decode experts
@@ -187,6 +197,37 @@ def test_decode_experts_small(tiled, M, limit):
     y = moe.moe_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, limit)
     ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, *[w.cpu().numpy() for w in ws], I, limit)
     close(y.cpu().numpy(), ref, f"decode small M={M} tiled={tiled} L={limit}")
+
+
+@pytest.mark.parametrize("M,func,norm", [(1, "softmax", True), (3, "sigmoid", True), (16, "sqrtsoftplus", True), (5, "softmax", False)])
+def test_decode_up_routing_and_tables(M, func, norm):
+    """The fused decode entry routes from the logits: its ids / weights equal the standalone gate kernel's (the
+    same device code) and the oracle's, its bucketing tables equal moe_dispatch's exactly (one group per
+    expert), and the layer output matches the oracle."""
+    from dsv41_amd import fused2, moe, quant
+    E, H, I, k = 384, 512, 128, 8
+    ws = make_experts(E, H, I, 300 + M)
+    ex = to_ex(*ws, True)
+    rng = np.random.default_rng(M)
+    logits = (rng.standard_normal((M, E)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    lg, bs = torch.from_numpy(logits).to(DEV), torch.from_numpy(bias).to(DEV)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 7 + M).to(DEV))
+    eo = torch.full((M, k), -7, dtype=torch.int32, device=DEV)
+    wo = torch.empty(M, k, device=DEV)
+    y = moe.moe_route_experts(xq, lg, bs, 1.0, k, 2.5, func, norm, ex, 10.0, eid_out=eo, wt_out=wo)
+    ge_i, ge_w = fused2.gate_topk(lg, bs, 1.0, k, 2.5, func, norm, eid=torch.empty_like(eo), wt=torch.empty_like(wo))
+    assert torch.equal(eo, ge_i) and torch.equal(wo, ge_w)
+    eid, wt = O.gate_topk(logits, bias, 1.0, k, 2.5, func, norm)
+    assert np.array_equal(eo.cpu().numpy(), eid)
+    assert np.allclose(wo.cpu().numpy(), wt, rtol=4e-6, atol=0)
+    w_dev = wo.cpu().numpy()
+    tok, wts, _, g_e, g_s, _ = O.moe_dispatch(eid, w_dev, k, E, 16)
+    wsp = moe._WS[(DEV, M, k, H, I)]
+    for got, ref in ((wsp.tok_sorted, tok), (wsp.wt_sorted, wts), (wsp.grp_expert, g_e), (wsp.grp_start, g_s)):
+        assert np.array_equal(got.cpu().numpy(), ref)
+    ref = O.moe_layer_routed(bf16_vals(xq), eid, w_dev, *[w.cpu().numpy() for w in ws], I, 10.0)
+    close(y.cpu().numpy(), ref, f"decode routed from logits M={M} {func}")
 
 
 @pytest.fixture(scope="module")
@@ -281,6 +322,7 @@ def test_graph_capture_replay(full_layer):
     ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
     out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
     s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())           # inputs were produced on the current stream
     with torch.cuda.stream(s):
         moe.moe_experts(xq, ed, wd, ex, 10.0, out=out)   # warm-up (workspaces allocated outside capture)
     torch.cuda.synchronize()
