@@ -144,6 +144,18 @@ __device__ __forceinline__ float wave_reduce_sum(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 63));
 }
 
+__device__ __forceinline__ unsigned umax2(unsigned a, unsigned b) { return a > b ? a : b; }
+__device__ __forceinline__ unsigned wave_reduce_max_u32(unsigned x) {
+    DPP_STEP(unsigned, x, umax2, 0x111, 0xF, 0xF);
+    DPP_STEP(unsigned, x, umax2, 0x112, 0xF, 0xF);
+    DPP_STEP(unsigned, x, umax2, 0x113, 0xF, 0xF);
+    DPP_STEP(unsigned, x, umax2, 0x114, 0xF, 0xE);
+    DPP_STEP(unsigned, x, umax2, 0x118, 0xF, 0xC);
+    DPP_STEP(unsigned, x, umax2, 0x142, 0xA, 0xF);
+    DPP_STEP(unsigned, x, umax2, 0x143, 0xC, 0xF);
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 // wave max of 64-bit unsigned keys (two 32-bit DPP moves per step)
 __device__ __forceinline__ unsigned long long wave_reduce_max_u64(unsigned long long x) {
 #define DPP_MAX64(ctrl, rmask, bmask)                                                                          \

@@ -41,18 +41,57 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     extern __shared__ __align__(16) uint8_t smem[];   // staged activation rows (codes) then their E8M0 bytes
     __shared__ int s_eid[UP_MAXM * UP_MAXK];
     __shared__ float s_wt[UP_MAXM * UP_MAXK];
-    __shared__ int s_pos[UP_MAXM * UP_MAXK];          // sorted slot of pair p
-    __shared__ int s_lt[UP_MAXM * UP_MAXK];           // pairs with a smaller expert id (= group start)
-    __shared__ int s_gidx[UP_MAXE];                   // group index of a selected expert
-    __shared__ int s_wsum[UP_WAVES];
+    __shared__ unsigned long long s_bits[UP_MAXE / 64];   // selected experts
     __shared__ int s_tok[UP_MAXM * UP_MAXK], s_slot[UP_MAXM * UP_MAXK];   // members of this workgroup's group
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
-    __shared__ int s_eg, s_mg, s_ng;
+    __shared__ int s_mg;
     __shared__ v4f s_acc[UP_WAVES][64];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform values kept in scalar registers
     const int M = a.M, topk = a.topk, P = M * a.topk, E = a.E;
+    const int K = a.H, nk = K >> 7, Kh = K >> 1, Ks = K >> 5, LS = K + 16;
+    uint8_t* lds_s = smem + a.rows * LS;
+
+    // Activation row `row` of LDS <- token `tok`: E4M3 codes + E8M0 bytes. Two lanes per 32-value group,
+    // 16 values (2 x 16 bytes) each; a lane pair is always active together. load / convert are split so the
+    // loads can be issued early.
+    const int per_row = Ks * 2;
+    auto x_load = [&](int tok, int q, v4i& r0, v4i& r1) {
+        const uint16_t* src = a.x + (long long)tok * a.ldx + q * 16;
+        r0 = *(const v4i*)src;
+        r1 = *(const v4i*)(src + 8);
+    };
+    auto x_store = [&](int row, int q, v4i r0, v4i r1) {
+        const uint32_t wd[8] = {(uint32_t)r0.x, (uint32_t)r0.y, (uint32_t)r0.z, (uint32_t)r0.w,
+                                (uint32_t)r1.x, (uint32_t)r1.y, (uint32_t)r1.z, (uint32_t)r1.w};
+        float f[16];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            f[2 * j] = bf16_to_f32(wd[j] & 0xFFFFu);
+            f[2 * j + 1] = bf16_to_f32(wd[j] >> 16);
+        }
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(f[j]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
+        const int e = fq8_exponent(amax);
+        uint32_t cw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            cw[j] = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) cw[j] |= fq8_code(f[4 * j + b], e) << (8 * b);
+        }
+        *(v4i*)(smem + row * LS + q * 16) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+        if ((q & 1) == 0) lds_s[row * Ks + (q >> 1)] = (uint8_t)(e + 127);
+    };
+
+    // ---- one token: its activations are the only row, staged while the routing runs
+    const bool early = M == 1 && per_row <= (int)blockDim.x;
+    v4i xr0, xr1;
+    if (early && tid < per_row) x_load(0, tid, xr0, xr1);
+    if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
 
     // ---- routing for all M tokens (one wave per token), identical in every workgroup
     for (int t = wave; t < M; t += UP_WAVES) {
@@ -69,163 +108,106 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             s_wt[t * topk + lane] = kw;
         }
     }
-    for (int e = tid; e < E; e += blockDim.x) s_gidx[e] = 0;
+    if (early && tid < per_row) x_store(0, tid, xr0, xr1);
     __syncthreads();
-    for (int p = tid; p < P; p += blockDim.x)
-        if (s_eid[p] >= 0) s_gidx[s_eid[p]] = 1;
-    __syncthreads();
-    // ---- bucketing: group index of each selected expert (ballot prefix over experts, ascending ids)
-    {
-        int base = 0;
-        for (int e0 = 0; e0 < E; e0 += blockDim.x) {
-            const int e = e0 + tid;
-            const int mark = e < E ? s_gidx[e] : 0;
-            const unsigned long long bal = __ballot(mark);
-            if (lane == 0) s_wsum[wave] = __popcll(bal);
-            __syncthreads();
-            int before = base;
-            for (int w = 0; w < wave; ++w) before += s_wsum[w];
-            int total = 0;
-            for (int w = 0; w < UP_WAVES; ++w) total += s_wsum[w];
-            const unsigned long long below = lane == 63 ? ~0ull >> 1 : ((1ull << lane) - 1ull);
-            if (e < E) s_gidx[e] = mark ? before + __popcll(bal & below) : -1;
-            base += total;
-            __syncthreads();
-        }
-        if (tid == 0) s_ng = base;
-    }
-    // sorted slot of every pair: pairs of smaller experts first, then same expert with a smaller token
     for (int p = tid; p < P; p += blockDim.x) {
         const int e = s_eid[p];
-        int lt = 0, same = 0;
-        for (int q = 0; q < P; ++q) {
-            const int eq = s_eid[q];
-            lt += (eq >= 0 && eq < e) ? 1 : 0;
-            same += (eq == e && q < p) ? 1 : 0;   // pairs are token-major: q < p = earlier token (or slot)
-        }
-        s_lt[p] = lt;
-        s_pos[p] = e >= 0 ? lt + same : -1;
+        if (e >= 0) atomicOr(&s_bits[e >> 6], 1ull << (e & 63));
     }
     __syncthreads();
-    const int U = __builtin_amdgcn_readfirstlane(s_ng);
+
+    // ---- this workgroup's expert: the g-th smallest selected id (groups are in ascending expert order)
     const int g = blockIdx.y;
-    // ---- workgroup (0, 0) publishes the routing and the tables of the down projection
-    if (blockIdx.x == 0 && g == 0) {
-        int valid = 0;
-        for (int p = 0; p < P; ++p) valid += s_eid[p] >= 0 ? 1 : 0;
-        for (int p = tid; p < P; p += blockDim.x) {
-            if (a.eid_out) a.eid_out[p] = s_eid[p];
-            if (a.wt_out) a.wt_out[p] = s_wt[p];
-            if (s_pos[p] >= 0) {
-                a.tok_sorted[s_pos[p]] = p / topk;
-                a.wt_sorted[s_pos[p]] = s_wt[p];
-                if (s_pos[p] == s_lt[p]) {   // first pair of its expert: the group entry
-                    a.grp_expert[s_gidx[s_eid[p]]] = s_eid[p];
-                    a.grp_start[s_gidx[s_eid[p]]] = s_lt[p];
-                }
-            }
+    int U = 0, eg = -1;
+#pragma unroll
+    for (int w = 0; w < UP_MAXE / 64; ++w) {
+        unsigned long long bits = s_bits[w];
+        bits = ((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(bits >> 32)) << 32) |
+               (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)bits);
+        const int c = __popcll(bits);
+        if (eg < 0 && g < U + c) {
+            for (int r = g - U; r > 0; --r) bits &= bits - 1ull;   // drop the lower set bits
+            eg = 64 * w + (int)__builtin_ctzll(bits);
         }
-        for (int s2 = U + tid; s2 < P; s2 += blockDim.x) { a.grp_expert[s2] = -1; a.grp_start[s2] = valid; }
-        if (tid == 0) { a.grp_start[U] = valid; a.grp_start[P] = valid; }
-        for (int s2 = valid + tid; s2 < P; s2 += blockDim.x) { a.tok_sorted[s2] = 0; a.wt_sorted[s2] = 0.f; }
+        U += c;
     }
-    if (g >= U) return;   // uniform: fewer distinct experts than slots
-    // ---- this group's expert and tokens (ascending)
-    if (tid < E && s_gidx[tid] == g) s_eg = tid;
-    for (int e = tid + blockDim.x; e < E; e += blockDim.x)
-        if (s_gidx[e] == g) s_eg = e;
-    __syncthreads();
-    const int eg = __builtin_amdgcn_readfirstlane(s_eg);
-    if (tid == 0) s_mg = 0;
-    __syncthreads();
-    for (int p = tid; p < P; p += blockDim.x)
-        if (s_eid[p] == eg) {   // member rank = sorted slot - group start (token order)
-            const int r = s_pos[p] - s_lt[p];
-            s_tok[r] = p / topk;
-            s_slot[r] = s_pos[p];
-            s_pw[r] = s_wt[p];
-            atomicAdd(&s_mg, 1);
-        }
-    __syncthreads();
-    const int mg = __builtin_amdgcn_readfirstlane(s_mg);
+    const bool publish = blockIdx.x == 0 && g == 0;
+    if (g >= U && !publish) return;   // uniform: fewer distinct experts than slots
 
     // ---- this wave's weight stream: row block rb of {gate c0, gate c0 + 16, up c0, up c0 + 16}, K-half kh
-    const int K = a.H, nk = K >> 7, Kh = K >> 1, Ks = K >> 5, LS = K + 16;
     const int c0 = blockIdx.x * 32;
     const int rbi = wave & 3, kh = wave >> 2;
     const int row_first = (rbi < 2 ? c0 : a.I + c0) + (rbi & 1) * 16;
     const int nb = row_first >> 4;
     const int nk_h = nk / 2, k0c = kh * nk_h, nk_w = kh ? nk - nk_h : nk_h;
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W13 + (long long)eg * a.stride_we, (uint32_t)a.stride_we);
-    const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S13 + (long long)eg * a.stride_se, (uint32_t)a.stride_se);
+    const int egw = eg < 0 ? 0 : eg;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W13 + (long long)egw * a.stride_we, (uint32_t)a.stride_we);
+    const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S13 + (long long)egw * a.stride_se, (uint32_t)a.stride_se);
     const uint32_t wv = (uint32_t)wtile_off<TILED>(nb, k0c, nk, Kh, lane), sv = (uint32_t)stile_off<TILED>(nb, k0c, nk, Ks, lane);
     const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
     const int col = lane & 15, kb = lane >> 4;
-    uint8_t* lds_s = smem + a.rows * LS;
     v4i A[PF];
     int SA[PF];
-    const uint8_t* xl;
-    const uint8_t* xsl;
-    v4f acc;
     auto load = [&](int slot, int kc) {
         A[slot] = buffer_load_tile(wr, wv, (uint32_t)(kc * ws));
         SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
     };
-    auto use = [&](int slot) {
-        const v4i b0 = *(const v4i*)(xl);
-        const v4i b1 = *(const v4i*)(xl + 64);
-        const int sb = *xsl;
-        xl += 128;
-        xsl += 4;
-        acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
-                             v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, SA[slot], sb);
-    };
-    // Activation rows base .. base + mp - 1 of the group -> E4M3 codes + E8M0 bytes in LDS. Two lanes per
-    // 32-value group, 16 values (2 x 16 bytes) each; a lane pair is always active together.
-    auto stage = [&](int base, int mp) {
-        const int per_row = Ks * 2;
+    const bool work = g < U;
+    if (work) pipeline_start<PF>(nk_w, load);   // the weight tiles go out as soon as the expert is known
+
+    // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
+    if (tid == 0) s_mg = 0;
+    __syncthreads();
+    if (work)
+        for (int p = tid; p < P; p += blockDim.x)
+            if (s_eid[p] == eg) {
+                int lt = 0, same = 0;
+                for (int q = 0; q < P; ++q) {
+                    const int eq = s_eid[q];
+                    lt += (eq >= 0 && eq < eg) ? 1 : 0;
+                    same += (eq == eg && q < p) ? 1 : 0;   // pairs are token-major: q < p = earlier token (or slot)
+                }
+                s_tok[same] = p / topk;
+                s_slot[same] = lt + same;
+                s_pw[same] = s_wt[p];
+                atomicAdd(&s_mg, 1);
+            }
+    __syncthreads();
+    // LDS holds every token of the group (at most M when a token's expert ids are distinct, as the gate
+    // guarantees; members past a.rows, possible only with repeated ids, are not computed)
+    const int mg = min(a.rows, __builtin_amdgcn_readfirstlane(s_mg));
+    if (work && !early) {
 #pragma unroll 1
-        for (int i = tid; i < mp * per_row; i += blockDim.x) {
+        for (int i = tid; i < mg * per_row; i += blockDim.x) {
             const int r = i / per_row, q = i - r * per_row;
-            const uint16_t* src = a.x + (long long)s_tok[base + r] * a.ldx + q * 16;
-            const v4i r0 = *(const v4i*)src, r1 = *(const v4i*)(src + 8);
-            const uint32_t wd[8] = {(uint32_t)r0.x, (uint32_t)r0.y, (uint32_t)r0.z, (uint32_t)r0.w,
-                                    (uint32_t)r1.x, (uint32_t)r1.y, (uint32_t)r1.z, (uint32_t)r1.w};
-            float f[16];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f[2 * j] = bf16_to_f32(wd[j] & 0xFFFFu);
-                f[2 * j + 1] = bf16_to_f32(wd[j] >> 16);
-            }
-            float amax = 0.f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(f[j]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
-            const int e = fq8_exponent(amax);
-            uint32_t cw[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                cw[j] = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) cw[j] |= fq8_code(f[4 * j + b], e) << (8 * b);
-            }
-            *(v4i*)(smem + r * LS + q * 16) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
-            if ((q & 1) == 0) lds_s[r * Ks + (q >> 1)] = (uint8_t)(e + 127);
+            v4i r0, r1;
+            x_load(s_tok[r], q, r0, r1);
+            x_store(r, q, r0, r1);
         }
-    };
-    // B columns: pass token col (columns past the pass read row 0; their results are not used)
-    auto reset = [&](int mp) {
-        const int brow = col < mp ? col : 0;
-        xl = smem + brow * LS + k0c * 128 + kb * 16;
-        xsl = lds_s + brow * Ks + k0c * 4 + kb;
-        acc = v4f{0.f, 0.f, 0.f, 0.f};
-    };
-    // SwiGLU epilogue: half-wave i handles pass token i; lane c of it handles column c0 + c
-    auto epilogue = [&](int base, int mp) {
+        __syncthreads();
+    }
+
+    if (work) {
+        // B columns: member col (columns past the group read row 0; their results are not used)
+        const int brow = col < mg ? col : 0;
+        const uint8_t* xl = smem + brow * LS + k0c * 128 + kb * 16;
+        const uint8_t* xsl = lds_s + brow * Ks + k0c * 4 + kb;
+        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+        auto use = [&](int slot) {
+            const v4i b0 = *(const v4i*)(xl);
+            const v4i b1 = *(const v4i*)(xl + 64);
+            const int sb = *xsl;
+            xl += 128;
+            xsl += 4;
+            acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
+                                 v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, SA[slot], sb);
+        };
+        pipeline_finish<PF>(nk_w, load, use);
         s_acc[wave][lane] = acc;
         __syncthreads();
+        // SwiGLU epilogue: half-wave i handles member i; lane c of it handles column c0 + c
         const int hw = tid >> 5, c = tid & 31;
-        if (hw < mp) {
+        if (hw < mg) {
             // D[row][col] of a 16x16 accumulator sits in lane col + 16 (row / 4), element row % 4
             const int r16 = c & 15, l = hw + 16 * (r16 >> 2), el = r16 & 3;
             const int wg = c >> 4;   // gate row block of column c (0 / 1), up block = 2 + wg
@@ -236,25 +218,45 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 gg = fminf(gg, a.limit);
             }
             float h = gg * (1.0f / (1.0f + expf(-gg))) * uu;
-            h = h * s_pw[base + hw];
+            h = h * s_pw[hw];
             h = bf16_round(h);
             const int e = fq8_exponent(wave_max32(fabsf(h)));
-            const int slot = s_slot[base + hw];
+            const int slot = s_slot[hw];
             a.hc[(long long)slot * a.ldhc + c0 + c] = (uint8_t)fq8_code(h, e);
             if (c == 0) a.hs[(long long)slot * a.ldhs + (c0 >> 5)] = (uint8_t)(e + 127);
         }
-    };
+    }
 
-    // One pass: LDS holds every token of the group (at most M when a token's expert ids are distinct, as the
-    // gate guarantees; members past a.rows, possible only with repeated ids, are not computed). The weight
-    // tiles go out first; quantising the activations into LDS overlaps their latency.
-    const int mp0 = min(a.rows, mg);
-    pipeline_start<PF>(nk_w, load);
-    stage(0, mp0);
-    __syncthreads();
-    reset(mp0);
-    pipeline_finish<PF>(nk_w, load, use);
-    epilogue(0, mp0);
+    // ---- workgroup (0, 0) publishes the routing and the tables of the down projection (off the critical path:
+    // the down projection is the next launch)
+    if (publish) {
+        int valid = 0;
+        for (int p = 0; p < P; ++p) valid += s_eid[p] >= 0 ? 1 : 0;
+        for (int p = tid; p < P; p += blockDim.x) {
+            const int e = s_eid[p];
+            if (a.eid_out) a.eid_out[p] = e;
+            if (a.wt_out) a.wt_out[p] = s_wt[p];
+            if (e < 0) continue;
+            int lt = 0, same = 0;
+            for (int q = 0; q < P; ++q) {
+                const int eq = s_eid[q];
+                lt += (eq >= 0 && eq < e) ? 1 : 0;
+                same += (eq == e && q < p) ? 1 : 0;
+            }
+            a.tok_sorted[lt + same] = p / topk;
+            a.wt_sorted[lt + same] = s_wt[p];
+            if (same == 0) {   // first pair of its expert: the group entry; group index = selected ids below e
+                int gi = 0;
+                for (int w = 0; w < (e >> 6); ++w) gi += __popcll(s_bits[w]);
+                gi += __popcll(s_bits[e >> 6] & ((1ull << (e & 63)) - 1ull));
+                a.grp_expert[gi] = e;
+                a.grp_start[gi] = lt;
+            }
+        }
+        for (int s2 = U + tid; s2 < P; s2 += blockDim.x) { a.grp_expert[s2] = -1; a.grp_start[s2] = valid; }
+        if (tid == 0) { a.grp_start[U] = valid; a.grp_start[P] = valid; }
+        for (int s2 = valid + tid; s2 < P; s2 += blockDim.x) { a.tok_sorted[s2] = 0; a.wt_sorted[s2] = 0.f; }
+    }
 }
 
 extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const float* bias, float temp, float route_scale, int score_func,
@@ -290,6 +292,7 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const flo
         moe_decode_up_kernel<T, 8, PER><<<grid, block, lds, st>>>(a);                                         \
     } while (0)
     if (E <= 256) { if (tiled) UP_LAUNCH(1, 4); else UP_LAUNCH(0, 4); }
+    else if (E <= 384) { if (tiled) UP_LAUNCH(1, 6); else UP_LAUNCH(0, 6); }
     else { if (tiled) UP_LAUNCH(1, 8); else UP_LAUNCH(0, 8); }
 #undef UP_LAUNCH
     return (int)hipGetLastError();

@@ -1,8 +1,10 @@
 // The MoE gate of one token row, computed by one wave (fused2.gate_topk, fused2.py:418-452; model.MoE.gate,
 // model.py:391-404): scoring function, + bias for the selection only, top-k with the lowest index winning ties,
-// weights renormalised (+1e-20) and scaled. Lane l owns scores e = l, l + 64, ... in registers; every reduction
-// is a DPP row operation (no LDS round trips); each of the topk rounds is one 64-bit max-reduction over keys
-// (order(score + bias) << 32 | ~index). On return lane k < topk holds the k-th expert id and its weight.
+// weights renormalised (+1e-20) and scaled. Lane l owns the contiguous scores e = l * PER .. l * PER + PER - 1
+// in registers, so a lower lane always holds lower indices: each of the topk rounds is one 32-bit DPP
+// max-reduction over the lanes' current maxima (order-preserving keys of score + bias) and one ballot, whose
+// lowest set lane is the winner (ties -> lowest index). Only the winning lane rescans its PER keys. On return
+// lane k < topk holds the k-th expert id and its weight.
 #pragma once
 #include "common.h"
 
@@ -10,12 +12,12 @@ template <int PER>
 __device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, const float* __restrict__ bias, int E, float temp, int topk,
                                               float route_scale, int mode, int norm, int* out_i, float* out_w) {
     const int lane = threadIdx.x & 63;
+    const int e0 = lane * PER;
     float s[PER];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        s[i] = e < E ? S[e] / temp : -INFINITY;
+        s[i] = e0 + i < E ? S[e0 + i] / temp : -INFINITY;
         mx = fmaxf(mx, s[i]);
     }
     // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440
@@ -24,7 +26,7 @@ __device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, const
         float sum = 0.f;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            s[i] = lane + 64 * i < E ? expf(s[i] - mx) : 0.f;
+            s[i] = e0 + i < E ? expf(s[i] - mx) : 0.f;
             sum += s[i];
         }
         sum = wave_reduce_sum(sum);
@@ -35,29 +37,42 @@ __device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, const
         for (int i = 0; i < PER; ++i)
             s[i] = mode == 1 ? 1.0f / (1.0f + expf(-s[i])) : sqrtf(s[i] > 20.f ? s[i] : log1pf(expf(s[i])));
     }
-    unsigned long long key[PER];
+    unsigned key[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        const int e = lane + 64 * i;
-        const float v = e < E ? s[i] + (bias ? bias[e] : 0.f) : -INFINITY;
-        // invalid entries and NaN scores get key 0: they never beat a real candidate
-        key[i] = (e < E && v == v) ? ((unsigned long long)float_order_key(v) << 32) | (unsigned)(0xFFFFFFFFu - (unsigned)e) : 0ull;
+        const float v = e0 + i < E ? s[i] + (bias ? bias[e0 + i] : 0.f) : -INFINITY;
+        // invalid entries and NaN scores get key 0: every real candidate's key is larger
+        key[i] = (e0 + i < E && v == v) ? float_order_key(v) : 0u;
     }
+    // the lane's best key, its slot (lowest on ties) and score
+    unsigned lk = 0u;
+    int li = 0;
+    float ls = 0.f;
+    auto rescan = [&]() {
+        lk = 0u;
+        li = 0;
+        ls = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+            if (key[i] > lk) { lk = key[i]; li = i; ls = s[i]; }
+    };
+    rescan();
     float wsum = 0.f, my_w = 0.f;
     int my_i = 0;
     for (int k = 0; k < topk; ++k) {
-        unsigned long long best = 0;
+        const unsigned best = wave_reduce_max_u32(lk);
+        // no candidate left (every remaining score NaN): index k, so no index is ever >= E
+        const unsigned long long m = __ballot(best != 0u && lk == best);
+        const int owner = m ? (int)__builtin_ctzll(m) : 0;
+        const int slot = __builtin_amdgcn_readlane(li, owner);
+        const int bi = m ? owner * PER + slot : k;
+        const float w = m ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner)) : 0.f;
+        if (m && lane == owner) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) best = key[i] > best ? key[i] : best;
-        best = wave_reduce_max_u64(best);
-        // no candidate left (every remaining score NaN): emit index k, so no index is ever >= E
-        const int bi = best ? (int)(0xFFFFFFFFu - (unsigned)best) : k;
-        const int owner = bi & 63, slot = bi >> 6;
-        float w = 0.f;
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (i == slot && lane == owner) { w = s[i]; key[i] = 0; }
-        w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), owner));
+            for (int i = 0; i < PER; ++i)
+                if (i == slot) key[i] = 0u;
+            rescan();
+        }
         wsum += w;
         if (lane == k) { my_w = w; my_i = bi; }
     }

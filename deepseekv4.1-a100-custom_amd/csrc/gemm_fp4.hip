@@ -239,95 +239,135 @@ struct DownSumArgs {
 // One workgroup per 16-row block of the output; its 8 waves split the selected experts (group slots g = wave,
 // wave + 8, ...), each accumulating sum over its experts and k of W2[e] . h in one MFMA accumulator whose
 // column t is token t; a token absent from a group reads the zero row. The partial accumulators are summed in
-// a fixed order through LDS. The (group, k-chunk) space of a wave is flattened so the weight pipeline runs
-// across expert boundaries. H_LDS: all h rows (+ the zero row) are staged in LDS, so the vector memory queue
-// holds only weight tiles.
+// a fixed order through LDS. A wave walks its (group, k-chunk) space with a scalar iterator, so the weight
+// pipeline runs across expert boundaries without branches.
+// Prologue: every table is fetched in one round trip. H_LDS: all h rows (+ the zero row) are staged in LDS and
+// the weight tiles go out before that staging (their addresses need only the group experts), so the first
+// tiles are in flight while the tables and h are prepared; the vector memory queue then holds weight tiles only.
 template <int TILED, int PF, int NKC, int H_LDS>
-__global__ void __launch_bounds__(DS_WAVES * 64) moe_down_sum_kernel(const DownSumArgs a) {
+__global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_kernel(const DownSumArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ short s_exp[DS_MAX_SLOTS];
-    __shared__ short s_pair[DS_MAX_SLOTS][16];
-    __shared__ short s_we[DS_WAVES][DS_MAX_SLOTS / DS_WAVES + 1];        // per wave: expert of its j-th group
-    __shared__ short s_wq[DS_WAVES][DS_MAX_SLOTS / DS_WAVES + 1][16];    // per wave: pair row of token t in it
-    __shared__ int s_cnt[DS_WAVES];
+    __shared__ short s_pair[DS_MAX_SLOTS][16];        // pair row of token t in group slot g (zero row if absent)
+    __shared__ int s_start[DS_MAX_SLOTS + 1];
+    __shared__ short s_tok[DS_MAX_SLOTS];
     __shared__ v4f s_red[DS_WAVES][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = blockIdx.x;
     const int K = a.K, Ks = K >> 5, LS = K + 16;
-    for (int g = threadIdx.x; g < a.n_slots; g += blockDim.x) {
-        const int ge = a.grp_expert[g];
-        int e = ge < 0 ? -1 : ge - a.shard_start;
+    const int n_slots = a.n_slots;
+
+    // ---- one round trip: this wave's group experts (slot wave + 8 j in lane j), the group starts, the tokens
+    const int gslot = wave + DS_WAVES * lane;
+    int e = -1;
+    if (lane < DS_MAX_SLOTS / DS_WAVES && gslot < n_slots) {
+        const int ge = a.grp_expert[gslot];
+        e = ge < 0 ? -1 : ge - a.shard_start;
         if (e >= a.shard_n) e = -1;
-        s_exp[g] = (short)e;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) s_pair[g][t] = (short)a.zero_row;
-        if (e >= 0)
-            for (int q = a.grp_start[g]; q < a.grp_start[g + 1]; ++q) s_pair[g][a.tok_sorted[q] & 15] = (short)q;
     }
-    if (H_LDS) {  // rows 0 .. zero_row of h (codes, 16-byte vectors) and their E8M0 bytes
-        uint8_t* hs_l = smem + (size_t)(a.zero_row + 1) * LS;
-        const int vpr = K >> 4;
-        for (int i = threadIdx.x; i < (a.zero_row + 1) * vpr; i += blockDim.x) {
-            const int r = i / vpr, v = i - r * vpr;
-            *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.hc + (long long)r * a.ldh + v * 16);
-        }
-        for (int i = threadIdx.x; i < (a.zero_row + 1) * Ks; i += blockDim.x) {
-            const int r = i / Ks, v = i - r * Ks;
-            hs_l[r * Ks + v] = a.hs[(long long)r * a.ldhs + v];
-        }
-    }
-    __syncthreads();
-    if (lane == 0) {  // this wave's valid groups, in slot order
-        int c = 0;
-        for (int g = wave; g < a.n_slots; g += DS_WAVES)
-            if (s_exp[g] >= 0) {
-                s_we[wave][c] = s_exp[g];
-#pragma unroll
-                for (int t = 0; t < 16; ++t) s_wq[wave][c][t] = s_pair[g][t];
-                ++c;
-            }
-        s_cnt[wave] = c;
-    }
-    __syncthreads();
+    int st = 0, tk = 0;
+    if (tid <= n_slots) st = a.grp_start[tid];
+    if (tid < n_slots) tk = a.tok_sorted[tid];
+    const unsigned long long vmask = __ballot(e >= 0);   // this wave's valid groups
+
     const int col = lane & 15, kb = lane >> 4;
     const int nk = NKC > 0 ? NKC : (K >> 7), Kh = K >> 1;
-    const long long w0 = wtile_off<TILED>(nb, 0, nk, Kh, lane), s0 = stile_off<TILED>(nb, 0, nk, Ks, lane);
+    const uint32_t w0 = (uint32_t)wtile_off<TILED>(nb, 0, nk, Kh, lane), s0 = (uint32_t)stile_off<TILED>(nb, 0, nk, Ks, lane);
     const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
-    const int total = s_cnt[wave] * nk;
+    const int total = __popcll(vmask) * nk;
+    // producer iterator (load order = consume order): valid-lane mask, k-chunk, expert
+    unsigned long long pm = vmask;
+    int pkc = 0;
+    long long pe = pm ? __builtin_amdgcn_readlane(e, (int)__builtin_ctzll(pm)) : 0;
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
     v4i A[PF], B0[H_LDS ? 1 : PF], B1[H_LDS ? 1 : PF];
     int SA[PF], SB[H_LDS ? 1 : PF];
-    int uit = 0;   // consume-side iteration (H_LDS reads B when the slot is consumed)
     const uint8_t* hs_l = smem + (size_t)(a.zero_row + 1) * LS;
-    // flattened (group, k-chunk) iteration: addresses computed without branches so the pipeline stays exact
-    pipelined<PF>(total,
-        [&](int slot, int it) {
-            const int j = it / nk, kc = it - j * nk;
-            const long long e = s_we[wave][j];
-            A[slot] = load_weight_tile(a.W + e * a.stride_we + w0 + (long long)kc * ws);
-            SA[slot] = a.S[e * a.stride_se + s0 + (long long)kc * ss];
-            if (!H_LDS) {
-                const long long q = s_wq[wave][j][col];
-                const uint8_t* hb = a.hc + q * a.ldh + kc * 128 + kb * 16;
-                B0[slot] = *(const v4i*)hb;
-                B1[slot] = *(const v4i*)(hb + 64);
-                SB[slot] = a.hs[q * a.ldhs + kc * 4 + kb];
-            }
-        },
-        [&](int slot) {
-            if (H_LDS) {
-                const int j = uit / nk, kc = uit - j * nk;
-                ++uit;
-                const int q = s_wq[wave][j][col];
-                const uint8_t* hb = smem + q * LS + kc * 128 + kb * 16;
-                const v4i b0 = *(const v4i*)hb;
-                const v4i b1 = *(const v4i*)(hb + 64);
-                const int sb = hs_l[q * Ks + kc * 4 + kb];
-                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
-            } else {
-                acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
-            }
-        });
+    // !H_LDS: the lane's h row (global) of the producer's current group, set at group boundaries
+    const uint8_t* phb = a.hc;
+    const uint8_t* phs = a.hs;
+    auto prod_rows = [&]() {
+        const long long q = pm ? s_pair[wave + DS_WAVES * (int)__builtin_ctzll(pm)][col] : a.zero_row;
+        phb = a.hc + q * a.ldh + kb * 16;
+        phs = a.hs + q * a.ldhs + kb;
+    };
+    auto load = [&](int slot, int) {
+        // one expert's tiles through a buffer descriptor: scalar base, 32-bit lane offset, scalar k offset
+        A[slot] = buffer_load_tile(buffer_rsrc(a.W + pe * a.stride_we, (uint32_t)a.stride_we), w0, (uint32_t)(pkc * ws));
+        SA[slot] = buffer_load_byte(buffer_rsrc(a.S + pe * a.stride_se, (uint32_t)a.stride_se), s0, (uint32_t)(pkc * ss));
+        if (!H_LDS) {
+            B0[slot] = *(const v4i*)phb;
+            B1[slot] = *(const v4i*)(phb + 64);
+            SB[slot] = *phs;
+            phb += 128;
+            phs += 4;
+        }
+        if (++pkc == nk) {
+            pkc = 0;
+            pm &= pm - 1ull;
+            pe = pm ? __builtin_amdgcn_readlane(e, (int)__builtin_ctzll(pm)) : 0;
+            if (!H_LDS) prod_rows();
+        }
+    };
+    // consumer iterator: the lane's h row pointers move along k and jump at group boundaries
+    unsigned long long cm = vmask;
+    int ckc = 0;
+    const uint8_t* hb = smem;
+    const uint8_t* hsb = hs_l;
+    auto group_rows = [&]() {
+        const int q = cm ? s_pair[wave + DS_WAVES * (int)__builtin_ctzll(cm)][col] : a.zero_row;
+        hb = smem + q * LS + kb * 16;
+        hsb = hs_l + q * Ks + kb;
+    };
+    auto use = [&](int slot) {
+        if (H_LDS) {
+            const v4i b0 = *(const v4i*)hb;
+            const v4i b1 = *(const v4i*)(hb + 64);
+            const int sb = *hsb;
+            hb += 128;
+            hsb += 4;
+            acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
+        } else {
+            acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
+        }
+        if (++ckc == nk) {
+            ckc = 0;
+            cm &= cm - 1ull;
+            if (H_LDS) group_rows();
+        }
+    };
+    if (H_LDS) pipeline_start<PF>(total, load);
+
+    // ---- tables -> LDS (and h rows 0 .. zero_row when H_LDS), then the pair rows of every valid group
+    if (tid <= n_slots) s_start[tid] = st;
+    if (tid < n_slots) s_tok[tid] = (short)tk;
+    if (H_LDS) {
+        const int vpr = K >> 4;
+        for (int i = tid; i < (a.zero_row + 1) * vpr; i += blockDim.x) {
+            const int r = i / vpr, v = i - r * vpr;
+            *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.hc + (long long)r * a.ldh + v * 16);
+        }
+        uint8_t* hsw = smem + (size_t)(a.zero_row + 1) * LS;
+        for (int i = tid; i < (a.zero_row + 1) * Ks; i += blockDim.x) {
+            const int r = i / Ks, v = i - r * Ks;
+            hsw[r * Ks + v] = a.hs[(long long)r * a.ldhs + v];
+        }
+    }
+    __syncthreads();
+    if (lane < DS_MAX_SLOTS / DS_WAVES && gslot < n_slots) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) s_pair[gslot][t] = (short)a.zero_row;
+        if (e >= 0)
+            for (int q = s_start[gslot]; q < s_start[gslot + 1]; ++q) s_pair[gslot][s_tok[q] & 15] = (short)q;
+    }
+    __syncthreads();
+    if (H_LDS) {
+        group_rows();
+        pipeline_finish<PF>(total, load, use);
+    } else {
+        prod_rows();
+        pipelined<PF>(total, load, use);
+    }
     s_red[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
@@ -420,21 +460,20 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                                   int shard_start, int shard_n, void* stream) {
     if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb)) return DSV41_EINVAL;
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0) return DSV41_EINVAL;
+    // one expert's weights are addressed with 32-bit offsets and hold N rows of K / 2 bytes
+    if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
+        stride_se < (long long)N * (K / 32))
+        return DSV41_EINVAL;
     if ((ldh & 15) || (((uintptr_t)hc) & 15)) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n};
     hipStream_t st = (hipStream_t)stream;
     const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
-    const bool h_lds = lds <= 32 * 1024;
+    const bool h_lds = lds <= 60 * 1024;
     const dim3 grid(N / 16), block(DS_WAVES * 64);
 #define DS_LAUNCH(T, PF, NK, HL) moe_down_sum_kernel<T, PF, NK, HL><<<grid, block, HL ? lds : 0, st>>>(a)
-    if (K == 1664) {   // the decode shape: k-chunk count known at compile time
-        if (h_lds) { if (tiled) DS_LAUNCH(1, 13, 13, 1); else DS_LAUNCH(0, 13, 13, 1); }
-        else { if (tiled) DS_LAUNCH(1, 8, 13, 0); else DS_LAUNCH(0, 8, 13, 0); }
-    } else {
-        if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1); else DS_LAUNCH(0, 12, 0, 1); }
-        else { if (tiled) DS_LAUNCH(1, 8, 0, 0); else DS_LAUNCH(0, 8, 0, 0); }
-    }
+    if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1); else DS_LAUNCH(0, 12, 0, 1); }
+    else { if (tiled) DS_LAUNCH(1, 8, 0, 0); else DS_LAUNCH(0, 8, 0, 0); }
 #undef DS_LAUNCH
     return (int)hipGetLastError();
 }

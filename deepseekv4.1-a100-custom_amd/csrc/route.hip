@@ -34,6 +34,7 @@ extern "C" int dsv41_gate_topk(const float* scores, long long lds, const float* 
     if (B == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     if (E <= 64 * 4) gate_topk_kernel<4><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
+    else if (E <= 64 * 6) gate_topk_kernel<6><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
     else if (E <= 64 * 8) gate_topk_kernel<8><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
     else gate_topk_kernel<GATE_MAX_PER_LANE><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
     return (int)hipGetLastError();
