@@ -31,6 +31,10 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 E, H, I, TOPK = 384, 7168, 1664, 8
 LIMIT = 10.0               # swiglu_limit of the reference tests (test_cpumoe.py:23)
 N_COPIES = 4
+# HBM bytes per launch of the dominant kernel (moe_decode_up_kernel, M = 1): rocprofv3 FETCH_SIZE 49,709.8 KiB and
+# WRITE_SIZE 16.4 KiB per dispatch, scaled by what the same counters read for a plain 512 MiB device copy
+# (FETCH x 2.000, WRITE x 1.000); summary and commands in profiles/moe_decode_up_kernel__configs1_decode_m1.txt
+UP_TRAFFIC_BYTES = int(round((49709.8 * 2.0 + 16.4 * 1.0) * 1024))
 
 
 def expert_bytes():
@@ -44,6 +48,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
+    ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
+                                                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
 
 
@@ -211,9 +217,10 @@ def main():
     # logits and activations it also reads are < 0.03 % of that and not counted)
     w13_bytes = TOPK * (2 * I * (H // 2) + 2 * I * (H // 32))
     t_up = bench_up_kernel(torch, dev, layers, K, W)
-    roof = {"bound": "hbm", "kernel": "moe_decode_up_kernel<1,8,8> (routing + w13 + SwiGLU, M=1)", "achieved": round(w13_bytes / t_up / 1e9, 1),
-            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(w13_bytes / t_up / HBM_PEAK, 4), "traffic": None,
-            "avg_launch_us": round(t_up * 1e6, 2), "algorithmic_bytes": w13_bytes}
+    roof = {"bound": "hbm", "kernel": "moe_decode_up_kernel<1,8,6,1> (routing + w13 + SwiGLU, M=1)", "achieved": round(w13_bytes / t_up / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(w13_bytes / t_up / HBM_PEAK, 4), "traffic": UP_TRAFFIC_BYTES,
+            "traffic_over_algorithmic": round(UP_TRAFFIC_BYTES / w13_bytes, 4), "avg_launch_us": round(t_up * 1e6, 2),
+            "algorithmic_bytes": w13_bytes}
     extra["down_sum_us_est"] = round((t_routed - t_up) * 1e6, 2)
     if not args.quick:
         g = torch.Generator(device=dev).manual_seed(5)
@@ -225,6 +232,13 @@ def main():
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                                      "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4)}
+    if args.calib:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).random_(0, 256)
+        dst = torch.empty_like(src)
+        t_copy, _ = graph_time(torch, lambda i: dst.copy_(src), 4, 2)
+        extra["copy_calibration"] = {"bytes_read": src.numel(), "bytes_written": dst.numel(), "us": round(t_copy * 1e6, 2),
+                                     "GBps_read": round(src.numel() / t_copy / 1e9, 1)}
+        del src, dst
     cpu = {"value": None, "note": "skipped"} if args.no_cpu else cpu_baseline()
     result = {
         "metric": "FP4 MoE decode us/layer + HBM TB/s; prefill grouped-GEMM MXFP4 TFLOPS",

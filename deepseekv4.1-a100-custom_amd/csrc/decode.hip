@@ -19,14 +19,13 @@
 #define UP_MAXM 16
 #define UP_MAXK 16
 #define UP_MAXE 512
-#define UP_MAX_LDS (136 * 1024)   // dynamic LDS bound (gfx950: 160 KiB per workgroup, less the static arrays)
 
 struct DecodeUpArgs {
     const float* logits; long long ldl;      // fp32 [M][E] router logits (or NULL: eid_in / wt_in given)
     const float* bias; float temp; float route_scale; int score_func; int norm;
     const int* eid_in; const float* wt_in;   // precomputed routing [M][topk] when logits is NULL
     int M, topk, E;
-    int rows;                                // activation rows LDS holds (= M)
+    int rows;                                // activation rows LDS holds (members staged per pass)
     const uint16_t* x; long long ldx;        // bf16 [M][H] activations on the FP8 grid
     const uint8_t* W13; long long stride_we; const uint8_t* S13; long long stride_se;
     int H, I;
@@ -36,7 +35,7 @@ struct DecodeUpArgs {
     int* grp_expert; int* grp_start; int* tok_sorted; float* wt_sorted;   // tables, P = M * topk slots
 };
 
-template <int TILED, int PF, int PER>
+template <int TILED, int PF, int PER, int EARLY>
 __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const DecodeUpArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];   // staged activation rows (codes) then their E8M0 bytes
     __shared__ int s_eid[UP_MAXM * UP_MAXK];
@@ -88,7 +87,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     };
 
     // ---- one token: its activations are the only row, staged while the routing runs
-    const bool early = M == 1 && per_row <= (int)blockDim.x;
+    const bool early = EARLY && per_row <= (int)blockDim.x;   // host guarantees both for EARLY
     v4i xr0, xr1;
     if (early && tid < per_row) x_load(0, tid, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
@@ -153,7 +152,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
     };
     const bool work = g < U;
-    if (work) pipeline_start<PF>(nk_w, load);   // the weight tiles go out as soon as the expert is known
+    if (EARLY && work) pipeline_start<PF>(nk_w, load);   // the weight tiles go out as soon as the expert is known
 
     // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
     if (tid == 0) s_mg = 0;
@@ -173,41 +172,33 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 atomicAdd(&s_mg, 1);
             }
     __syncthreads();
-    // LDS holds every token of the group (at most M when a token's expert ids are distinct, as the gate
-    // guarantees; members past a.rows, possible only with repeated ids, are not computed)
-    const int mg = min(a.rows, __builtin_amdgcn_readfirstlane(s_mg));
-    if (work && !early) {
-#pragma unroll 1
-        for (int i = tid; i < mg * per_row; i += blockDim.x) {
-            const int r = i / per_row, q = i - r * per_row;
-            v4i r0, r1;
-            x_load(s_tok[r], q, r0, r1);
-            x_store(r, q, r0, r1);
-        }
-        __syncthreads();
-    }
+    const int mg = __builtin_amdgcn_readfirstlane(s_mg);
 
-    if (work) {
-        // B columns: member col (columns past the group read row 0; their results are not used)
-        const int brow = col < mg ? col : 0;
-        const uint8_t* xl = smem + brow * LS + k0c * 128 + kb * 16;
-        const uint8_t* xsl = lds_s + brow * Ks + k0c * 4 + kb;
-        v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-        auto use = [&](int slot) {
-            const v4i b0 = *(const v4i*)(xl);
-            const v4i b1 = *(const v4i*)(xl + 64);
-            const int sb = *xsl;
-            xl += 128;
-            xsl += 4;
-            acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
-                                 v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, SA[slot], sb);
-        };
-        pipeline_finish<PF>(nk_w, load, use);
+    const uint8_t* xl;
+    const uint8_t* xsl;
+    v4f acc;
+    auto use = [&](int slot) {
+        const v4i b0 = *(const v4i*)(xl);
+        const v4i b1 = *(const v4i*)(xl + 64);
+        const int sb = *xsl;
+        xl += 128;
+        xsl += 4;
+        acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
+                             v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, SA[slot], sb);
+    };
+    // B column c = member base + c of the pass (columns past the pass read row 0; their results are unused)
+    auto start_pass = [&](int mp) {
+        const int brow = col < mp ? col : 0;
+        xl = smem + brow * LS + k0c * 128 + kb * 16;
+        xsl = lds_s + brow * Ks + k0c * 4 + kb;
+        acc = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    // SwiGLU epilogue: half-wave i handles member base + i; lane c of it handles column c0 + c
+    auto epilogue = [&](int base, int mp) {
         s_acc[wave][lane] = acc;
         __syncthreads();
-        // SwiGLU epilogue: half-wave i handles member i; lane c of it handles column c0 + c
         const int hw = tid >> 5, c = tid & 31;
-        if (hw < mg) {
+        if (hw < mp) {
             // D[row][col] of a 16x16 accumulator sits in lane col + 16 (row / 4), element row % 4
             const int r16 = c & 15, l = hw + 16 * (r16 >> 2), el = r16 & 3;
             const int wg = c >> 4;   // gate row block of column c (0 / 1), up block = 2 + wg
@@ -218,12 +209,40 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 gg = fminf(gg, a.limit);
             }
             float h = gg * (1.0f / (1.0f + expf(-gg))) * uu;
-            h = h * s_pw[hw];
+            h = h * s_pw[base + hw];
             h = bf16_round(h);
             const int e = fq8_exponent(wave_max32(fabsf(h)));
-            const int slot = s_slot[hw];
+            const int slot = s_slot[base + hw];
             a.hc[(long long)slot * a.ldhc + c0 + c] = (uint8_t)fq8_code(h, e);
             if (c == 0) a.hs[(long long)slot * a.ldhs + (c0 >> 5)] = (uint8_t)(e + 127);
+        }
+    };
+
+    if (EARLY) {
+        // one token: its codes are in LDS row 0 already and the first tiles are in flight (a token's expert ids
+        // are distinct, as the gate guarantees, so the group has one member)
+        if (work) {
+            start_pass(1);
+            pipeline_finish<PF>(nk_w, load, use);
+            epilogue(0, 1);
+        }
+    } else {
+        // passes of up to a.rows members (16 B columns); a group with more members than LDS rows holds (possible
+        // only when many tokens share an expert) streams the expert's weights once per pass
+        for (int base = 0; base < mg; base += a.rows) {
+            const int mp = min(a.rows, mg - base);
+            if (base > 0) __syncthreads();   // LDS rows are reused
+#pragma unroll 1
+            for (int i = tid; i < mp * per_row; i += blockDim.x) {
+                const int r = i / per_row, q = i - r * per_row;
+                v4i r0, r1;
+                x_load(s_tok[base + r], q, r0, r1);
+                x_store(r, q, r0, r1);
+            }
+            __syncthreads();
+            start_pass(mp);
+            pipelined<PF>(nk_w, load, use);
+            epilogue(base, mp);
         }
     }
 
@@ -273,10 +292,14 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const flo
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
         stride_we < (long long)2 * I * (H / 2) || stride_se < (long long)2 * I * (H / 32)) return DSV41_EINVAL;
-    // LDS holds the quantised activations of every token of a group: at most M rows
+    // M = 1: the single token's codes are staged while the routing runs (one LDS row, H / 16 <= 512 lanes).
+    // M > 1: members are staged after the bucketing, up to `rows` per pass, as many as fit in 60 KiB of LDS
+    // (two workgroups per CU)
     const size_t row_bytes = (size_t)(H + 16) + (size_t)(H / 32);
-    const int rows = M;
-    if (rows * row_bytes > UP_MAX_LDS) return DSV41_EINVAL;
+    const bool early = M == 1 && H / 16 <= UP_WAVES * 64;
+    int rows = early ? 1 : (int)((60 * 1024) / row_bytes);
+    rows = rows > 16 ? 16 : (rows > M ? M : rows);
+    if (rows < 1) return DSV41_EINVAL;
     DecodeUpArgs a{logits, ldl, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
                    stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted};
     const size_t lds = rows * row_bytes;
@@ -284,12 +307,8 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const flo
     hipStream_t st = (hipStream_t)stream;
 #define UP_LAUNCH(T, PER)                                                                                         \
     do {                                                                                                      \
-        if (lds > 64 * 1024) {                                                                                \
-            const hipError_t e = hipFuncSetAttribute((const void*)moe_decode_up_kernel<T, 8, PER>,             \
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);    \
-            if (e != hipSuccess) return (int)e;                                                               \
-        }                                                                                                     \
-        moe_decode_up_kernel<T, 8, PER><<<grid, block, lds, st>>>(a);                                         \
+        if (early) moe_decode_up_kernel<T, 8, PER, 1><<<grid, block, lds, st>>>(a);                           \
+        else moe_decode_up_kernel<T, 4, PER, 0><<<grid, block, lds, st>>>(a);                                 \
     } while (0)
     if (E <= 256) { if (tiled) UP_LAUNCH(1, 4); else UP_LAUNCH(0, 4); }
     else if (E <= 384) { if (tiled) UP_LAUNCH(1, 6); else UP_LAUNCH(0, 6); }

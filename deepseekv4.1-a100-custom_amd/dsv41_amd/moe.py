@@ -72,6 +72,8 @@ class _Workspace:
         self.wt_sorted = torch.empty(P, dtype=f32, device=dev)
         self.grp_expert = torch.empty(P, dtype=i32, device=dev)
         self.grp_start = torch.empty(P + 1, dtype=i32, device=dev)
+        self.eid = torch.empty(M, k, dtype=i32, device=dev)       # routing, when the caller keeps none
+        self.wt = torch.empty(M, k, dtype=f32, device=dev)
 
 
 _WS: dict = {}
@@ -148,9 +150,22 @@ def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor
                       score_func: str, norm: bool, ex: ExpertWeights, limit: float, ys: torch.Tensor | None = None,
                       out: torch.Tensor | None = None, y32: torch.Tensor | None = None, eid_out: torch.Tensor | None = None,
                       wt_out: torch.Tensor | None = None) -> torch.Tensor:
-    """gate_topk (fused2.py:418-452) fused into the routed experts: logits fp32 [M, E] -> routing (written to
-    eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts."""
-    ws = decode_up(xq, ex, limit, topk, logits=logits, gate=(bias, temp, route_scale, score_func, norm), eid_out=eid_out, wt_out=wt_out)
+    """gate_topk (fused2.py:418-452) with the routed experts: logits fp32 [M, E] -> routing (written to
+    eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts.
+    M = 1: the routing runs inside the up-projection launch (every workgroup routes the one token while its
+    activations load). M > 1: one gate launch first; the up projection then reads the ids (routing M tokens in
+    each of its workgroups would cost more than the extra launch)."""
+    M = xq.shape[0]
+    gate = (bias, temp, route_scale, score_func, norm)
+    if M == 1:
+        ws = decode_up(xq, ex, limit, topk, logits=logits, gate=gate, eid_out=eid_out, wt_out=wt_out)
+    else:
+        from .fused2 import gate_topk
+        ws0 = _workspace(_lib.require_cuda(xq), M, topk, ex.H, ex.I)
+        eid = ws0.eid if eid_out is None else eid_out
+        wt = ws0.wt if wt_out is None else wt_out
+        gate_topk(logits, bias, temp, topk, route_scale, score_func, norm, eid=eid, wt=wt)
+        ws = decode_up(xq, ex, limit, topk, eid=eid, wt=wt)
     return decode_down(ws, ex, ys, out, y32)
 
 

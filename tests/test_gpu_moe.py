@@ -228,6 +228,14 @@ def test_decode_up_routing_and_tables(M, func, norm):
         assert np.array_equal(got.cpu().numpy(), ref)
     ref = O.moe_layer_routed(bf16_vals(xq), eid, w_dev, *[w.cpu().numpy() for w in ws], I, 10.0)
     close(y.cpu().numpy(), ref, f"decode routed from logits M={M} {func}")
+    # the up-projection launch routing all M tokens itself (moe_route_experts uses it at M = 1 only)
+    eo2, wo2 = torch.full_like(eo, -7), torch.empty_like(wo)
+    wsp2 = moe.decode_up(xq, ex, 10.0, k, logits=lg, gate=(bs, 1.0, 2.5, func, norm), eid_out=eo2, wt_out=wo2)
+    assert torch.equal(eo2, eo) and torch.equal(wo2, wo)
+    for got, ref_t in ((wsp2.tok_sorted, tok), (wsp2.wt_sorted, wts), (wsp2.grp_expert, g_e), (wsp2.grp_start, g_s)):
+        assert np.array_equal(got.cpu().numpy(), ref_t)
+    y2 = moe.decode_down(wsp2, ex)
+    assert torch.equal(y2, y)
 
 
 @pytest.fixture(scope="module")
