@@ -33,36 +33,7 @@ struct GroupedArgs {
     int shard_start, shard_n, zero_out, min_tok, max_tok, vec_store;
     int accum;                               // 0 store, 1 add (distinct rows), 2 atomic add (rows may repeat)
     int lds_rows;                            // B_LDS: activation rows staged per pass (<= 16)
-    // B_LDS only: bf16 activations on the FP8 grid, quantised to E4M3 + E8M0 while staging (xc / xs unused)
-    const uint16_t* xbf; long long ldxb;
-    // fused SwiGLU epilogue (cnt != null): the last workgroup of group g turns the group's gate/up rows of out
-    // into h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) codes (fused.py:284-306); cnt[g] is reset to 0
-    int* cnt; const float* sw_wt; float limit; int inter;
-    uint8_t* hc; long long ldhc; uint8_t* hs; long long ldhs;
 };
-
-// SwiGLU + routing weight + bf16 + per-32 FP8 for rows [p0, p1) of gu (one 32-lane half-wave per 32 columns)
-__device__ __forceinline__ void swiglu_rows(const float* gu, long long ld_gu, const float* wt, int p0, int p1, int inter, float limit,
-                                            uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs) {
-    const int lane = threadIdx.x & 31, hw = threadIdx.x >> 5, nhw = blockDim.x >> 5;
-    const int gpr = inter >> 5;
-    for (int idx = hw; idx < (p1 - p0) * gpr; idx += nhw) {
-        const int r = p0 + idx / gpr;
-        const int c = (idx % gpr) * 32 + lane;
-        float g = __builtin_nontemporal_load(gu + (long long)r * ld_gu + c);
-        float u = __builtin_nontemporal_load(gu + (long long)r * ld_gu + inter + c);
-        if (limit > 0.f) {
-            u = fminf(fmaxf(u, -limit), limit);
-            g = fminf(g, limit);
-        }
-        float h = g * (1.0f / (1.0f + expf(-g))) * u;
-        if (wt) h = h * wt[r];
-        h = bf16_round(h);
-        const int e = fq8_exponent(wave_max32(fabsf(h)));
-        hc[(long long)r * ldhc + c] = (uint8_t)fq8_code(h, e);
-        if (lane == 0) hs[(long long)r * ldhs + (c >> 5)] = (uint8_t)(e + 127);
-    }
-}
 
 // LDS row stride for staged activation codes: +16 bytes so 16 rows fall in different banks
 __device__ __forceinline__ int lds_stride(int K) { return K + 16; }
@@ -141,31 +112,7 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
         if (active) pipeline_start<PF>(nk, load);
         if (B_LDS) {
             __syncthreads();
-            if (a.xbf) {
-                // stage rows base .. base+mp-1 from bf16, one thread per 32-element group: E4M3 codes + E8M0
-                for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
-                    const int r = i / Ks, v = i - r * Ks;
-                    const uint16_t* src = a.xbf + (long long)a.pair_tok[base + r] * a.ldxb + v * 32;
-                    v4i raw[4];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) raw[j] = ((const v4i*)src)[j];
-                    const uint16_t* hv = (const uint16_t*)raw;
-                    float amax = 0.f;
-#pragma unroll
-                    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(bf16_to_f32(hv[j])));
-                    const int e = fq8_exponent(amax);
-                    uint32_t w[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        w[j] = 0;
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) w[j] |= fq8_code(bf16_to_f32(hv[4 * j + b]), e) << (8 * b);
-                    }
-                    *(v4i*)(smem + r * LS + v * 32) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-                    *(v4i*)(smem + r * LS + v * 32 + 16) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
-                    lds_s[r * Ks + v] = (uint8_t)(e + 127);
-                }
-            } else {
+            {
                 // stage rows base .. base+mp-1: codes as 16-byte vectors, then the E8M0 bytes
                 const int vpr = K >> 4;
                 for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
@@ -197,22 +144,6 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
                 o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
             }
         }
-    }
-    if (a.cnt) {
-        // completion count of group g over its gridDim.x workgroups; the last one runs the SwiGLU epilogue
-        // (release: every workgroup's gate/up stores are made visible before its increment; acquire: the last
-        // workgroup fences after observing the final count). The count is reset for the next launch.
-        __shared__ int s_last;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            s_last = atomicAdd(a.cnt + g, 1) == (int)gridDim.x - 1;
-        }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        swiglu_rows(a.out, a.ldo, a.sw_wt, p0, p1, a.inter, a.limit, a.hc, a.ldhc, a.hs, a.ldhs);
-        if (threadIdx.x == 0) atomicExch(a.cnt + g, 0);
     }
 }
 
@@ -411,8 +342,7 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
     if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15)) return DSV41_EINVAL;
     if (G == 0) return 0;
     GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, grp_expert, grp_start, pair_tok, out, ldo, out_row, pair_wt,
-                  shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0,
-                  nullptr, 0, nullptr, nullptr, 0.f, 0, nullptr, 0, nullptr, 0};
+                  shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0};
     a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
     const int rows = max_tokens < 16 ? max_tokens : 16;
@@ -424,32 +354,6 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
     } else {
         if (use_lds) launch_grouped<0, 1>(a, G, lds, st); else launch_grouped<0, 0>(a, G, 0, st);
     }
-    return (int)hipGetLastError();
-}
-
-extern "C" int dsv41_moe_up_swiglu(const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se, int tiled,
-                                   int N, int K, int E, const uint16_t* x, long long ldx, const int* grp_expert, const int* grp_start,
-                                   int G, const int* pair_tok, int max_tokens, float* gu, long long ldgu, int* counters, const float* wt,
-                                   float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs, void* stream) {
-    if (!W13 || !S13 || !x || !grp_expert || !grp_start || !pair_tok || !gu || (counters && (!hc || !hs || !wt))) return DSV41_EINVAL;
-    if (N <= 0 || (N & 63) || K <= 0 || (K & 127) || G < 0 || ldgu < N || ldx < K || (ldx & 7) || (((uintptr_t)x) & 15) ||
-        max_tokens < 1 || E < 1)
-        return DSV41_EINVAL;
-    if (G == 0) return 0;
-    const int inter = N / 2;
-    GroupedArgs a{W13, stride_we, S13, stride_se, N, K, nullptr, 0, nullptr, 0, grp_expert, grp_start, pair_tok, gu, ldgu, nullptr, nullptr,
-                  0, E, 0, 0, 1 << 30, 0, 0, 0,   // expert ids outside [0, E) are skipped, never dereferenced
-                  x, ldx, counters, wt, limit, inter, hc, ldhc, hs, ldhs};
-    a.vec_store = ((ldgu & 3) == 0 && (((uintptr_t)gu) & 15) == 0) ? 1 : 0;
-    // activation rows staged per pass: as many as fit in 64 KiB of LDS (<= 16)
-    const size_t row_bytes = (size_t)(K + 16) + (size_t)(K / 32);
-    int rows = (int)((64 * 1024) / row_bytes);
-    rows = rows > 16 ? 16 : rows;
-    rows = rows > max_tokens ? max_tokens : rows;
-    if (rows < 1) return DSV41_EINVAL;
-    a.lds_rows = rows;
-    hipStream_t st = (hipStream_t)stream;
-    if (tiled) launch_grouped<1, 1>(a, G, rows * row_bytes, st); else launch_grouped<0, 1>(a, G, rows * row_bytes, st);
     return (int)hipGetLastError();
 }
 

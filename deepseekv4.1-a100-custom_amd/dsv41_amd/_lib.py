@@ -29,7 +29,6 @@ SIGNATURES = {
     "dsv41_quant_fp8": [P, I, LL, I, LL, I, P, P, P, P],
     "dsv41_swiglu_quant": [P, LL, P, I, I, F, P, P, P, I, P],
     "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, P, P, I, P, P, LL, P, P, I, I, I, I, I, I, I, P],
-    "dsv41_moe_up_swiglu": [P, LL, P, LL, I, I, I, I, P, LL, P, P, I, P, I, P, LL, P, P, F, P, LL, P, LL, P],
     "dsv41_moe_decode_up": [P, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P, P],
     "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P],
     "dsv41_dense_gemv_bf16": [P, LL, I, I, P, LL, I, P, LL, P, LL, P],

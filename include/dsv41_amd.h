@@ -52,18 +52,6 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
                            float* out, long long ldo, const int* out_row, const float* pair_wt, int accum, int max_tokens,
                            int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
 
-/* Decode up projection with its epilogue fused: x bf16 [rows][ldx] on the FP8 grid (fake_quant_fp8 output) is
- * quantised to E4M3 + E8M0 while staged in LDS, gu[p] = x[pair_tok[p]] . deq(W13[e_g])^T (fp32 [pairs][ldgu],
- * N = 2 * inter rows: w1 then w3), and the last workgroup of each group writes h = fq8(bf16(wt[p] *
- * silu(min(g, L)) * clamp(u, +-L))) as FP8 codes hc [pairs][ldhc] + E8M0 hs [pairs][ldhs]. E: experts in W13;
- * groups whose expert id is outside [0, E) are skipped (their rows are not written). counters: int [G],
- * zero before the first call; every call leaves them zero. counters = NULL: no epilogue (gu only). Replaces the w13 fp4_gemm_tc call and swiglu_quant
- * of decode.DecodeRuntime.experts_tc (decode.py:316-335; cukern.py:238-276; fused.py:283-345). */
-int dsv41_moe_up_swiglu(const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se, int tiled,
-                        int N, int K, int E, const uint16_t* x, long long ldx, const int* grp_expert, const int* grp_start,
-                        int G, const int* pair_tok, int max_tokens, float* gu, long long ldgu, int* counters, const float* wt,
-                        float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs, void* stream);
-
 /* Decode routing + up projection + SwiGLU in one launch (M <= 16 tokens, topk <= 16, E <= 512):
  * routing from fp32 logits [M][ldl] (gate_topk semantics, score_func 0 sqrt(softplus) / 1 sigmoid / 2 softmax;
  * bias may be NULL) or, with logits = NULL, from given eid_in / wt_in [M][topk]; the (token, expert) pairs are
