@@ -123,6 +123,31 @@ def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared
     return t, statistics.mean(uniq)
 
 
+def bench_stack(torch, dev, layers, steps, warmup, n_layers=20):
+    """batch-1 decode through n_layers independent MoE layers in one graph, with device routing.
+    Per layer: one launch for the router (x <- rmsnorm(x + y_prev), logits = G_l . x with G_l [384, 7168] bf16
+    ~N(0, 1/sqrt(7168)), fused with the FP8 fake-quantisation of x; our choice of chaining, unit norm weight),
+    then the routed experts (softmax top-8). The first len(layers) layers reuse the headline copies; the rest get
+    their own seeds. Returns (seconds per step, bytes per step)."""
+    from dsv41_amd import moe
+    stack = list(layers) + make_layers(torch, dev, n_layers - len(layers), 2000)
+    g = torch.Generator(device=dev).manual_seed(77)
+    routers = [(torch.randn(E, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16) for _ in range(n_layers)]
+    xs = [torch.randn(1, H, generator=g, device=dev).to(torch.bfloat16), torch.empty(1, H, dtype=torch.bfloat16, device=dev)]
+    xq = torch.empty(1, H, dtype=torch.bfloat16, device=dev)
+    y = torch.zeros(1, H, dtype=torch.bfloat16, device=dev)
+    part = torch.empty(H // 1024, 1, E, dtype=torch.float32, device=dev)
+
+    def step(i):
+        for l in range(n_layers):
+            moe.router_logits(xs[l % 2], y, routers[l], None, 1e-6, part=part, xn=xs[(l + 1) % 2], xq=xq)
+            moe.moe_route_experts(xq, part, None, 1.0, TOPK, 1.0, "softmax", True, stack[l], LIMIT, out=y)
+
+    t, _ = graph_time(torch, step, steps, warmup)
+    del stack, routers
+    return t, n_layers * (TOPK * expert_bytes() + E * H * 2)
+
+
 def bench_up_kernel(torch, dev, layers, steps, warmup):
     """The dominant kernel alone (dsv41_moe_decode_up at M = 1: routing + w13 + SwiGLU): average launch duration
     from HIP events on its launch stream, over the same rotating layers and fresh logits."""
@@ -232,6 +257,11 @@ def main():
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                                      "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4)}
+        ks = max(2, min(K, 10))
+        t_s, b_s = bench_stack(torch, dev, layers, ks, 1)
+        extra["stack20"] = {"workload": "configs[4]: 20 layers, batch-1 decode; per layer rmsnorm + router GEMV (one launch), then "
+                                        "gate + routed experts (two launches); one graph", "steps": ks, "us_per_step": round(t_s * 1e6, 1),
+                            "bytes_per_step": b_s, "GBps": round(b_s / t_s / 1e9, 1), "frac_hbm": round(b_s / t_s / HBM_PEAK, 4)}
     if args.calib:
         src = torch.empty(512 << 20, dtype=torch.uint8, device=dev).random_(0, 256)
         dst = torch.empty_like(src)

@@ -22,6 +22,7 @@
 
 struct DecodeUpArgs {
     const float* logits; long long ldl;      // fp32 [M][E] router logits (or NULL: eid_in / wt_in given)
+    int nparts; long long pstride;           // logits as nparts partial sums, part p at logits + p * pstride
     const float* bias; float temp; float route_scale; int score_func; int norm;
     const int* eid_in; const float* wt_in;   // precomputed routing [M][topk] when logits is NULL
     int M, topk, E;
@@ -97,7 +98,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         int ki = 0;
         float kw = 0.f;
         if (a.logits) {
-            gate_row_wave<PER>(a.logits + (long long)t * a.ldl, a.bias, E, a.temp, topk, a.route_scale, a.score_func, a.norm, &ki, &kw);
+            gate_row_wave<PER>(a.logits + (long long)t * a.ldl, a.nparts, a.pstride, a.bias, E, a.temp, topk, a.route_scale, a.score_func,
+                               a.norm, &ki, &kw);
         } else if (lane < topk) {
             ki = a.eid_in[t * topk + lane];
             kw = a.wt_in[t * topk + lane];
@@ -278,8 +280,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     }
 }
 
-extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const float* bias, float temp, float route_scale, int score_func,
-                                   int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
+extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                                   float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
                                    long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                                    int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                                    int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
@@ -288,6 +290,7 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const flo
         return DSV41_EINVAL;
     if (M < 1 || M > UP_MAXM || topk < 1 || topk > UP_MAXK || topk > E || E < 1 || E > UP_MAXE || score_func < 0 || score_func > 2)
         return DSV41_EINVAL;
+    if (logits && (nparts < 1 || (nparts > 1 && part_stride < (long long)M * ldl))) return DSV41_EINVAL;
     if (H <= 0 || (H & 255) || I <= 0 || (I & 31) || ldx < H || (ldx & 7) || (((uintptr_t)x) & 15) || (logits && ldl < E)) return DSV41_EINVAL;
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
@@ -300,7 +303,7 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, const flo
     int rows = early ? 1 : (int)((60 * 1024) / row_bytes);
     rows = rows > 16 ? 16 : (rows > M ? M : rows);
     if (rows < 1) return DSV41_EINVAL;
-    DecodeUpArgs a{logits, ldl, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
+    DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
                    stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted};
     const size_t lds = rows * row_bytes;
     const dim3 grid(I / 32, M * topk), block(UP_WAVES * 64);

@@ -9,15 +9,35 @@
 #include "common.h"
 
 template <int PER>
-__device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, const float* __restrict__ bias, int E, float temp, int topk,
-                                              float route_scale, int mode, int norm, int* out_i, float* out_w) {
+__device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, int nparts, long long pstride, const float* __restrict__ bias, int E,
+                                              float temp, int topk, float route_scale, int mode, int norm, int* out_i, float* out_w) {
     const int lane = threadIdx.x & 63;
     const int e0 = lane * PER;
     float s[PER];
     float mx = -INFINITY;
+    // the logits may arrive as nparts partial sums (a split-K router GEMV), added in ascending part order. Loads
+    // go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch).
+    constexpr int Q = PER <= 8 ? 8 : 1;
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) v[i] = 0.f;
+    for (int p0 = 0; p0 < nparts; p0 += Q) {
+        float t[Q][PER];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const long long off = (long long)min(p0 + q, nparts - 1) * pstride;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) t[q][i] = e0 + i < E ? S[off + e0 + i] : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+            if (p0 + q < nparts)
+#pragma unroll
+                for (int i = 0; i < PER; ++i) v[i] += t[q][i];
+    }
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-        s[i] = e0 + i < E ? S[e0 + i] / temp : -INFINITY;
+        s[i] = e0 + i < E ? v[i] / temp : -INFINITY;
         mx = fmaxf(mx, s[i]);
     }
     // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440

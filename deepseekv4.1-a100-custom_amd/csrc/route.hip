@@ -14,12 +14,12 @@
 #define GATE_MAX_PER_LANE 32   // E <= 2048 scores per row, held in registers (32 per lane)
 
 template <int PER>
-__global__ void __launch_bounds__(64) gate_topk_kernel(const float* __restrict__ scores, long long lds, const float* __restrict__ bias,
-                                                       int E, float temp, int topk, float route_scale, int mode, int norm,
-                                                       int* __restrict__ eid, float* __restrict__ wt) {
+__global__ void __launch_bounds__(64) gate_topk_kernel(const float* __restrict__ scores, long long lds, int nparts, long long pstride,
+                                                       const float* __restrict__ bias, int E, float temp, int topk, float route_scale,
+                                                       int mode, int norm, int* __restrict__ eid, float* __restrict__ wt) {
     int ki;
     float kw;
-    gate_row_wave<PER>(scores + (long long)blockIdx.x * lds, bias, E, temp, topk, route_scale, mode, norm, &ki, &kw);
+    gate_row_wave<PER>(scores + (long long)blockIdx.x * lds, nparts, pstride, bias, E, temp, topk, route_scale, mode, norm, &ki, &kw);
     if (threadIdx.x < topk) {
         eid[(long long)blockIdx.x * topk + threadIdx.x] = ki;
         wt[(long long)blockIdx.x * topk + threadIdx.x] = kw;
@@ -27,16 +27,19 @@ __global__ void __launch_bounds__(64) gate_topk_kernel(const float* __restrict__
 }
 
 extern "C" int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B, int E, float temp, int topk, float route_scale,
-                               int score_func, int norm, int* eid, float* wt, void* stream) {
+                               int score_func, int norm, int* eid, float* wt, int nparts, long long part_stride, void* stream) {
     if (!scores || !eid || !wt || B < 0 || E < 1 || E > 64 * GATE_MAX_PER_LANE || topk < 1 || topk > 64 || topk > E || score_func < 0 ||
-        score_func > 2 || lds < E)
+        score_func > 2 || lds < E || nparts < 1 || (nparts > 1 && part_stride < (long long)B * lds))
         return DSV41_EINVAL;
     if (B == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    if (E <= 64 * 4) gate_topk_kernel<4><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
-    else if (E <= 64 * 6) gate_topk_kernel<6><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
-    else if (E <= 64 * 8) gate_topk_kernel<8><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
-    else gate_topk_kernel<GATE_MAX_PER_LANE><<<B, 64, 0, st>>>(scores, lds, bias, E, temp, topk, route_scale, score_func, norm, eid, wt);
+#define GATE_LAUNCH(PER) \
+    gate_topk_kernel<PER><<<B, 64, 0, st>>>(scores, lds, nparts, part_stride, bias, E, temp, topk, route_scale, score_func, norm, eid, wt)
+    if (E <= 64 * 4) GATE_LAUNCH(4);
+    else if (E <= 64 * 6) GATE_LAUNCH(6);
+    else if (E <= 64 * 8) GATE_LAUNCH(8);
+    else GATE_LAUNCH(GATE_MAX_PER_LANE);
+#undef GATE_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -1,0 +1,170 @@
+// Router logits of the next MoE layer with the layer-to-layer step fused in, for M <= 16 token rows:
+//   r  = bf16(x + y)                                  (y NULL: r = x)
+//   xn = bf16(r * rsqrt(mean(r^2) + eps) * w)         (fused.rmsnorm, fused.py:92-110; w NULL = ones)
+//   logits[t][e] = sum_k xn[t][k] * G[e][k]           (the router GEMV, model.py:391-392; decode.py:357)
+// The GEMV is split along K into KS = H / 1024 parts so the 5.5 MB of router weights stream through
+// (E / 16) x KS workgroups: part[ks][t][e] holds the sum over k in [1024 ks, 1024 ks + 1024). The gate adds the KS
+// parts in ascending order (gate_row_wave's nparts), so the logits are deterministic. The workgroups also
+// write xn and xq = fake_quant_fp8(xn) (quant.py:34-54) for the experts and the next step: the workgroups of
+// row block 0 each write their own k range.
+// Each workgroup recomputes the rms statistics of all M rows (M x 28 KB of L2 reads, one round trip per row)
+// rather than waiting on another launch; its 16 x 512 weight tile is in flight meanwhile.
+#include "common.h"
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define RT_THREADS 512
+#define RT_KC 1024     // k per workgroup: 8 waves x 128
+#define RT_MAXM 16
+
+struct RouterArgs {
+    const uint16_t* x; long long ldx;
+    const uint16_t* y; long long ldy;
+    const uint16_t* w; float eps;
+    const uint16_t* G; long long ldg;   // bf16 [E][ldg]
+    int E, H, M;
+    float* part;                        // fp32 [KS][M][E]
+    uint16_t* xn; long long ldn;        // bf16 [M][H] (written by the workgroups of row block 0)
+    uint16_t* xq; long long ldq;
+};
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
+    const v4i v = *(const v4i*)p;
+    const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f[2 * j] = bf16_to_f32(w[j] & 0xFFFFu);
+        f[2 * j + 1] = bf16_to_f32(w[j] >> 16);
+    }
+}
+
+// r = bf16(x + y) for 8 consecutive elements of row t (y NULL: r = x)
+__device__ __forceinline__ void load_r8(const RouterArgs& a, int t, int k, float* f) {
+    float g[8];
+    load8(a.x + (long long)t * a.ldx + k, f);
+    if (a.y) {
+        load8(a.y + (long long)t * a.ldy + k, g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = bf16_round(f[j] + g[j]);
+    }
+}
+
+__global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArgs a) {
+    __shared__ float s_ss[RT_THREADS / 64][RT_MAXM];
+    __shared__ float s_inv[RT_MAXM];
+    __shared__ __align__(16) uint16_t s_xn[RT_MAXM][RT_KC + 8];
+    __shared__ v4f s_acc[RT_THREADS / 64][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.x, ks = blockIdx.y;
+    const int M = a.M, H = a.H, nvec = H >> 3;
+    const int col = lane & 15, kg = lane >> 4;
+    const int k0 = ks * RT_KC + wave * 128;
+
+    // this wave's weight tile (16 rows x 128 k) goes out first: 4 loads of 16 B per lane
+    v4i A[4];
+    const uint16_t* gp = a.G + (long long)(rb * 16 + col) * a.ldg + k0 + kg * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) A[i] = __builtin_nontemporal_load((const v4i*)(gp + i * 32));
+
+    // ---- sum of squares of r per row. A thread owns vectors tid, tid + 512, ... (at most 2 for H <= 8192);
+    // their loads are issued together (indices clamped, out-of-range vectors weighted 0), one round trip per row.
+    for (int t = 0; t < M; ++t) {
+        float f[2][8];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) load_r8(a, t, min(tid + u * RT_THREADS, nvec - 1) * 8, f[u]);
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const float m = tid + u * RT_THREADS < nvec ? 1.f : 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += m * f[u][j] * f[u][j];
+        }
+        ss = wave_reduce_sum(ss);
+        if (lane == 0) s_ss[wave][t] = ss;
+    }
+    // this workgroup's k range of r (128 vectors per row) is loaded before the reduction completes
+    const int nkv = RT_KC / 8;
+    const bool kmine = tid < M * nkv;       // M <= 4: one vector per thread
+    float rk[8];
+    const int kt = kmine ? tid / nkv : 0, kv = tid - kt * nkv;
+    if (M * nkv <= RT_THREADS && kmine) load_r8(a, kt, ks * RT_KC + kv * 8, rk);
+    __syncthreads();
+    if (tid < M) {
+        float tot = 0.f;
+#pragma unroll
+        for (int i = 0; i < RT_THREADS / 64; ++i) tot += s_ss[i][tid];
+        s_inv[tid] = 1.0f / sqrtf(tot / (float)H + a.eps);
+    }
+    __syncthreads();
+
+    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there
+    for (int i = tid; i < M * nkv; i += RT_THREADS) {
+        const int t = i / nkv, v = i - t * nkv;
+        const int k = ks * RT_KC + v * 8;
+        float f[8], wv[8];
+        if (M * nkv <= RT_THREADS) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = rk[j];
+        } else {
+            load_r8(a, t, k, f);
+        }
+        if (a.w) load8(a.w + k, wv);
+        float n[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) n[j] = bf16_round(f[j] * s_inv[t] * (a.w ? wv[j] : 1.f));
+        uint32_t on[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) on[j] = f32_to_bf16_bits(n[2 * j]) | (f32_to_bf16_bits(n[2 * j + 1]) << 16);
+        const v4i ov = v4i{(int)on[0], (int)on[1], (int)on[2], (int)on[3]};
+        *(v4i*)&s_xn[t][v * 8] = ov;
+        if (rb == 0) {
+            // four consecutive threads hold one FP8 group (the range and the row are multiples of 32 elements)
+            float amax = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(n[j]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, 4));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, 4));
+            const int e = fq8_exponent(amax);
+            uint32_t oq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                oq[j] = f32_to_bf16_bits(fq8_value(fq8_code(n[2 * j], e), e)) | (f32_to_bf16_bits(fq8_value(fq8_code(n[2 * j + 1], e), e)) << 16);
+            *(v4i*)(a.xn + (long long)t * a.ldn + k) = ov;
+            *(v4i*)(a.xq + (long long)t * a.ldq + k) = v4i{(int)oq[0], (int)oq[1], (int)oq[2], (int)oq[3]};
+        }
+    }
+    __syncthreads();
+
+    // ---- 4 MFMAs per wave (B column = token; columns past M read row 0 and are not stored)
+    const int brow = col < M ? col : 0;
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const v4i b = *(const v4i*)&s_xn[brow][wave * 128 + i * 32 + kg * 8];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, A[i]), __builtin_bit_cast(v8bf, b), acc, 0, 0, 0);
+    }
+    s_acc[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && col < M) {
+        v4f sum = s_acc[0][lane];
+#pragma unroll
+        for (int w = 1; w < RT_THREADS / 64; ++w) sum += s_acc[w][lane];
+        // lane l holds D[4 (l / 16) + i][l % 16]: rows = experts, column = token
+        float* o = a.part + ((long long)ks * M + col) * a.E + rb * 16 + 4 * kg;
+        o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
+    }
+}
+
+extern "C" int dsv41_router_logits(const uint16_t* x, long long ldx, const uint16_t* y, long long ldy, const uint16_t* w, float eps,
+                                   const uint16_t* G, long long ldg, int E, int H, int M, float* part, uint16_t* xn, long long ldn,
+                                   uint16_t* xq, long long ldq, void* stream) {
+    if (!x || !G || !part || !xn || !xq || M < 1 || M > RT_MAXM || E <= 0 || (E & 15) || H <= 0 || (H % RT_KC) || H > 2 * RT_THREADS * 8 ||
+        ldg < H || ldx < H ||
+        ldn < H || ldq < H || (y && ldy < H) || ((ldx | ldn | ldq | ldg | (y ? ldy : 0)) & 7) || !(eps >= 0.f) ||
+        ((((uintptr_t)x) | ((uintptr_t)y) | ((uintptr_t)w) | ((uintptr_t)G) | ((uintptr_t)xn) | ((uintptr_t)xq)) & 15))
+        return DSV41_EINVAL;
+    RouterArgs a{x, ldx, y, ldy, w, eps, G, ldg, E, H, M, part, xn, ldn, xq, ldq};
+    router_norm_kernel<<<dim3(E / 16, H / RT_KC), RT_THREADS, 0, (hipStream_t)stream>>>(a);
+    return (int)hipGetLastError();
+}

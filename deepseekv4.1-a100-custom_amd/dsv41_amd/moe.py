@@ -106,14 +106,17 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
         xq = xq.contiguous()
     ws = _workspace(dev, M, k, H, ex.I)
     if logits is not None:
+        # logits fp32 [M, E], or [parts, M, E] partial sums (dsv41_router_logits), added in part order
         bias, temp, route_scale, score_func, norm = gate
-        lg = logits if (logits.dtype == torch.float32 and logits.stride(-1) == 1) else logits.float().contiguous()
+        lg = logits if (logits.dtype == torch.float32 and logits.is_contiguous()) else logits.float().contiguous()
+        parts = lg.shape[0] if lg.dim() == 3 else 1
         b = None if bias is None else _as(bias, torch.float32)
-        assert lg.shape[-1] == ex.E and (b is None or b.numel() == ex.E)
-        route = (_lib.ptr(lg), lg.stride(0), _lib.ptr(b), float(temp), float(route_scale), _MODES[score_func], 1 if norm else 0, None, None)
+        assert lg.shape[-1] == ex.E and lg.shape[-2] == M and (b is None or b.numel() == ex.E)
+        route = (_lib.ptr(lg), ex.E, parts, M * ex.E, _lib.ptr(b), float(temp), float(route_scale), _MODES[score_func], 1 if norm else 0,
+                 None, None)
     else:
         eid32, wt32 = _as(eid, torch.int32), _as(wt, torch.float32)
-        route = (None, ex.E, None, 1.0, 1.0, 0, 0, _lib.ptr(eid32), _lib.ptr(wt32))
+        route = (None, ex.E, 1, 0, None, 1.0, 1.0, 0, 0, _lib.ptr(eid32), _lib.ptr(wt32))
     _lib.call("dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, H, ex.I, float(limit), _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0),
               _lib.ptr(eid_out), _lib.ptr(wt_out), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.tok_sorted),
@@ -183,6 +186,41 @@ def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None
     _lib.call("dsv41_dense_gemv_bf16", _lib.ptr(W), W.stride(0), N, K, _lib.ptr(x), x.stride(0), M,
               None if is_b else _lib.ptr(out), out.stride(0), _lib.ptr(out) if is_b else None, out.stride(0), _lib.stream(dev))
     return out
+
+
+def residual_rmsnorm_quant(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor | None = None, eps: float = 1e-6,
+                           xn: torch.Tensor | None = None, xq: torch.Tensor | None = None):
+    """The step between two MoE layers of the decode stack: r = bf16(x + y), xn = rmsnorm(r) * w (fused.rmsnorm,
+    fused.py:92-110), xq = fake_quant_fp8(xn). x, y, w bf16; returns (xn, xq) bf16 [M, H]."""
+    dev = _lib.require_cuda(x, y, w, xn, xq)
+    M, H = x.shape
+    assert x.dtype == y.dtype == torch.bfloat16 and y.shape == x.shape and x.stride(1) == 1 and y.stride(1) == 1
+    xn = torch.empty_like(x) if xn is None else xn
+    xq = torch.empty_like(x) if xq is None else xq
+    wc = None if w is None else w.to(torch.bfloat16).contiguous()
+    _lib.call("dsv41_residual_rmsnorm_quant", _lib.ptr(x), x.stride(0), _lib.ptr(y), y.stride(0), _lib.ptr(wc), float(eps), M, H,
+              _lib.ptr(xn), xn.stride(0), _lib.ptr(xq), xq.stride(0), _lib.stream(dev))
+    return xn, xq
+
+
+def router_logits(x: torch.Tensor, y: torch.Tensor | None, G: torch.Tensor, w: torch.Tensor | None = None, eps: float = 1e-6,
+                  part: torch.Tensor | None = None, xn: torch.Tensor | None = None, xq: torch.Tensor | None = None):
+    """The next layer's router logits with the layer-to-layer step fused in (one launch): r = bf16(x + y),
+    xn = rmsnorm(r) * w, logits = xn . G^T (bf16 G [E, H]; model.py:391-392). Returns (part, xn, xq): the logits
+    as fp32 [H / 1024, M, E] partial sums (what moe_route_experts / gate_topk accept), xn and
+    xq = fake_quant_fp8(xn) bf16 [M, H]. xn / xq must not alias x or y."""
+    dev = _lib.require_cuda(x, y, G, w, part, xn, xq)
+    M, H = x.shape
+    E = G.shape[0]
+    assert x.dtype == torch.bfloat16 and G.dtype == torch.bfloat16 and G.shape[1] == H and G.stride(1) == 1 and x.stride(1) == 1
+    part = torch.empty(H // 1024, M, E, dtype=torch.float32, device=dev) if part is None else part
+    xn = torch.empty_like(x) if xn is None else xn
+    xq = torch.empty_like(x) if xq is None else xq
+    assert part.shape == (H // 1024, M, E) and part.is_contiguous()
+    wc = None if w is None else w.to(torch.bfloat16).contiguous()
+    _lib.call("dsv41_router_logits", _lib.ptr(x), x.stride(0), _lib.ptr(y), H if y is None else y.stride(0), _lib.ptr(wc), float(eps),
+              _lib.ptr(G), G.stride(0), E, H, M, _lib.ptr(part), _lib.ptr(xn), xn.stride(0), _lib.ptr(xq), xq.stride(0), _lib.stream(dev))
+    return part, xn, xq
 
 
 class _SharedWs:

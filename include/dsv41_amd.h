@@ -54,7 +54,7 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
 
 /* Decode routing + up projection + SwiGLU in one launch (M <= 16 tokens, topk <= 16, E <= 512):
  * routing from fp32 logits [M][ldl] (gate_topk semantics, score_func 0 sqrt(softplus) / 1 sigmoid / 2 softmax;
- * bias may be NULL) or, with logits = NULL, from given eid_in / wt_in [M][topk]; the (token, expert) pairs are
+ * bias may be NULL; the logits may be nparts partial sums part_stride floats apart, added in ascending order) or, with logits = NULL, from given eid_in / wt_in [M][topk]; the (token, expert) pairs are
  * bucketed by expert (groups in ascending expert id, tokens ascending inside a group); x bf16 [M][ldx] on the
  * FP8 grid is quantised to E4M3 + E8M0 in LDS, and h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) of
  * gu = x . deq(W13[e])^T (2 * I rows: w1 then w3) is written as FP8 codes hc [P][ldhc] + E8M0 hs [P][ldhs],
@@ -63,8 +63,8 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
  * Expert ids outside [0, E) are dropped. Replaces gate_topk + moe_dispatch + the w13 fp4_gemm_tc + swiglu_quant
  * of decode.DecodeRuntime.moe2 / experts_tc (decode.py:354-361, 316-335; fused2.py:418-452; cukern.py:238-276;
  * fused.py:283-345; p2p.cu:90-132). */
-int dsv41_moe_decode_up(const float* logits, long long ldl, const float* bias, float temp, float route_scale, int score_func,
-                        int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
+int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                        float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
                         long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                         int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                         int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
@@ -88,11 +88,29 @@ int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, 
 int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int N, int K, const uint16_t* x, long long ldx, int M,
                           float* out, long long ldo, uint16_t* outb, long long ldob, void* stream);
 
+/* Layer-to-layer step of the decode stack, per token row (M rows, H <= 8192, H % 32 == 0): r = bf16(x + y),
+ * xn = bf16(r * rsqrt(mean(r^2) + eps) * w) (fused.rmsnorm, fused.py:92-110; w NULL = ones) and
+ * xq = fake_quant_fp8(xn) (quant.py:34-54), all bf16. xn feeds the next router (model.py:391-392 routes on the
+ * unquantised activations), xq the next experts. No reference entry point: it stands in for the attention
+ * block between two MoE layers when the expert path runs as a stack. */
+int dsv41_residual_rmsnorm_quant(const uint16_t* x, long long ldx, const uint16_t* y, long long ldy, const uint16_t* w, float eps,
+                                 int M, int H, uint16_t* xn, long long ldn, uint16_t* xq, long long ldq, void* stream);
+
+/* Router logits of the next layer with the layer-to-layer step fused in (M <= 16 rows, H % 1024 == 0, E % 16 == 0):
+ * r = bf16(x + y) (y NULL: r = x), xn = bf16(r * rsqrt(mean(r^2) + eps) * w) (fused.rmsnorm, fused.py:92-110;
+ * w NULL = ones), logits = xn . G^T (bf16 G [E][ldg]; model.py:391-392, decode.py:357) written as KS = H / 1024
+ * partial sums part [KS][M][E] for dsv41_gate_topk / dsv41_moe_decode_up (nparts = KS, part_stride = M * E).
+ * Also writes xn and xq = fake_quant_fp8(xn) (quant.py:34-54), bf16 [M][H]. */
+int dsv41_router_logits(const uint16_t* x, long long ldx, const uint16_t* y, long long ldy, const uint16_t* w, float eps,
+                        const uint16_t* G, long long ldg, int E, int H, int M, float* part, uint16_t* xn, long long ldn,
+                        uint16_t* xq, long long ldq, void* stream);
+
 /* MoE gate on logits: score_func 0 sqrt(softplus), 1 sigmoid, 2 softmax; top-k of scores + bias (lowest index
  * wins ties); weights renormalised when norm, times route_scale. fused2.gate_topk (fused2.py:418-471),
- * model.MoE.gate (model.py:391-404). */
+ * model.MoE.gate (model.py:391-404). nparts > 1: scores are that many partial sums part_stride floats apart
+ * (dsv41_router_logits output), added in ascending order; nparts = 1: plain scores. */
 int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B, int E, float temp, int topk, float route_scale,
-                    int score_func, int norm, int* eid, float* wt, void* stream);
+                    int score_func, int norm, int* eid, float* wt, int nparts, long long part_stride, void* stream);
 
 /* Expert bucketing of n = tokens * topk pairs: tok_sorted, wt_sorted, inv, grp_expert (-1 padded), grp_start
  * (n padded), groups of <= gmax pairs per expert; n_groups (optional) receives the group count. Pairs keep

@@ -35,6 +35,7 @@ PINS = {
     "moe_dispatch": "invariants + brute force on tiny inputs",
     "grouped_gemm": "textbook matmul against dense fp64 on tiny inputs",
     "moe_layer": "compiled reference CPU library (oracle/_ref, bf16 mode) on I = 256",
+    "residual_rmsnorm_quant": "torch.nn.functional.rms_norm (fp32, CPU) + golden-pinned fake_quant_fp8",
 }
 
 
@@ -215,6 +216,18 @@ def fake_quant_fp8(x, block: int = 32) -> np.ndarray:
     shape = np.shape(x)
     q, s = quant_fp8(x, block)
     return (q.reshape(-1, block) * s.reshape(-1, 1)).astype(F32).reshape(shape)
+
+
+def residual_rmsnorm_quant(x, y, w, eps: float):
+    """The stack's layer-to-layer step: r = bf16(x + y); xn = bf16(r * (1 / sqrt(mean(r^2) + eps)) * w)
+    (fused.py:92-110: fp32 statistics, one rounding); xq = fake_quant_fp8(xn) (quant.py:45-54).
+    Inputs are bf16 values held in fp32; returns (xn, xq) as fp32 arrays of bf16 values."""
+    r = bf16_round(np.asarray(x, F32) + np.asarray(y, F32))
+    var = (r.astype(np.float64) ** 2).sum(axis=-1, keepdims=True) / r.shape[-1]
+    inv = (1.0 / np.sqrt(var.astype(F32) + F32(eps))).astype(F32)
+    wv = np.ones(r.shape[-1], F32) if w is None else np.asarray(w, F32)
+    xn = bf16_round((r * inv * wv).astype(F32))
+    return xn, fake_quant_fp8(xn).astype(F32)
 
 
 _PERM8 = np.array([0, 4, 2, 6, 1, 5, 3, 7])

@@ -83,3 +83,21 @@ def test_swiglu_quant(limit, weighted, permute):
     c, s = fused.swiglu_quant_codes(gu.to(DEV), wt.to(DEV) if weighted else None, inter, limit)
     vals = O.e4m3_decode(c.cpu().numpy()) * np.repeat(O.e8m0_to_f32(s.cpu().numpy()), 32, axis=-1)
     assert np.array_equal(vals, got if not permute else O.unpermute_x(got))
+
+
+@pytest.mark.parametrize("M,H,weighted", [(1, 7168, False), (4, 7168, True), (3, 256, True)])
+def test_residual_rmsnorm_quant(M, H, weighted):
+    """The stack's layer-to-layer step against the oracle: xn within one bf16 ulp (fp32 sum order of the
+    variance), xq exactly fake_quant_fp8 of the kernel's own xn."""
+    from dsv41_amd import moe
+    g = torch.Generator().manual_seed(M * 31 + H)
+    x = (torch.randn(M, H, generator=g) * 2).to(torch.bfloat16)
+    y = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    w = (torch.rand(H, generator=g) + 0.5).to(torch.bfloat16) if weighted else None
+    xn, xq = moe.residual_rmsnorm_quant(x.to(DEV), y.to(DEV), None if w is None else w.to(DEV), 1e-6)
+    f = lambda t: O.bf16_bits_to_f32(u16(t.contiguous()))
+    ref_n, _ = O.residual_rmsnorm_quant(f(x), f(y), None if w is None else f(w), 1e-6)
+    got_n = f(xn)
+    assert np.all(np.abs(got_n - ref_n) <= np.abs(ref_n) * 2.0 ** -7 + 1e-30)
+    assert (got_n == ref_n).mean() > 0.99
+    assert np.array_equal(f(xq), O.fake_quant_fp8(got_n))

@@ -345,3 +345,33 @@ def test_graph_capture_replay(full_layer):
         assert torch.equal(out, eager), f"replay {i}"
         moe.moe_experts(xq, ed, wd, ex, 0.0)            # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M,with_y", [(1, True), (1, False), (5, True)])
+def test_router_logits_fused_step(M, with_y):
+    """The stack's fused router launch: xn / xq against the oracle's layer-to-layer step, the split-K logits
+    against a dense matmul of the kernel's own xn, and the gate over the partial sums (added in part order)
+    against the oracle gate on the same sums."""
+    from dsv41_amd import fused2, moe
+    E, H, k = 384, 7168, 8
+    g = torch.Generator(device=DEV).manual_seed(300 + M)
+    G = (torch.randn(E, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16)
+    x = (torch.randn(M, H, generator=g, device=DEV) * 2).to(torch.bfloat16)
+    y = torch.randn(M, H, generator=g, device=DEV).to(torch.bfloat16) if with_y else None
+    part, xn, xq = moe.router_logits(x, y, G)
+    yv = bf16_vals(y) if with_y else np.zeros((M, H), np.float32)
+    ref_n, _ = O.residual_rmsnorm_quant(bf16_vals(x), yv, None, 1e-6)
+    got_n = bf16_vals(xn)
+    assert np.all(np.abs(got_n - ref_n) <= np.abs(ref_n) * 2.0 ** -7 + 1e-30) and (got_n == ref_n).mean() > 0.99
+    assert np.array_equal(bf16_vals(xq), O.fake_quant_fp8(got_n))
+    parts = part.cpu().numpy()
+    summed = np.zeros((M, E), np.float32)
+    for p in range(parts.shape[0]):
+        summed = (summed + parts[p]).astype(np.float32)
+    dense = got_n.astype(np.float64) @ bf16_vals(G).astype(np.float64).T
+    assert np.allclose(summed, dense, rtol=1e-4, atol=1e-4)
+    eid, wt = fused2.gate_topk(part, None, 1.0, k, 1.0, "softmax", True, eid=torch.empty(M, k, dtype=torch.int32, device=DEV),
+                               wt=torch.empty(M, k, device=DEV))
+    ref_i, ref_w = O.gate_topk(summed, None, 1.0, k, 1.0, "softmax", True)
+    assert np.array_equal(eid.cpu().numpy(), ref_i)
+    assert np.allclose(wt.cpu().numpy(), ref_w, rtol=4e-6, atol=0)

@@ -189,3 +189,19 @@ def test_dequant_shortcut_matches_full_path():
     w = rng.integers(0, 256, (64, 128), dtype=np.uint8)
     s = rng.integers(2, 251, (64, 8), dtype=np.uint8)
     assert np.array_equal(O.dequant_fp4_values(w, s), O.bf16_bits_to_f32(O.dequant_fp4(w, s)))
+
+
+def test_residual_rmsnorm_quant_matches_torch_rms_norm():
+    """Closed form pin: torch's own rms_norm (fp32, CPU) on the bf16 residual sum, then the golden-pinned fq8."""
+    import torch
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(3, 512, generator=g) * 3).to(torch.bfloat16)
+    y = (torch.randn(3, 512, generator=g)).to(torch.bfloat16)
+    w = (torch.rand(512, generator=g) + 0.5).to(torch.bfloat16)
+    xn, xq = O.residual_rmsnorm_quant(x.float().numpy(), y.float().numpy(), w.float().numpy(), 1e-6)
+    r = (x + y).float()
+    ref = torch.nn.functional.rms_norm(r, (512,), w.float(), eps=1e-6).to(torch.bfloat16).float().numpy()
+    # fp32 evaluation order may move a value across a bf16 rounding boundary: at most one bf16 ulp
+    assert np.all(np.abs(xn - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+    assert (xn == ref).mean() > 0.99
+    assert np.array_equal(xq, O.fake_quant_fp8(xn))
