@@ -188,6 +188,62 @@ def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None
     return out
 
 
+class PrefillState:
+    """Intermediates of the prefill path (sorted pair order): dispatch tables, h codes + E8M0, per-pair y2."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float) -> PrefillState:
+    """First half of the prefill path: xq bf16 [T, H] on the FP8 grid -> E4M3 codes (exact); (token, expert) pairs
+    bucketed by expert in groups of <= 128 (moe_dispatch, p2p.cu:90-132); the w13 GEMM with the SwiGLU/FP8
+    epilogue: h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) (model.py:584-587, fused.py:284-306)."""
+    from .hipkern import moe_dispatch
+    from .quant import quant_fp8_e8m0
+    dev = _lib.require_cuda(xq, eid, wt)
+    T, H = xq.shape
+    k = eid.shape[-1]
+    P = T * k
+    I = ex.I
+    assert H == ex.H and xq.dtype == torch.bfloat16 and ex.E <= 512
+    xc, xs = quant_fp8_e8m0(xq)
+    tok_sorted, wt_sorted, inv, grp_expert, grp_start = moe_dispatch(eid, wt, k, ex.E, 128, dev)
+    G = min(P, ex.E + (P + 127) // 128)   # groups of <= 128 pairs: at most E + P / 128 of them
+    hc = torch.empty(P, I, dtype=torch.uint8, device=dev)
+    hs = torch.empty(P, I // 32, dtype=torch.uint8, device=dev)
+    _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
+              ex.s13.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(grp_expert), _lib.ptr(grp_start), G, _lib.ptr(tok_sorted),
+              _lib.ptr(wt_sorted), float(limit), _lib.ptr(hc), hc.stride(0), _lib.ptr(hs), hs.stride(0), _lib.stream(dev))
+    return PrefillState(T=T, k=k, P=P, G=G, tok_sorted=tok_sorted, wt_sorted=wt_sorted, inv=inv, grp_expert=grp_expert,
+                        grp_start=grp_start, hc=hc, hs=hs, y2=None)
+
+
+def prefill_down(st: PrefillState, ex: ExpertWeights, ys: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 y32: torch.Tensor | None = None) -> torch.Tensor:
+    """Second half: y2[p] = h[p] . deq(W2[e])^T (fp32 per pair, model.py:588), then y[t] = sum over the k slots of
+    t in slot order (model.py:589, view(n, k, dim).sum(1)) -> fp32 [T, H], or out = bf16(y + ys) (model.py:590-591)."""
+    dev = _lib.require_cuda(st.hc, ys, out, y32)
+    H, I, T = ex.H, ex.I, st.T
+    s = _lib.stream(dev)
+    st.y2 = torch.empty(st.P, H, dtype=torch.float32, device=dev)
+    _lib.call("dsv41_prefill_down", _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), _lib.ptr(ex.w2), ex.w2.stride(0),
+              _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), st.G,
+              _lib.ptr(st.y2), st.y2.stride(0), s)
+    if out is None and y32 is None:
+        y32 = torch.empty(T, H, dtype=torch.float32, device=dev)
+    _lib.call("dsv41_combine_pairs", _lib.ptr(st.y2), st.y2.stride(0), _lib.ptr(st.inv), st.k, T, H, _lib.ptr(ys), H if ys is None else ys.stride(0),
+              _lib.ptr(out), H if out is None else out.stride(0), _lib.ptr(y32), H if y32 is None else y32.stride(0), s)
+    return out if out is not None else y32
+
+
+def prefill_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
+                    ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed experts for many tokens (model.MoE.__call__ beyond 16 tokens, model.py:539-551, 584-591): prefill_up
+    then prefill_down. Returns fp32 [T, H], or writes out = bf16(sum + ys)."""
+    return prefill_down(prefill_up(xq, eid, wt, ex, limit), ex, ys, out, y32)
+
+
 def residual_rmsnorm_quant(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor | None = None, eps: float = 1e-6,
                            xn: torch.Tensor | None = None, xq: torch.Tensor | None = None):
     """The step between two MoE layers of the decode stack: r = bf16(x + y), xn = rmsnorm(r) * w (fused.rmsnorm,

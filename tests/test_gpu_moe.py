@@ -375,3 +375,76 @@ def test_router_logits_fused_step(M, with_y):
     ref_i, ref_w = O.gate_topk(summed, None, 1.0, k, 1.0, "softmax", True)
     assert np.array_equal(eid.cpu().numpy(), ref_i)
     assert np.allclose(wt.cpu().numpy(), ref_w, rtol=4e-6, atol=0)
+
+
+# ------------------------------------------------------------------------------------------ prefill
+def _skewed_routing(T, E, k, hot, seed):
+    """Every token routes to expert `hot` plus k - 1 others (so `hot` spans several 128-pair groups)."""
+    rng = np.random.default_rng(seed)
+    eid = np.stack([rng.permutation(np.concatenate([[hot], rng.choice([e for e in range(E) if e != hot], k - 1, replace=False)]))
+                    for _ in range(T)]).astype(np.int32)
+    lg = rng.standard_normal((T, k)).astype(np.float32)
+    wt = (np.exp(lg) / np.exp(lg).sum(1, keepdims=True)).astype(np.float32)
+    return eid, wt
+
+
+def _e4m3_values(codes, scales):
+    c = codes.cpu().numpy()
+    s = O.e8m0_to_f32(scales.cpu().numpy())
+    return O.e4m3_decode(c) * np.repeat(s, 32, axis=1)
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+@pytest.mark.parametrize("limit", [10.0, 0.0])
+def test_prefill_stages_vs_oracle(tiled, limit):
+    """Prefill stage by stage (T = 200 tokens, top-4 of 16 experts, expert 3 in every token: 200 pairs = two
+    groups). h: the oracle's SwiGLU + fq8 of gu = x . deq(W13)^T, element for element, except where fp32
+    summation order moves a value across an E4M3 rounding boundary (one code step, rare). y2: fp64 product of the
+    kernel's own h with deq(W2), tolerance of the spec. Combine: slot-ordered sum, bit-exact."""
+    from dsv41_amd import moe, quant
+    E, H, I, k, T = 16, 512, 384, 4, 200
+    ws = make_experts(E, H, I, 500 + int(tiled))
+    ex = to_ex(*ws, tiled)
+    eid, wt = _skewed_routing(T, E, k, 3, 7)
+    xq = quant.fake_quant_fp8(rand_x(T, H, 8).to(DEV))
+    st = moe.prefill_up(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, limit)
+    tok = st.tok_sorted.cpu().numpy()
+    ge, gs = st.grp_expert.cpu().numpy(), st.grp_start.cpu().numpy()
+    assert np.count_nonzero(ge == 3) == 2
+    W13, S13, W2, S2 = [w.cpu().numpy() for w in ws]
+    x = bf16_vals(xq)
+    gu = O.grouped_gemm(x, W13, S13, ge, gs, tok, int(np.count_nonzero(ge >= 0))).astype(np.float32)
+    h_ref = O.swiglu_quant(gu, st.wt_sorted.cpu().numpy(), I, limit)
+    h = _e4m3_values(st.hc, st.hs)
+    diff = h != h_ref
+    assert diff.mean() < 2e-3, f"{diff.mean():.2e} of h differs"
+    assert np.all(np.abs(h - h_ref)[diff] <= np.abs(h_ref)[diff] * 0.25 + 2.0 ** -9 * np.abs(h_ref).max())
+    y = moe.prefill_down(st, ex)
+    y2_ref = O.grouped_gemm(h, W2, S2, ge, gs, np.arange(T * k, dtype=np.int32), int(np.count_nonzero(ge >= 0)))
+    close(st.y2.cpu().numpy(), y2_ref, f"prefill w2 tiled={tiled} L={limit}")
+    inv = st.inv.cpu().numpy().reshape(T, k)
+    y2 = st.y2.cpu().numpy()
+    comb = np.zeros((T, H), np.float32)
+    for j in range(k):
+        comb = (comb + y2[inv[:, j]]).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy(), comb)
+    # bf16 output with a shared-expert term equals bf16(y32 + ys)
+    ys = rand_x(T, H, 9).to(DEV)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=DEV)
+    y32 = torch.empty(T, H, device=DEV)
+    moe.prefill_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, limit, ys=ys, out=out, y32=y32)
+    assert torch.equal(y32, y)
+    assert np.array_equal(out.view(torch.int16).cpu().numpy().view(np.uint16), O.f32_to_bf16_bits((y32.cpu().numpy() + bf16_vals(ys)).astype(np.float32)))
+
+
+def test_prefill_layer_vs_oracle():
+    """End to end at the benchmark's intermediate size (I = 1664, hidden 512, 16 experts, 300 tokens, top-8)."""
+    from dsv41_amd import moe, quant
+    E, H, I, k, T = 16, 512, 1664, 8, 300
+    ws = make_experts(E, H, I, 600)
+    ex = to_ex(*ws, True)
+    eid, wt = _skewed_routing(T, E, k, 5, 11)
+    xq = quant.fake_quant_fp8(rand_x(T, H, 12).to(DEV))
+    y = moe.prefill_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, 10.0)
+    ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, *[w.cpu().numpy() for w in ws], I, 10.0)
+    close(y.cpu().numpy(), ref, "prefill layer I=1664")
