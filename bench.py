@@ -148,6 +148,65 @@ def bench_stack(torch, dev, layers, steps, warmup, n_layers=20):
     return t, n_layers * (TOPK * expert_bytes() + E * H * 2)
 
 
+MXFP4_PEAK = 10.1e15       # MI355X dense MXFP4 MFMA, FLOP/s
+FP8_PEAK = 5.0e15          # dense FP8 rate (the fp4 x fp8 block-scaled MFMA)
+
+
+def zipf_routing(T, seed, s=1.1):
+    """configs[3] routing: Zipf(s) popularity over the 384 expert ranks, permuted by seed; 8 distinct experts per
+    token drawn without replacement proportionally to popularity; weights = softmax of per-token N(0,1) logits
+    over the 8."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    pop = 1.0 / np.arange(1, E + 1) ** s
+    pop = pop[rng.permutation(E)]
+    pop /= pop.sum()
+    eid = np.stack([rng.choice(E, TOPK, replace=False, p=pop) for _ in range(T)]).astype(np.int32)
+    lg = rng.standard_normal((T, TOPK))
+    wt = (np.exp(lg) / np.exp(lg).sum(1, keepdims=True)).astype(np.float32)
+    return eid, wt
+
+
+def bench_prefill(torch, dev, ex, T, iters=5, seed=31):
+    """prefill of T tokens (x bf16 ~N(0,1) -> FP8 fake-quant -> codes; Zipf routing) through the
+    expert path: quantise + dispatch, w13 GEMM + SwiGLU, w2 GEMM, combine. Times each stage with HIP events
+    (median over iters) and returns a dict."""
+    import numpy as np
+    from dsv41_amd import moe, quant
+    eid_np, wt_np = zipf_routing(T, seed)
+    eid, wt = torch.from_numpy(eid_np).to(dev), torch.from_numpy(wt_np).to(dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    xq = quant.fake_quant_fp8(torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16))
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    counts = np.bincount(eid_np.reshape(-1), minlength=E)
+    touched = int((counts > 0).sum())
+    flops = T * TOPK * (2 * 2 * I * H + 2 * H * I)
+    wbytes = touched * expert_bytes()
+    rec = {"total": [], "up": [], "down": []}
+    for it in range(iters + 1):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        st = moe.prefill_up(xq, eid, wt, ex, LIMIT)
+        ev[1].record()
+        moe.prefill_down(st, ex, out=out)
+        ev[2].record()
+        torch.cuda.synchronize()
+        if it > 0:
+            rec["up"].append(ev[0].elapsed_time(ev[1]) / 1e3)
+            rec["down"].append(ev[1].elapsed_time(ev[2]) / 1e3)
+            rec["total"].append(ev[0].elapsed_time(ev[2]) / 1e3)
+        del st
+    t = statistics.median(rec["total"])
+    t_hbm = wbytes / HBM_PEAK
+    return {"tokens": T, "pairs": T * TOPK, "experts_touched": touched, "max_pairs_per_expert": int(counts.max()),
+            "us": round(t * 1e6, 1), "us_up_with_quant_dispatch": round(statistics.median(rec["up"]) * 1e6, 1),
+            "us_down_with_combine": round(statistics.median(rec["down"]) * 1e6, 1), "TFLOPS": round(flops / t / 1e12, 1),
+            "frac_mxfp4_peak": round(flops / t / MXFP4_PEAK, 4), "frac_fp8_rate": round(flops / t / FP8_PEAK, 4),
+            "weight_GBps": round(wbytes / t / 1e9, 1),
+            "attainable_frac": round(max(t_hbm, flops / FP8_PEAK) / t, 4), "flop": flops, "weight_bytes": wbytes}
+
+
 def bench_up_kernel(torch, dev, layers, steps, warmup):
     """The dominant kernel alone (dsv41_moe_decode_up at M = 1: routing + w13 + SwiGLU): average launch duration
     from HIP events on its launch stream, over the same rotating layers and fresh logits."""
@@ -257,6 +316,10 @@ def main():
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                                      "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4)}
+        extra["prefill_2048"] = dict(bench_prefill(torch, dev, layers[0], 2048),
+                                     workload="configs[3]: 2048 tokens x top-8, Zipf(1.1) routing, full expert path")
+        extra["prefill_16384_probe"] = dict(bench_prefill(torch, dev, layers[1], 16384, iters=3),
+                                            workload="16,384-token probe (~341 pairs per expert)")
         ks = max(2, min(K, 10))
         t_s, b_s = bench_stack(torch, dev, layers, ks, 1)
         extra["stack20"] = {"workload": "configs[4]: 20 layers, batch-1 decode; per layer rmsnorm + router GEMV (one launch), then "

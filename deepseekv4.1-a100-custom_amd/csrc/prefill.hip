@@ -3,16 +3,13 @@
 // moe_kernels.py:127-200).
 //
 // The (token, expert) pairs arrive bucketed by expert in groups of <= 128 pairs (moe_dispatch tables, gmax 128).
-// One workgroup computes a 128-row x 128-pair tile of one group over the full K:
-//   MODE 0 (w13): rows = 64 gate rows c0 .. c0 + 63 and the matching 64 up rows I + c0 .., so the epilogue turns
-//          the tile into h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) for 64 columns (two FP8 groups) of
-//          every pair (fused.py:284-306) -- gate/up never reach HBM;
-//   MODE 1 (w2):  rows = 128 consecutive output rows; the epilogue stores fp32 y2[pair][row].
-// 8 waves: wave w owns row blocks (w & 3) and 4 + (w & 3) (a gate block and its up block in MODE 0) and the 64
-// pairs of half w >> 2, i.e. 2 x 4 MFMA accumulators. Per 128-k step a wave issues 8 MFMAs; the weight operand
-// (raw E2M1 nibbles + E8M0 bytes, as stored) streams from HBM through a PF-deep register ring, the activation
-// operand (E4M3 codes of the 128 pairs' tokens, gathered by token id) is staged into a double-buffered LDS tile
-// by all 512 threads from the same ring.
+// One workgroup computes a 256-row x 128-pair tile of one group over the full K:
+//   MODE 0 (w13): rows = 128 gate rows c0 .. c0 + 127 and the matching 128 up rows I + c0 .., so the epilogue
+//          turns the tile into h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) for 128 columns (four FP8
+//          groups) of every pair (fused.py:284-306) -- gate/up never reach HBM;
+//   MODE 1 (w2):  rows = 256 consecutive output rows; the epilogue stores fp32 y2[pair][row].
+// The weight operand is the raw E2M1 nibbles + E8M0 bytes as stored; the activation operand the E4M3 codes of the
+// group's tokens, gathered by token id.
 // Workgroup order is XCD-aware: the hardware hands workgroup i to XCD i % 8, so the linear id is remapped such
 // that each XCD walks its share of (column block, group) items group-fastest. Consecutive groups of one expert
 // (a popular expert has many) then run together on one XCD and read each weight tile from that XCD's L2.
@@ -20,8 +17,7 @@
 
 #define PG_THREADS 512
 #define PG_T 128                // pairs per tile
-#define PG_LDB (128 + 16)       // LDS row stride of a staged 128-k activation chunk (bytes)
-#define PG_PF 2                 // k-steps in flight
+#define PG_PF 3                 // minimum k-steps (K >= 384)
 
 struct PrefillArgs {
     const uint8_t* xc; long long ldx;        // E4M3 codes [rows][ldx]: activations (MODE 0) or h (MODE 1)
@@ -39,14 +35,46 @@ struct PrefillArgs {
     int g_pad;                                // G rounded up to a multiple of 8 (XCD remap)
 };
 
-template <int MODE, int TILED>
-__global__ void __launch_bounds__(PG_THREADS, 2) prefill_gemm_kernel(const PrefillArgs a) {
-    __shared__ __align__(16) uint8_t s_b[2][PG_T][PG_LDB];
-    __shared__ uint32_t s_bs[2][PG_T];           // E8M0 bytes of the k-step's four 32-k blocks, per pair
-    __shared__ int s_row[PG_T];
-    __shared__ float s_amax[8][64];
+// ------------------------------------------------------------------------------------------ direct-to-LDS variant
+// A 256-row x 128-pair tile (MODE 0: 128 gate rows + the matching 128 up rows = 128 SwiGLU columns; MODE 1: 256
+// output rows). Doubling the rows per tile halves how often each activation byte is re-read (once per column
+// block), which is what bounds the kernel once many tokens share an expert.
+// Every operand moves HBM/L2 -> LDS through the load unit itself (buffer_load ... lds / global_load_lds_dwordx4):
+// no staging registers, PV_NS k-steps (PV_NS x 33 KB) in flight per workgroup. Per k-step, with wave-uniform
+// branches only: wave w loads weight slots 2 w, 2 w + 1 (1 KB each, 16 B per lane) and token block w (two 1 KB
+// halves); waves 0-3 the E8M0 bytes of 4 weight slots each; waves 4-5 the E8M0 words of 64 pairs each.
+// A wave waits for its own loads with vmcnt (they complete in order), then a barrier makes every wave's part
+// visible. The load unit writes lane l's 16 bytes to LDS offset 16 l, and each lane chooses which 16 global
+// bytes it fetches, so the tiles land in MFMA operand order: weight slot s holds, at 16 l, the 16 bytes lane l
+// of the MFMA takes (row l % 16, k chunk l / 16); token block tb holds two 1 KB halves h = 0, 1 with, at 16 l,
+// pair 16 tb + l % 16's k chunk 4 h + l / 16. Every operand read is one contiguous 1 KB ds_read_b128 per wave.
+// Wave w computes 4 row blocks (MODE 0: gate slots 2 cg, 2 cg + 1 and their up slots, cg = w & 3, one FP8 group
+// of 32 columns) for the 64 pairs of half w >> 2: 4 x 4 accumulators, 192 B of LDS reads per lane per k-step
+// for 16 MFMAs. The operands of step k + 1 are read while the MFMAs of step k run; stage k is refilled with
+// step k + PV_NS as soon as every wave has read it.
+#define PV_NS 4
+#define PV_A 0
+#define PV_AS 16384
+#define PV_B 17408
+#define PV_BS 33792
+#define PV_STAGE 34304
+typedef __attribute__((address_space(3))) void lds_void;
 
-    // ---- XCD-aware item: each XCD walks a contiguous range of (column block, group) items, group fastest
+__device__ __forceinline__ void wait_vm(int n) {   // s_waitcnt vmcnt(n), 0 <= n <= 20
+#define PV_W(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
+    switch (n) {
+        PV_W(1) PV_W(2) PV_W(3) PV_W(4) PV_W(5) PV_W(6) PV_W(7) PV_W(8) PV_W(9) PV_W(10)
+        PV_W(11) PV_W(12) PV_W(13) PV_W(14) PV_W(15) PV_W(16) PV_W(17) PV_W(18) PV_W(19) PV_W(20)
+        default: __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); break;
+    }
+#undef PV_W
+}
+
+template <int MODE, int TILED>
+__global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];   // PV_NS stages of PV_STAGE bytes
+    __shared__ int s_row[PG_T];
+
     const int L = blockIdx.x;
     const int per_xcd = gridDim.x / 8;
     const int item = (L & 7) * per_xcd + (L >> 3);
@@ -54,147 +82,183 @@ __global__ void __launch_bounds__(PG_THREADS, 2) prefill_gemm_kernel(const Prefi
     if (g >= a.G || cb >= a.n_cb) return;
     const int e = a.grp_expert[g];
     if (e < 0 || e >= a.E) return;
-    const int p0 = a.grp_start[g], m = a.grp_start[g + 1] - p0;
+    const int p0 = a.grp_start[g], m = min(a.grp_start[g + 1] - p0, PG_T);
     if (m <= 0) return;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rsel = wave & 3, half = wave >> 2;
+    const int cg = wave & 3, ph = wave >> 2;
     const int col = lane & 15, kb = lane >> 4;
     const int K = a.K, nk = K >> 7, Kh = K >> 1, Ks = K >> 5;
-    // this wave's two 16-row weight blocks
-    int nbA, nbB;
-    if (MODE == 0) {
-        const int I = a.N >> 1;
-        nbA = (cb * 64 + 16 * rsel) >> 4;
-        nbB = (I + cb * 64 + 16 * rsel) >> 4;
-    } else {
-        nbA = (cb * 128 + 16 * rsel) >> 4;
-        nbB = nbA + 4;
-    }
+    const int I = a.N >> 1;
+    // 16-row weight block of tile slot b = 0..15 (MODE 0: slots 0-7 gate blocks, 8-15 the matching up blocks)
+    auto block_of = [&](int b) {
+        if (MODE == 0) return b < 8 ? (cb * 128 + 16 * b) >> 4 : (I + cb * 128 + 16 * (b - 8)) >> 4;
+        return cb * 16 + b;
+    };
+    int slot_of[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) slot_of[j] = MODE == 0 ? (j < 2 ? 2 * cg + j : 8 + 2 * cg + (j - 2)) : 4 * cg + j;
     const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W + (long long)e * a.stride_we, (uint32_t)a.stride_we);
     const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + (long long)e * a.stride_se, (uint32_t)a.stride_se);
-    const uint32_t wA = (uint32_t)wtile_off<TILED>(nbA, 0, nk, Kh, lane), wB = (uint32_t)wtile_off<TILED>(nbB, 0, nk, Kh, lane);
-    const uint32_t sA = (uint32_t)stile_off<TILED>(nbA, 0, nk, Ks, lane), sB = (uint32_t)stile_off<TILED>(nbB, 0, nk, Ks, lane);
-    const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
 
-    // pair rows of the tile (pairs past the group repeat its first row; their results are not stored)
     if (tid < PG_T) {
         const int p = p0 + (tid < m ? tid : 0);
         s_row[tid] = MODE == 0 ? a.row_of_pair[p] : p;
     }
     __syncthreads();
-    // staging: thread tid moves 32 bytes (k quarter q) of pair row r; threads with q == 0 also the 4 E8M0 bytes
-    const int sr_ = tid >> 2, sq = tid & 3;
-    const uint8_t* xsrc = a.xc + (long long)s_row[sr_] * a.ldx + sq * 32;
-    const uint8_t* ssrc = a.xs + (long long)s_row[sr_] * a.ldxs;
 
-    v4i RA[PG_PF], RB[PG_PF], X0[PG_PF], X1[PG_PF];
-    int SA_[PG_PF], SB_[PG_PF];
-    uint32_t XS[PG_PF];
-    auto load = [&](int slot, int kc) {
-        RA[slot] = buffer_load_tile(wr, wA, (uint32_t)(kc * ws));
-        RB[slot] = buffer_load_tile(wr, wB, (uint32_t)(kc * ws));
-        SA_[slot] = buffer_load_byte(sr, sA, (uint32_t)(kc * ss));
-        SB_[slot] = buffer_load_byte(sr, sB, (uint32_t)(kc * ss));
-        X0[slot] = *(const v4i*)(xsrc + kc * 128);
-        X1[slot] = *(const v4i*)(xsrc + kc * 128 + 16);
-        XS[slot] = sq == 0 ? *(const uint32_t*)(ssrc + kc * 4) : 0u;
+    // ---- DMA descriptors (MFMA A layout: lane l takes row l % 16, k chunk l / 16)
+    const int nbw0 = block_of(2 * wave), nbw1 = block_of(2 * wave + 1);
+    auto a_off = [&](int nb) {
+        return TILED ? (uint32_t)(nb * nk * 1024 + col * 64 + kb * 16) : (uint32_t)((nb * 16 + col) * Kh + kb * 16);
     };
-    auto stage = [&](int slot, int buf) {
-        *(v4i*)&s_b[buf][sr_][sq * 32] = X0[slot];
-        *(v4i*)&s_b[buf][sr_][sq * 32 + 16] = X1[slot];
-        if (sq == 0) s_bs[buf][sr_] = XS[slot];
-    };
-    v4f accA[4], accB[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) { accA[t] = v4f{0.f, 0.f, 0.f, 0.f}; accB[t] = accA[t]; }
-    int kstep = 0;   // k-step being consumed (slot = kstep % PG_PF)
-    auto use = [&](int slot) {
-        const int buf = kstep & 1;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int pr = half * 64 + t * 16 + col;
-            const v4i b0 = *(const v4i*)&s_b[buf][pr][kb * 16];
-            const v4i b1 = *(const v4i*)&s_b[buf][pr][64 + kb * 16];
-            const int sb = (int)(s_bs[buf][pr] >> (8 * kb));
-            const v8i bv = v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-            accA[t] = mfma_fp4w_fp8x(v8i{RA[slot].x, RA[slot].y, RA[slot].z, RA[slot].w, 0, 0, 0, 0}, bv, accA[t], SA_[slot], sb);
-            accB[t] = mfma_fp4w_fp8x(v8i{RB[slot].x, RB[slot].y, RB[slot].z, RB[slot].w, 0, 0, 0, 0}, bv, accB[t], SB_[slot], sb);
+    const uint32_t a_voff0 = a_off(nbw0), a_voff1 = a_off(nbw1);
+    const int a_ks = TILED ? 1024 : 64;
+    const int asb = block_of(4 * (wave & 3) + (lane >> 4)), asr = lane & 15;   // waves 0-3: 4 slots' scales
+    const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + asr * 4) : (uint32_t)((asb * 16 + asr) * Ks);
+    const int as_ks = TILED ? 64 : 4;
+    // MFMA B layout of token block `wave`: half h, lane l takes pair 16 wave + l % 16, k chunk 4 h + l / 16
+    const uint8_t* b0src = a.xc + (long long)s_row[16 * wave + col] * a.ldx + kb * 16;
+    const uint8_t* b1src = b0src + 64;
+    const uint8_t* bssrc = a.xs + (long long)s_row[(64 * (wave & 1) + lane) & (PG_T - 1)] * a.ldxs;
+    const bool ldb = 16 * wave < m;   // wave-uniform: the token block holds pairs of the group
+    const bool lda = wave < 4, ldbs = (wave == 4 || wave == 5) && 64 * (wave & 1) < m;
+    const int per_step = 2 + (lda ? 1 : 0) + (ldb ? 2 : 0) + (ldbs ? 1 : 0);
+    auto issue = [&](int kc, int st) {
+        uint8_t* so = smem + st * PV_STAGE;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + 2 * wave * 1024), 16, a_voff0, (uint32_t)(kc * a_ks), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + (2 * wave + 1) * 1024), 16, a_voff1, (uint32_t)(kc * a_ks), 0, 0);
+        if (lda)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
+        if (ldb) {
+            __builtin_amdgcn_global_load_lds((const void*)(b0src + kc * 128), (lds_void*)(so + PV_B + wave * 2048), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(b1src + kc * 128), (lds_void*)(so + PV_B + wave * 2048 + 1024), 16, 0, 0);
         }
-        // the next k-step's activations (loaded PF - 1 steps ago) into the other buffer, which every wave
-        // finished reading before the previous barrier
-        if (kstep + 1 < nk) stage((slot + 1) % PG_PF, buf ^ 1);
-        __syncthreads();
-        ++kstep;
+        if (ldbs)
+            __builtin_amdgcn_global_load_lds((const void*)(bssrc + kc * 4), (lds_void*)(so + PV_BS + (wave - 4) * 256), 4, 0, 0);
     };
-    // nk >= PG_PF (checked by the host): the prologue puts steps 0 .. PG_PF - 1 in flight
-    pipeline_start<PG_PF>(nk, load);
-    stage(0, 0);
-    __syncthreads();
-    pipeline_finish<PG_PF>(nk, load, use);
 
-    // ---- epilogue
-    if (MODE == 0) {
-        // lane (col, kb) of wave w holds, for pair half * 64 + 16 t + col, rows 4 kb .. 4 kb + 3 of its gate block
-        // (accA) and up block (accB): SwiGLU columns c0 + 16 rsel + 4 kb + i
-        const int I = a.N >> 1;
-        float h[4][4];
-        float am[4];
+    // ---- operand registers (double-buffered) and their LDS reads
+    const int lofs = lane * 16;
+    bool tb_on[4];   // token blocks holding pairs (wave-uniform)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int pr = half * 64 + t * 16 + col;
+    for (int u = 0; u < 4; ++u) tb_on[u] = 64 * ph + 16 * u < m;
+    v4i OA[2][4], OB0[2][4], OB1[2][4];
+    int OSA[2][4], OSB[2][4];
+    auto read_ops = [&](int kk, int r) {
+        const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
+            OSA[r][j] = st[PV_AS + slot_of[j] * 64 + col * 4 + kb];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (!tb_on[u]) continue;
+            const uint8_t* bt = st + PV_B + (4 * ph + u) * 2048 + lofs;
+            OB0[r][u] = *(const v4i*)bt;
+            OB1[r][u] = *(const v4i*)(bt + 1024);
+            OSB[r][u] = st[PV_BS + (64 * ph + 16 * u + col) * 4 + kb];
+        }
+    };
+    v4f acc[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[j][u] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&](int r) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (!tb_on[u]) continue;
+            const v8i bv = v8i{OB0[r][u].x, OB0[r][u].y, OB0[r][u].z, OB0[r][u].w, OB1[r][u].x, OB1[r][u].y, OB1[r][u].z, OB1[r][u].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[j][u] = mfma_fp4w_fp8x(v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], OSA[r][j], OSB[r][u]);
+        }
+    };
+    // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue) and
+    // one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, nk - 1) for kk = 0 and
+    // min(PV_NS - 2, nk - 1 - kk) after that.
+    auto sync_step = [&](int kk) {
+        const int after = kk == 0 ? min(PV_NS - 1, nk - 1) : min(PV_NS - 2, nk - 1 - kk);
+        wait_vm(per_step * after);
+        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+
+    for (int s0 = 0; s0 < PV_NS; ++s0)
+        if (s0 < nk) issue(s0, s0);
+    sync_step(0);
+    read_ops(0, 0);
+    for (int kk = 0; kk < nk; kk += 2) {
+        if (kk + 1 < nk) {
+            sync_step(kk + 1);                                    // every wave has read step kk: refill its stage
+            if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS);
+            read_ops(kk + 1, 1);
+        }
+        mfmas(0);
+        if (kk + 1 >= nk) break;
+        if (kk + 2 < nk) {
+            sync_step(kk + 2);
+            if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS);
+            read_ops(kk + 2, 0);
+        }
+        mfmas(1);
+    }
+    __syncthreads();
+
+    if (MODE == 0) {
+        // acc[0..1][u]: gate rows of columns cb * 128 + 32 cg + 16 j + 4 kb + i (j = 0, 1); acc[2..3][u]: up rows
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int pr = 64 * ph + 16 * u + col;
             const float wgt = pr < m ? a.wt_sorted[p0 + pr] : 0.f;
-            const float gv[4] = {accA[t].x, accA[t].y, accA[t].z, accA[t].w};
-            const float uv[4] = {accB[t].x, accB[t].y, accB[t].z, accB[t].w};
+            float h[2][4];
             float mx = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float gg = gv[i], uu = uv[i];
-                if (a.limit > 0.f) {
-                    uu = fminf(fmaxf(uu, -a.limit), a.limit);
-                    gg = fminf(gg, a.limit);
+            for (int j = 0; j < 2; ++j) {
+                const float gv[4] = {acc[j][u].x, acc[j][u].y, acc[j][u].z, acc[j][u].w};
+                const float uv[4] = {acc[2 + j][u].x, acc[2 + j][u].y, acc[2 + j][u].z, acc[2 + j][u].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float gg = gv[i], uu = uv[i];
+                    if (a.limit > 0.f) {
+                        uu = fminf(fmaxf(uu, -a.limit), a.limit);
+                        gg = fminf(gg, a.limit);
+                    }
+                    float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
+                    hv = bf16_round(hv * wgt);
+                    h[j][i] = hv;
+                    mx = fmaxf(mx, fabsf(hv));
                 }
-                float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
-                hv = bf16_round(hv * wgt);
-                h[t][i] = hv;
-                mx = fmaxf(mx, fabsf(hv));
             }
-            // max over the 16 rows of this wave: the 4 lanes holding column col (kb = 0..3)
+            // the 32 columns of pair pr sit in the 4 lanes col + 16 kb: one FP8 group
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            am[t] = mx;
-        }
-        // one FP8 group = 32 columns = the 16 rows of this wave and of its partner (rsel ^ 1)
-        if (kb == 0) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) s_amax[wave][t * 16 + col] = am[t];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int pr = half * 64 + t * 16 + col;
-            const float gmax = fmaxf(am[t], s_amax[wave ^ 1][t * 16 + col]);
-            const int ex = fq8_exponent(gmax);
+            const int ex = fq8_exponent(mx);
             if (pr < m) {
                 const long long p = p0 + pr;
-                uint32_t codes = 0;
+                const int c0 = cb * 128 + 32 * cg;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) codes |= fq8_code(h[t][i], ex) << (8 * i);
-                const int c = cb * 64 + 16 * rsel + 4 * kb;
-                *(uint32_t*)(a.hc + p * a.ldhc + c) = codes;
-                if ((rsel & 1) == 0 && kb == 0) a.hs[p * a.ldhs + (c >> 5)] = (uint8_t)(ex + 127);
+                for (int j = 0; j < 2; ++j) {
+                    uint32_t codes = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
+                    *(uint32_t*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
+                }
+                if (kb == 0) a.hs[p * a.ldhs + (c0 >> 5)] = (uint8_t)(ex + 127);
             }
         }
-        (void)I;
     } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int pr = half * 64 + t * 16 + col;
+        for (int u = 0; u < 4; ++u) {
+            const int pr = 64 * ph + 16 * u + col;
             if (pr < m) {
                 float* o = a.y + (long long)(p0 + pr) * a.ldy;
-                *(v4f*)(o + nbA * 16 + 4 * kb) = accA[t];
-                *(v4f*)(o + nbB * 16 + 4 * kb) = accB[t];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) *(v4f*)(o + block_of(slot_of[j]) * 16 + 4 * kb) = acc[j][u];
             }
         }
     }
@@ -236,8 +300,17 @@ static int launch_prefill(PrefillArgs& a, int mode, int tiled, hipStream_t st) {
     const long long items = (long long)a.n_cb * a.g_pad;   // a multiple of 8
     if (items > 0x7FFFFFFFll) return DSV41_EINVAL;
     const dim3 grid((unsigned)items), block(PG_THREADS);
-    if (mode == 0) { if (tiled) prefill_gemm_kernel<0, 1><<<grid, block, 0, st>>>(a); else prefill_gemm_kernel<0, 0><<<grid, block, 0, st>>>(a); }
-    else { if (tiled) prefill_gemm_kernel<1, 1><<<grid, block, 0, st>>>(a); else prefill_gemm_kernel<1, 0><<<grid, block, 0, st>>>(a); }
+    const size_t lds = (size_t)PV_NS * PV_STAGE;
+#define PV_LAUNCH(M, T)                                                                                               \
+    do {                                                                                                          \
+        const hipError_t err = hipFuncSetAttribute((const void*)prefill_gemm_lds_kernel<M, T>,                    \
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);         \
+        if (err != hipSuccess) return (int)err;                                                                   \
+        prefill_gemm_lds_kernel<M, T><<<grid, block, lds, st>>>(a);                                               \
+    } while (0)
+    if (mode == 0) { if (tiled) PV_LAUNCH(0, 1); else PV_LAUNCH(0, 0); }
+    else { if (tiled) PV_LAUNCH(1, 1); else PV_LAUNCH(1, 0); }
+#undef PV_LAUNCH
     return (int)hipGetLastError();
 }
 
@@ -246,7 +319,7 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
                                 const int* grp_start, int G, const int* tok_sorted, const float* wt_sorted, float limit, uint8_t* hc,
                                 long long ldhc, uint8_t* hs, long long ldhs, void* stream) {
     if (!xc || !xs || !W13 || !S13 || !grp_expert || !grp_start || !tok_sorted || !wt_sorted || !hc || !hs) return DSV41_EINVAL;
-    if (E < 1 || H < 128 * PG_PF || (H & 127) || I <= 0 || (I & 63) || G < 0 || ldx < H || (ldx & 15) || (((uintptr_t)xc) & 15) || ldxs < H / 32 ||
+    if (E < 1 || H < 128 * PG_PF || (H & 127) || I <= 0 || (I & 127) || G < 0 || ldx < H || (ldx & 15) || (((uintptr_t)xc) & 15) || ldxs < H / 32 ||
         (ldxs & 3) || (((uintptr_t)xs) & 3) || ldhc < I || (ldhc & 3) || (((uintptr_t)hc) & 3) || ldhs < I / 32)
         return DSV41_EINVAL;
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)2 * I * (H / 2) ||
@@ -254,7 +327,7 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
         return DSV41_EINVAL;
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, W13, stride_we, S13, stride_se, 2 * I, H, E, grp_expert, grp_start, G, tok_sorted, wt_sorted, limit,
-                  hc, ldhc, hs, ldhs, nullptr, 0, I / 64, 0};
+                  hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0};
     return launch_prefill(a, 0, tiled, (hipStream_t)stream);
 }
 
@@ -262,7 +335,7 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
                                   const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                                   const int* grp_start, int G, float* y2, long long ldy, void* stream) {
     if (!hc || !hs || !W2 || !S2 || !grp_expert || !grp_start || !y2) return DSV41_EINVAL;
-    if (E < 1 || H <= 0 || (H & 127) || I < 128 * PG_PF || (I & 127) || G < 0 || ldhc < I || (ldhc & 15) || (((uintptr_t)hc) & 15) || ldhs < I / 32 ||
+    if (E < 1 || H <= 0 || (H & 255) || I < 128 * PG_PF || (I & 127) || G < 0 || ldhc < I || (ldhc & 15) || (((uintptr_t)hc) & 15) || ldhs < I / 32 ||
         (ldhs & 3) || (((uintptr_t)hs) & 3) || ldy < H || (ldy & 3) || (((uintptr_t)y2) & 15))
         return DSV41_EINVAL;
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)H * (I / 2) ||
@@ -270,7 +343,7 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
         return DSV41_EINVAL;
     if (G == 0) return 0;
     PrefillArgs a{hc, ldhc, hs, ldhs, W2, stride_we, S2, stride_se, H, I, E, grp_expert, grp_start, G, nullptr, nullptr, 0.f,
-                  nullptr, 0, nullptr, 0, y2, ldy, H / 128, 0};
+                  nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0};
     return launch_prefill(a, 1, tiled, (hipStream_t)stream);
 }
 
