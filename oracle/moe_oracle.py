@@ -36,6 +36,10 @@ PINS = {
     "grouped_gemm": "textbook matmul against dense fp64 on tiny inputs",
     "moe_layer": "compiled reference CPU library (oracle/_ref, bf16 mode) on I = 256",
     "residual_rmsnorm_quant": "torch.nn.functional.rms_norm (fp32, CPU) + golden-pinned fake_quant_fp8",
+    "int8_quant_blocks": "closed form (|v - q s| <= s / 2, q range, zero block) + compiled reference CPU library (int8 mode) layer output",
+    "w4a8_gemv": "brute force on tiny inputs (integer dot by hand) + compiled reference CPU library (int8 mode) layer output",
+    "swiglu_quant_host": "compiled reference CPU library stage-2 output h (inter a multiple of 256) + golden-pinned fake_quant_fp8",
+    "host_layer": "compiled reference CPU library (oracle/_ref) gu, h and out, int8 and bf16 modes, inter a multiple of 256",
 }
 
 
@@ -419,6 +423,80 @@ def moe_layer(x_bf16_vals, eid, wt, W13, S13, W2, S2, Ws13, Ws2, inter: int, lim
     if Ws13 is not None:
         y = (y + shared_expert(xq, Ws13, Ws2, inter, limit)).astype(F32)
     return bf16_round(y)
+
+
+# --------------------------------------------------------------------------- host (CPU) int8 path
+# Twice the E2M1 value of each code: the int8 weights of the CPU library's int8 mode (moe_cpu.cpp:210-216).
+FP4_TABLE_X2 = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], dtype=np.int64)
+
+
+def int8_quant_blocks(v, block: int = 32):
+    """Per-block symmetric int8 re-quantisation of an activation (quant_x_u8, moe_cpu.cpp:218-228):
+    s = fp32(amax / 127) (s = 1 for an all-zero block), q = clamp(rint(fp32(v * fp32(1 / s))), -127, 127).
+    Returns (q int64 [..., K], s fp32 [..., K / block])."""
+    v = np.asarray(v, F32)
+    g = v.reshape(*v.shape[:-1], v.shape[-1] // block, block)
+    amax = np.abs(g).max(-1)
+    s = np.where(amax > 0, (amax / F32(127.0)).astype(F32), F32(1.0)).astype(F32)
+    inv = (F32(1.0) / s).astype(F32)
+    q = np.clip(np.rint((g * inv[..., None]).astype(F32)), -127, 127).astype(np.int64)
+    return q.reshape(v.shape), s
+
+
+def w4a8_gemv(w, s, v) -> np.ndarray:
+    """The CPU library's int8-mode GEMV (dot_row_v2 / dot_row_vnni, moe_cpu.cpp:237-301): per 32-block, the
+    exact integer dot of q (int8_quant_blocks of v) with twice the E2M1 codes of w, times 2^(scale byte - 127)
+    (byte 0 -> 0) * s_v / 2; blocks summed in float64. w [N, K/2] u8, s [N, K/32] u8, v [K] -> float64 [N]."""
+    w = np.asarray(w, np.uint8)
+    N = w.shape[0]
+    K = w.shape[1] * 2
+    codes = np.empty((N, K), np.int64)
+    codes[:, 0::2] = FP4_TABLE_X2[w & 0x0F]
+    codes[:, 1::2] = FP4_TABLE_X2[w >> 4]
+    q, sv = int8_quant_blocks(np.asarray(v, F32).reshape(K))
+    dots = (codes.reshape(N, K // 32, 32) * q.reshape(1, K // 32, 32)).sum(-1)
+    s = np.asarray(s, np.int64)
+    sw = np.where(s == 0, 0.0, np.ldexp(1.0, s - 127))
+    return (dots.astype(np.float64) * sw * (sv.astype(np.float64) * 0.5)[None, :]).sum(1)
+
+
+def swiglu_quant_host(gu, wt: float, inter: int, limit: float) -> np.ndarray:
+    """Stage 2 of the CPU library (swiglu_quant_cols, moe_cpu.cpp:357-377) in its operation order:
+    v = bf16(fp32(fp32(wt * fp32(g / (1 + exp(-g)))) * u)), then fq8 per 32 (amax floor 1e-4), over ALL inter
+    columns (the reference skips the columns past the last full 256-block, moe_cpu.cpp:444; this oracle does not).
+    gu [2 * inter] fp32 -> fp32 values of the bf16 h [inter]."""
+    gu = np.asarray(gu, F32)
+    g, u = gu[:inter].copy(), gu[inter:2 * inter].copy()
+    if limit > 0:
+        u = np.clip(u, F32(-limit), F32(limit))
+        g = np.minimum(g, F32(limit))
+    with np.errstate(over="ignore"):
+        silu = (g / (F32(1.0) + np.exp(-g).astype(F32))).astype(F32)
+    v = bf16_round(((F32(wt) * silu).astype(F32) * u).astype(F32))
+    return fake_quant_fp8(v.reshape(1, -1), 32)[0]
+
+
+def host_layer(x, ids, wts, W13, S13, W2, S2, inter: int, limit: float, int8: bool = True):
+    """One token through the CPU library's three stages (cpumoe_forward, moe_cpu.cpp:386-503), with every
+    column of h computed. x: fp32 values of the bf16 input [K]; W13 [E, 2I, K/2], W2 [E, H, I/2] (+ scales).
+    int8=True: the int8 mode (w4a8_gemv); False: exact fp32-dequantised GEMVs (mode 0, dot_row,
+    moe_cpu.cpp:177-205), both evaluated in float64. Returns (gu fp32 [n, 2I], h fp32 [n, I], out float64 [H])."""
+    x = np.asarray(x, F32)
+    gus, hs = [], []
+    out = np.zeros(W2.shape[1], np.float64)
+    for e, wt in zip(ids, wts):
+        if int8:
+            gu = w4a8_gemv(W13[e], S13[e], x).astype(F32)
+        else:
+            gu = (dense_weights(W13[e], S13[e]).astype(np.float64) @ x.astype(np.float64)).astype(F32)
+        h = swiglu_quant_host(gu, float(wt), inter, limit)
+        if int8:
+            out += w4a8_gemv(W2[e], S2[e], h)
+        else:
+            out += dense_weights(W2[e], S2[e]).astype(np.float64) @ h.astype(np.float64)
+        gus.append(gu)
+        hs.append(h)
+    return np.stack(gus), np.stack(hs), out
 
 
 def rel_l2(a, b) -> float:
