@@ -8,8 +8,10 @@ Timing: K steps captured in one hipGraph, bracketed by a synchronize on both sid
 steps rotate over 4 resident copies of the layer (separate seeds) with fresh routing each step, so the
 >= 456 MB streamed between two uses of a copy exceeds the 256 MB Infinity Cache (no MALL reuse).
 Also reported (extra keys): the full layer with the bf16 shared expert, M = 4 / 8 / 16, the
-dominant kernel's roofline (HIP events around that kernel alone, same inputs), and the reference's CPU MoE
-library (oracle/_ref, compiled from the reference sources) timed on this host's cores.
+dominant kernel's roofline (HIP events around that kernel alone, same inputs), configs[0] (one FP4 GEMV) on the
+GPU and the CPU, configs[3] prefill, configs[4] 20-layer stack, and on this host's cores the reference's CPU MoE
+library (oracle/_ref, compiled from the reference sources; cpu_baseline) beside this build's own host library
+(cpu_port).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -221,38 +223,45 @@ def bench_up_kernel(torch, dev, layers, steps, warmup):
     return t
 
 
-def cpu_baseline(steps_cap=40):
-    """The reference's CPU MoE library (dsv41/cpu/moe_cpu.cpp built by oracle/Makefile into oracle/_ref), default
-    W4A8 int8 mode (DSV41_CPU_INT8=2, cpumoe.py:36), on a bounded sample: a 48-expert subset of the configs[1]
-    layer shapes (0.91 GB, larger than the host caches), 8 experts per call with rotating ids
-    (test_cpumoe.py:32-35), median over the calls."""
-    import numpy as np
+def host_info():
+    """lscpu fields the CPU numbers depend on, and the CPUs this process may use."""
+    import subprocess
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "NUMA node(s)", "L3 cache"):
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info["cpus_allowed"] = len(os.sched_getaffinity(0))
+    return info
+
+
+def _ref_lib():
+    """The reference's CPU MoE library (dsv41/cpu/moe_cpu.cpp built by oracle/Makefile into oracle/_ref), or None."""
     lib = os.path.join(REPO, "oracle", "_ref", "libmoe_cpu_ref.so")
-    if not os.path.exists(lib):
-        return {"value": None, "note": "oracle/_ref not built"}
     flags = open("/proc/cpuinfo").read()
-    if not all(f in flags for f in ("avx512f", "avx512bw", "avx512_vnni", "avx512vbmi", "avx512_bf16")):
-        return {"value": None, "note": "host CPU lacks the AVX-512 VNNI/VBMI/BF16 ISA the reference library needs"}
-    threads = int(os.environ.get("OMP_NUM_THREADS", "16"))
-    threads = max(1, min(threads, len(os.sched_getaffinity(0))))
+    if not os.path.exists(lib) or not all(f in flags for f in ("avx512f", "avx512bw", "avx512_vnni", "avx512vbmi", "avx512_bf16")):
+        return None
     L = ctypes.CDLL(lib)
     L.cpumoe_alloc.restype = ctypes.c_void_p
     L.cpumoe_alloc.argtypes = [ctypes.c_size_t]
+    L.cpumoe_init_list.restype = ctypes.c_int
     L.cpumoe_forward_ids.restype = ctypes.c_int
     L.cpumoe_forward_ids.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_size_t] * 4 + [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                      ctypes.c_void_p, ctypes.c_void_p]
-    L.cpumoe_init(threads, threads)
-    L.cpumoe_set_int8(2)
-    Es = 48
+    return L
+
+
+def _time_layer_calls(L, bufs, Es, steps_cap, budget_s):
+    """Median time of forward_ids over 8 of Es resident experts, expert ids rotating every call
+    (test_cpumoe.py:32-35); x is N(0,1) bf16, routing weights 1/8."""
+    import numpy as np
     b13, bs13, b2, bs2 = 2 * I * (H // 2), 2 * I * (H // 32), H * (I // 2), H * (I // 32)
-    rng = np.random.default_rng(3)
-    bufs = []
-    for nbytes, lo, hi in ((Es * b13, 0, 256), (Es * bs13, 119, 124), (Es * b2, 0, 256), (Es * bs2, 119, 124)):
-        p = L.cpumoe_alloc(nbytes)
-        arr = np.frombuffer((ctypes.c_uint8 * nbytes).from_address(p), dtype=np.uint8)
-        arr[:] = rng.integers(lo, hi, nbytes, dtype=np.uint8)
-        bufs.append(p)
+    rng = np.random.default_rng(4)
     x = rng.standard_normal(H).astype(np.float32)
     xb = (x.view(np.uint32) >> 16).astype(np.uint16)
     out = np.zeros(H, np.float32)
@@ -260,7 +269,7 @@ def cpu_baseline(steps_cap=40):
     hb = np.zeros(16 * I, np.uint16)
     wts = np.full(TOPK, 1.0 / TOPK, np.float32)
     times = []
-    t_end = time.perf_counter() + 20.0
+    t_end = time.perf_counter() + budget_s
     for it in range(steps_cap):
         ids = np.array([(j * 5 + 8 * it) % Es for j in range(TOPK)], np.int32)
         t0 = time.perf_counter()
@@ -270,10 +279,109 @@ def cpu_baseline(steps_cap=40):
         assert r == 0
         if time.perf_counter() > t_end:
             break
-    med = statistics.median(times[1:] if len(times) > 1 else times)
+    return statistics.median(times[1:] if len(times) > 1 else times), len(times)
+
+
+def cpu_baselines(steps_cap=40):
+    """CPU numbers, all on the same host buffers and the same worker CPUs (this process's CPUs minus one core
+    per NUMA node, as cpumoe.default_cpu_list):
+      cpu_baseline  the reference's CPU MoE library (oracle/_ref), default W4A8 int8 mode (cpumoe.py:36), on a
+                    bounded sample of configs[1]: a 48-expert subset of the layer shapes (0.91 GB, larger than
+                    the host caches), 8 experts per call with rotating ids (test_cpumoe.py:32-35);
+      cpu_port      this build's host library (libdsv41_cpu.so), same sample and mode;
+      cpu_gemv_configs0  this build's single FP4 GEMV (configs[0], W [2048, 4096]) over 128 resident copies
+                    (571 MB, so no copy is cache-resident between uses);
+      host          lscpu fields and the library's measured DRAM read bandwidth."""
+    import numpy as np
+    from dsv41_amd import cpumoe
+    res = {"host": host_info()}
+    try:
+        M = cpumoe.load_raw()
+    except RuntimeError as err:
+        return {"value": None, "note": str(err)}, res
+    lst = cpumoe._expand(cpumoe.default_cpu_list() or ",".join(str(c) for c in sorted(os.sched_getaffinity(0))))
+    per_node = int(os.environ.get("DSV41_CORES_PER_NODE", str(len(lst))))
+    arr = (ctypes.c_int * len(lst))(*lst)
+    M.cpumoe_init_list(arr, len(lst), per_node)
+    M.cpumoe_set_int8(2)
+    res["host"]["worker_cpus"] = len(lst)
+    res["host"]["workers_pinned"] = M.cpumoe_threads_pinned()
+    bw_bytes = 1 << 30
+    pbw = M.cpumoe_alloc(bw_bytes)
+    np.frombuffer((ctypes.c_uint8 * bw_bytes).from_address(pbw), dtype=np.uint8)[:] = 1
+    res["host"]["dram_read_GBps"] = round(M.cpumoe_bw_test(pbw, bw_bytes, 5, -1), 1)
+    M.cpumoe_free(pbw, bw_bytes)
+
+    Es = 48
+    b13, bs13, b2, bs2 = 2 * I * (H // 2), 2 * I * (H // 32), H * (I // 2), H * (I // 32)
+    rng = np.random.default_rng(3)
+    sizes = (Es * b13, Es * bs13, Es * b2, Es * bs2)
+    bufs = []
+    for nbytes, (lo, hi) in zip(sizes, ((0, 256), (119, 124), (0, 256), (119, 124))):
+        p = M.cpumoe_alloc(nbytes)
+        np.frombuffer((ctypes.c_uint8 * nbytes).from_address(p), dtype=np.uint8)[:] = rng.integers(lo, hi, nbytes, dtype=np.uint8)
+        bufs.append(p)
     sel = TOPK * expert_bytes()
-    return {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": threads, "kind": "reference",
-            "sample": f"configs[1] layer shapes, 48-expert subset (0.91 GB), top-8 per call with rotating ids, median of {len(times)} calls, int8 W4A8 mode"}
+    sample = (f"configs[1] layer shapes, 48-expert subset (0.91 GB), top-8 per call with rotating ids, int8 W4A8 mode, "
+              f"{len(lst)} pinned worker CPUs")
+    baseline = {"value": None, "note": "oracle/_ref not built or host lacks its ISA"}
+    R = _ref_lib()
+    if R is not None:
+        R.cpumoe_init_list(arr, len(lst), per_node)
+        R.cpumoe_set_int8(2)
+        med, n = _time_layer_calls(R, bufs, Es, steps_cap, 20.0)
+        baseline = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
+                    "kind": "reference", "sample": sample + f", median of {n} calls"}
+    med, n = _time_layer_calls(M, bufs, Es, steps_cap, 20.0)
+    res["cpu_port"] = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
+                       "kind": "port", "sample": sample + f", median of {n} calls",
+                       "note": "libdsv41_cpu.so: this build's restatement (bit-exact with the reference library in int8 mode "
+                               "for inter % 256 == 0; computes the I = 1664 tail the reference skips)"}
+    for p, nbytes in zip(bufs, sizes):
+        M.cpumoe_free(p, nbytes)
+
+    # configs[0] on the CPU: 128 copies of W [2048, 4096] + S, rotating
+    N0, K0, copies = 2048, 4096, 128
+    wb, sb = N0 * K0 // 2, N0 * K0 // 32
+    pw, ps = M.cpumoe_alloc(copies * wb), M.cpumoe_alloc(copies * sb)
+    np.frombuffer((ctypes.c_uint8 * (copies * wb)).from_address(pw), dtype=np.uint8)[:] = rng.integers(0, 256, copies * wb, dtype=np.uint8)
+    np.frombuffer((ctypes.c_uint8 * (copies * sb)).from_address(ps), dtype=np.uint8)[:] = rng.integers(119, 124, copies * sb, dtype=np.uint8)
+    x = (rng.standard_normal(K0).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    out = np.zeros(N0, np.float32)
+    times = []
+    for it in range(3 * copies):
+        c = (it * 37) % copies
+        t0 = time.perf_counter()
+        assert M.cpumoe_gemv(pw + c * wb, ps + c * sb, N0, K0, x.ctypes.data, out.ctypes.data) == 0
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times[copies:])
+    res["cpu_gemv_configs0"] = {"us": round(med * 1e6, 1), "GBps": round((wb + sb + 2 * K0 + 4 * N0) / med / 1e9, 1), "cores": len(lst),
+                                "sample": f"median of {2 * copies} calls over 128 rotating copies (571 MB), int8 W4A8 mode"}
+    M.cpumoe_free(pw, copies * wb)
+    M.cpumoe_free(ps, copies * sb)
+    return baseline, res
+
+
+def bench_gemv_gpu(torch, dev, steps, warmup):
+    """configs[0] on the GPU: one FP4 GEMV W [2048, 4096] x fq8(x) (cukern.fp4_gemv_pairs with one pair) per step,
+    over 64 resident copies (290 MB > the 256 MB Infinity Cache); launch-bound at this size."""
+    from dsv41_amd import hipkern, quant
+    N0, K0, copies = 2048, 4096, 64
+    g = torch.Generator(device=dev).manual_seed(9)
+    w = torch.randint(0, 256, (copies, N0, K0 // 2), generator=g, dtype=torch.uint8, device=dev)
+    s = torch.randint(119, 124, (copies, N0, K0 // 32), generator=g, dtype=torch.uint8, device=dev)
+    x = quant.fake_quant_fp8(torch.randn(1, K0, generator=g, device=dev).to(torch.bfloat16))
+    row_in = torch.zeros(1, dtype=torch.int32, device=dev)
+    wt = torch.ones(1, dtype=torch.float32, device=dev)
+    ids = [torch.full((1,), c, dtype=torch.int32, device=dev) for c in range(copies)]
+
+    def step(i):
+        hipkern.fp4_gemv_pairs(x, w, s, row_in, ids[(i * 37) % copies], wt, 1)
+
+    t, _ = graph_time(torch, step, steps, warmup)
+    nbytes = N0 * K0 // 2 + N0 * K0 // 32 + 2 * K0 + 4 * N0
+    return {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1), "bytes": nbytes,
+            "note": "x quantisation + GEMV launches per step, in one graph"}
 
 
 def main():
@@ -332,7 +440,13 @@ def main():
         extra["copy_calibration"] = {"bytes_read": src.numel(), "bytes_written": dst.numel(), "us": round(t_copy * 1e6, 2),
                                      "GBps_read": round(src.numel() / t_copy / 1e9, 1)}
         del src, dst
-    cpu = {"value": None, "note": "skipped"} if args.no_cpu else cpu_baseline()
+    if not args.quick:
+        extra["gemv_configs0_gpu"] = bench_gemv_gpu(torch, dev, K, W)
+    if args.no_cpu:
+        cpu = {"value": None, "note": "skipped"}
+    else:
+        cpu, cpu_extra = cpu_baselines()
+        extra.update(cpu_extra)
     result = {
         "metric": "FP4 MoE decode us/layer + HBM TB/s; prefill grouped-GEMM MXFP4 TFLOPS",
         "value": round(value, 4),
