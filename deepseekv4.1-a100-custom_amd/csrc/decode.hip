@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ unsigned long long s_bits[UP_MAXE / 64];   // selected experts
     __shared__ int s_tok[UP_MAXM * UP_MAXK], s_slot[UP_MAXM * UP_MAXK];   // members of this workgroup's group
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
-    __shared__ int s_mg;
+    __shared__ int s_mg, s_pick;
     __shared__ v4f s_acc[UP_WAVES][64];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -92,21 +92,100 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     v4i xr0, xr1;
     if (early && tid < per_row) x_load(0, tid, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
+    if (tid == 0) s_pick = -2;
+    if (early) __syncthreads();   // s_pick is set before any wave polls it
 
-    // ---- routing for all M tokens (one wave per token), identical in every workgroup
-    for (int t = wave; t < M; t += UP_WAVES) {
-        int ki = 0;
-        float kw = 0.f;
-        if (a.logits) {
-            gate_row_wave<PER>(a.logits + (long long)t * a.ldl, a.nparts, a.pstride, a.bias, E, a.temp, topk, a.route_scale, a.score_func,
-                               a.norm, &ki, &kw);
-        } else if (lane < topk) {
-            ki = a.eid_in[t * topk + lane];
-            kw = a.wt_in[t * topk + lane];
+    // ---- this wave's weight stream: row block rb of {gate c0, gate c0 + 16, up c0, up c0 + 16}, K-half kh; the
+    // expert (the buffer descriptors) comes from the routing
+    const int g = blockIdx.y;
+    const int c0 = blockIdx.x * 32;
+    const int rbi = wave & 3, kh = wave >> 2;
+    const int row_first = (rbi < 2 ? c0 : a.I + c0) + (rbi & 1) * 16;
+    const int nb = row_first >> 4;
+    const int nk_h = nk / 2, k0c = kh * nk_h, nk_w = kh ? nk - nk_h : nk_h;
+    const uint32_t wv = (uint32_t)wtile_off<TILED>(nb, k0c, nk, Kh, lane), sv = (uint32_t)stile_off<TILED>(nb, k0c, nk, Ks, lane);
+    const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
+    const int col = lane & 15, kb = lane >> 4;
+    __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W13, 0u), sr = buffer_rsrc(a.S13, 0u);
+    auto set_expert = [&](int e) {
+        wr = buffer_rsrc(a.W13 + (long long)e * a.stride_we, (uint32_t)a.stride_we);
+        sr = buffer_rsrc(a.S13 + (long long)e * a.stride_se, (uint32_t)a.stride_se);
+    };
+    v4i A[PF];
+    int SA[PF];
+    auto load = [&](int slot, int kc) {
+        A[slot] = buffer_load_tile(wr, wv, (uint32_t)(kc * ws));
+        SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
+    };
+
+    // ---- routing, identical in every workgroup.
+    // One token (early): wave 0 runs the gate; this workgroup's expert is the g-th pick, which wave 0 posts in LDS
+    // right after round g, so every wave's weight tiles go out while the later rounds run. (Its h row is still
+    // the expert's rank in ascending id order, found by the bucketing below.)
+    // M tokens: one wave per token; the workgroup's expert is the g-th smallest selected id.
+    int eg = -1;
+    if (early) {
+        if (wave == 0) {
+            int ki = 0;
+            float kw = 0.f;   // lane k keeps pick k
+            if (a.logits) {
+                GateRow<PER> gr;
+                gr.prepare(a.logits, a.nparts, a.pstride, a.bias, E, a.temp, a.score_func);
+                float wsum = 0.f;
+                for (int k = 0; k < topk; ++k) {
+                    int id;
+                    float w;
+                    gr.pick(k, &id, &w);
+                    wsum += w;
+                    if (k == g) {
+                        eg = (id >= 0 && id < E) ? id : -1;
+                        if (lane == 0) __hip_atomic_store(&s_pick, eg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        if (eg >= 0) {
+                            set_expert(eg);
+                            pipeline_start<PF>(nk_w, load);
+                        }
+                    }
+                    if (lane == k) { ki = id; kw = w; }
+                }
+                kw = gate_weight(kw, wsum, a.route_scale, a.norm);
+            } else if (lane < topk) {
+                ki = a.eid_in[lane];
+                kw = a.wt_in[lane];
+            }
+            if (lane < topk) {
+                s_eid[lane] = (ki >= 0 && ki < E) ? ki : -1;   // out-of-range ids are dropped, never read
+                s_wt[lane] = kw;
+            }
         }
-        if (lane < topk) {
-            s_eid[t * topk + lane] = (ki >= 0 && ki < E) ? ki : -1;   // out-of-range ids are dropped, never read
-            s_wt[t * topk + lane] = kw;
+        if (!a.logits || wave != 0) {
+            if (a.logits) {
+                // the pick, posted by wave 0 (s_pick starts at -2, before the first barrier)
+                while ((eg = __hip_atomic_load(&s_pick, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == -2) __builtin_amdgcn_s_sleep(1);
+                eg = __builtin_amdgcn_readfirstlane(eg);
+            } else {
+                eg = __builtin_amdgcn_readfirstlane(a.eid_in[g]);
+                if (!(eg >= 0 && eg < E)) eg = -1;
+            }
+            if (eg >= 0) {
+                set_expert(eg);
+                pipeline_start<PF>(nk_w, load);
+            }
+        }
+    } else {
+        for (int t = wave; t < M; t += UP_WAVES) {
+            int ki = 0;
+            float kw = 0.f;
+            if (a.logits) {
+                gate_row_wave<PER>(a.logits + (long long)t * a.ldl, a.nparts, a.pstride, a.bias, E, a.temp, topk, a.route_scale, a.score_func,
+                                   a.norm, &ki, &kw);
+            } else if (lane < topk) {
+                ki = a.eid_in[t * topk + lane];
+                kw = a.wt_in[t * topk + lane];
+            }
+            if (lane < topk) {
+                s_eid[t * topk + lane] = (ki >= 0 && ki < E) ? ki : -1;   // out-of-range ids are dropped, never read
+                s_wt[t * topk + lane] = kw;
+            }
         }
     }
     if (early && tid < per_row) x_store(0, tid, xr0, xr1);
@@ -117,44 +196,25 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     }
     __syncthreads();
 
-    // ---- this workgroup's expert: the g-th smallest selected id (groups are in ascending expert order)
-    const int g = blockIdx.y;
-    int U = 0, eg = -1;
+    // ---- the selected experts (groups are in ascending expert order)
+    int U = 0, eg_sorted = -1;
 #pragma unroll
     for (int w = 0; w < UP_MAXE / 64; ++w) {
         unsigned long long bits = s_bits[w];
         bits = ((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(bits >> 32)) << 32) |
                (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)bits);
         const int c = __popcll(bits);
-        if (eg < 0 && g < U + c) {
+        if (!early && eg_sorted < 0 && g < U + c) {
             for (int r = g - U; r > 0; --r) bits &= bits - 1ull;   // drop the lower set bits
-            eg = 64 * w + (int)__builtin_ctzll(bits);
+            eg_sorted = 64 * w + (int)__builtin_ctzll(bits);
         }
         U += c;
     }
+    if (!early) eg = eg_sorted;
     const bool publish = blockIdx.x == 0 && g == 0;
-    if (g >= U && !publish) return;   // uniform: fewer distinct experts than slots
-
-    // ---- this wave's weight stream: row block rb of {gate c0, gate c0 + 16, up c0, up c0 + 16}, K-half kh
-    const int c0 = blockIdx.x * 32;
-    const int rbi = wave & 3, kh = wave >> 2;
-    const int row_first = (rbi < 2 ? c0 : a.I + c0) + (rbi & 1) * 16;
-    const int nb = row_first >> 4;
-    const int nk_h = nk / 2, k0c = kh * nk_h, nk_w = kh ? nk - nk_h : nk_h;
-    const int egw = eg < 0 ? 0 : eg;
-    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W13 + (long long)egw * a.stride_we, (uint32_t)a.stride_we);
-    const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S13 + (long long)egw * a.stride_se, (uint32_t)a.stride_se);
-    const uint32_t wv = (uint32_t)wtile_off<TILED>(nb, k0c, nk, Kh, lane), sv = (uint32_t)stile_off<TILED>(nb, k0c, nk, Ks, lane);
-    const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
-    const int col = lane & 15, kb = lane >> 4;
-    v4i A[PF];
-    int SA[PF];
-    auto load = [&](int slot, int kc) {
-        A[slot] = buffer_load_tile(wr, wv, (uint32_t)(kc * ws));
-        SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
-    };
-    const bool work = g < U;
-    if (EARLY && work) pipeline_start<PF>(nk_w, load);   // the weight tiles go out as soon as the expert is known
+    const bool work = early ? eg >= 0 : g < U;
+    if (!work && !publish) return;   // uniform: fewer experts than slots
+    if (!early && work) set_expert(eg);
 
     // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
     if (tid == 0) s_mg = 0;

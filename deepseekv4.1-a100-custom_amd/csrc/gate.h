@@ -8,94 +8,119 @@
 #pragma once
 #include "common.h"
 
+// The gate's state in one wave. prepare(): the scores and selection keys of the row; pick(k): the k-th selection
+// round (the same result in every lane). A caller can act on each expert as soon as its round is done.
 template <int PER>
-__device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, int nparts, long long pstride, const float* __restrict__ bias, int E,
-                                              float temp, int topk, float route_scale, int mode, int norm, int* out_i, float* out_w) {
-    const int lane = threadIdx.x & 63;
-    const int e0 = lane * PER;
+struct GateRow {
     float s[PER];
-    float mx = -INFINITY;
-    // the logits may arrive as nparts partial sums (a split-K router GEMV), added in ascending part order. Loads
-    // go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch).
-    constexpr int Q = PER <= 8 ? 8 : 1;
-    float v[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) v[i] = 0.f;
-    for (int p0 = 0; p0 < nparts; p0 += Q) {
-        float t[Q][PER];
-#pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            const long long off = (long long)min(p0 + q, nparts - 1) * pstride;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) t[q][i] = e0 + i < E ? S[off + e0 + i] : 0.f;
-        }
-#pragma unroll
-        for (int q = 0; q < Q; ++q)
-            if (p0 + q < nparts)
-#pragma unroll
-                for (int i = 0; i < PER; ++i) v[i] += t[q][i];
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        s[i] = e0 + i < E ? v[i] / temp : -INFINITY;
-        mx = fmaxf(mx, s[i]);
-    }
-    // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440
-    if (mode == 2) {
-        mx = wave_reduce_max(mx);
-        float sum = 0.f;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            s[i] = e0 + i < E ? expf(s[i] - mx) : 0.f;
-            sum += s[i];
-        }
-        sum = wave_reduce_sum(sum);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) s[i] = s[i] / sum;
-    } else {
-#pragma unroll
-        for (int i = 0; i < PER; ++i)
-            s[i] = mode == 1 ? 1.0f / (1.0f + expf(-s[i])) : sqrtf(s[i] > 20.f ? s[i] : log1pf(expf(s[i])));
-    }
     unsigned key[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const float v = e0 + i < E ? s[i] + (bias ? bias[e0 + i] : 0.f) : -INFINITY;
-        // invalid entries and NaN scores get key 0: every real candidate's key is larger
-        key[i] = (e0 + i < E && v == v) ? float_order_key(v) : 0u;
-    }
-    // the lane's best key, its slot (lowest on ties) and score
-    unsigned lk = 0u;
-    int li = 0;
-    float ls = 0.f;
-    auto rescan = [&]() {
+    unsigned lk;   // the lane's best remaining key, its slot (lowest on ties) and score
+    int li;
+    float ls;
+
+    __device__ __forceinline__ void rescan() {
         lk = 0u;
         li = 0;
         ls = 0.f;
 #pragma unroll
         for (int i = 0; i < PER; ++i)
             if (key[i] > lk) { lk = key[i]; li = i; ls = s[i]; }
-    };
-    rescan();
-    float wsum = 0.f, my_w = 0.f;
-    int my_i = 0;
-    for (int k = 0; k < topk; ++k) {
+    }
+
+    __device__ __forceinline__ void prepare(const float* __restrict__ S, int nparts, long long pstride, const float* __restrict__ bias, int E,
+                                            float temp, int mode) {
+        const int lane = threadIdx.x & 63;
+        const int e0 = lane * PER;
+        float mx = -INFINITY;
+        // the logits may arrive as nparts partial sums (a split-K router GEMV), added in ascending part order.
+        // Loads go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch).
+        constexpr int Q = PER <= 8 ? 8 : 1;
+        float v[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = 0.f;
+        for (int p0 = 0; p0 < nparts; p0 += Q) {
+            float t[Q][PER];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const long long off = (long long)min(p0 + q, nparts - 1) * pstride;
+#pragma unroll
+                for (int i = 0; i < PER; ++i) t[q][i] = e0 + i < E ? S[off + e0 + i] : 0.f;
+            }
+#pragma unroll
+            for (int q = 0; q < Q; ++q)
+                if (p0 + q < nparts)
+#pragma unroll
+                    for (int i = 0; i < PER; ++i) v[i] += t[q][i];
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            s[i] = e0 + i < E ? v[i] / temp : -INFINITY;
+            mx = fmaxf(mx, s[i]);
+        }
+        // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440
+        if (mode == 2) {
+            mx = wave_reduce_max(mx);
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                s[i] = e0 + i < E ? expf(s[i] - mx) : 0.f;
+                sum += s[i];
+            }
+            sum = wave_reduce_sum(sum);
+#pragma unroll
+            for (int i = 0; i < PER; ++i) s[i] = s[i] / sum;
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                s[i] = mode == 1 ? 1.0f / (1.0f + expf(-s[i])) : sqrtf(s[i] > 20.f ? s[i] : log1pf(expf(s[i])));
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const float b = e0 + i < E ? s[i] + (bias ? bias[e0 + i] : 0.f) : -INFINITY;
+            // invalid entries and NaN scores get key 0: every real candidate's key is larger
+            key[i] = (e0 + i < E && b == b) ? float_order_key(b) : 0u;
+        }
+        rescan();
+    }
+
+    // round k: the id (k when no candidate is left, every remaining score NaN, so no id is ever >= E) and score
+    __device__ __forceinline__ void pick(int k, int* id, float* w) {
+        const int lane = threadIdx.x & 63;
         const unsigned best = wave_reduce_max_u32(lk);
-        // no candidate left (every remaining score NaN): index k, so no index is ever >= E
         const unsigned long long m = __ballot(best != 0u && lk == best);
         const int owner = m ? (int)__builtin_ctzll(m) : 0;
         const int slot = __builtin_amdgcn_readlane(li, owner);
-        const int bi = m ? owner * PER + slot : k;
-        const float w = m ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner)) : 0.f;
+        *id = m ? owner * PER + slot : k;
+        *w = m ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner)) : 0.f;
         if (m && lane == owner) {
 #pragma unroll
             for (int i = 0; i < PER; ++i)
                 if (i == slot) key[i] = 0u;
             rescan();
         }
+    }
+};
+
+// the routing weight of a pick: renormalised over the topk picks (+1e-20) and scaled, fused2.py:445-450
+__device__ __forceinline__ float gate_weight(float w, float wsum, float route_scale, int norm) {
+    return norm ? w / (wsum + 1e-20f) * route_scale : w * route_scale;
+}
+
+template <int PER>
+__device__ __forceinline__ void gate_row_wave(const float* __restrict__ S, int nparts, long long pstride, const float* __restrict__ bias, int E,
+                                              float temp, int topk, float route_scale, int mode, int norm, int* out_i, float* out_w) {
+    const int lane = threadIdx.x & 63;
+    GateRow<PER> gr;
+    gr.prepare(S, nparts, pstride, bias, E, temp, mode);
+    float wsum = 0.f, my_w = 0.f;
+    int my_i = 0;
+    for (int k = 0; k < topk; ++k) {
+        int id;
+        float w;
+        gr.pick(k, &id, &w);
         wsum += w;
-        if (lane == k) { my_w = w; my_i = bi; }
+        if (lane == k) { my_w = w; my_i = id; }
     }
     *out_i = my_i;
-    *out_w = norm ? my_w / (wsum + 1e-20f) * route_scale : my_w * route_scale;
+    *out_w = gate_weight(my_w, wsum, route_scale, norm);
 }
