@@ -156,6 +156,20 @@ __device__ __forceinline__ unsigned wave_reduce_max_u32(unsigned x) {
     return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
+// wave max of unsigned values whose identity is 0: a DPP source lane that does not exist or a row the mask
+// leaves out reads 0 (old = 0, bound_ctrl), which lets the compiler fold each move into the max
+__device__ __forceinline__ unsigned wave_reduce_max_u32z(unsigned x) {
+#define DPP_MAXZ(ctrl, rmask, bmask) x = umax2(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rmask, bmask, true))
+    DPP_MAXZ(0x111, 0xF, 0xF);   // row_shr:1
+    DPP_MAXZ(0x112, 0xF, 0xF);   // row_shr:2
+    DPP_MAXZ(0x114, 0xF, 0xF);   // row_shr:4 (after shr 1, 2: lane i holds lanes i-3..i)
+    DPP_MAXZ(0x118, 0xF, 0xF);   // row_shr:8
+    DPP_MAXZ(0x142, 0xA, 0xF);   // row_bcast:15 into rows 1, 3
+    DPP_MAXZ(0x143, 0xC, 0xF);   // row_bcast:31 into rows 2, 3
+#undef DPP_MAXZ
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 // wave max of 64-bit unsigned keys (two 32-bit DPP moves per step)
 __device__ __forceinline__ unsigned long long wave_reduce_max_u64(unsigned long long x) {
 #define DPP_MAX64(ctrl, rmask, bmask)                                                                          \

@@ -83,21 +83,21 @@ struct GateRow {
         rescan();
     }
 
-    // round k: the id (k when no candidate is left, every remaining score NaN, so no id is ever >= E) and score
+    // round k: the id (k when no candidate is left, every remaining score NaN, so no id is ever >= E) and score.
+    // Branch-free: the winner's key is cleared through a per-lane bit mask and every lane rescans (only the
+    // owner's keys changed), so no scalar branch tree is built on the winning slot.
     __device__ __forceinline__ void pick(int k, int* id, float* w) {
         const int lane = threadIdx.x & 63;
-        const unsigned best = wave_reduce_max_u32(lk);
+        const unsigned best = wave_reduce_max_u32z(lk);
         const unsigned long long m = __ballot(best != 0u && lk == best);
         const int owner = m ? (int)__builtin_ctzll(m) : 0;
         const int slot = __builtin_amdgcn_readlane(li, owner);
         *id = m ? owner * PER + slot : k;
         *w = m ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ls), owner)) : 0.f;
-        if (m && lane == owner) {
+        const unsigned clear = (m && lane == owner) ? 1u << li : 0u;
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if (i == slot) key[i] = 0u;
-            rescan();
-        }
+        for (int i = 0; i < PER; ++i) key[i] = ((clear >> i) & 1u) ? 0u : key[i];
+        rescan();
     }
 };
 
