@@ -33,10 +33,10 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 E, H, I, TOPK = 384, 7168, 1664, 8
 LIMIT = 10.0               # swiglu_limit of the reference tests (test_cpumoe.py:23)
 N_COPIES = 4
-# HBM bytes per launch of the dominant kernel (moe_decode_up_kernel, M = 1): rocprofv3 FETCH_SIZE 49,709.8 KiB and
-# WRITE_SIZE 16.4 KiB per dispatch, scaled by what the same counters read for a plain 512 MiB device copy
+# HBM bytes per launch of the dominant kernel (moe_decode_up_kernel, M = 1): rocprofv3 FETCH_SIZE 49,732.6 KiB and
+# WRITE_SIZE 16.44 KiB per dispatch, scaled by what the same counters read for a plain 512 MiB device copy
 # (FETCH x 2.000, WRITE x 1.000); summary and commands in profiles/moe_decode_up_kernel__configs1_decode_m1.txt
-UP_TRAFFIC_BYTES = int(round((49709.8 * 2.0 + 16.4 * 1.0) * 1024))
+UP_TRAFFIC_BYTES = int(round((49732.6 * 2.0 + 16.44 * 1.0) * 1024))
 
 
 def expert_bytes():
@@ -384,6 +384,11 @@ def bench_gemv_gpu(torch, dev, steps, warmup):
             "note": "x quantisation + GEMV launches per step, in one graph"}
 
 
+def progress(msg):
+    """One line per finished phase on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -402,7 +407,9 @@ def main():
     eb = expert_bytes()
     sel_bytes = TOPK * eb
 
+    progress("layers resident")
     t_routed, _ = bench_decode(torch, dev, layers, K, W, 1)
+    progress(f"configs[1] decode layer {t_routed * 1e6:.2f} us")
     value = sel_bytes / t_routed / 1e12
     extra = {}
     # dominant kernel roofline: the fused up kernel at M = 1 (8 experts x (W13 + S13) bytes per launch; the
@@ -414,22 +421,26 @@ def main():
             "traffic_over_algorithmic": round(UP_TRAFFIC_BYTES / w13_bytes, 4), "avg_launch_us": round(t_up * 1e6, 2),
             "algorithmic_bytes": w13_bytes}
     extra["down_sum_us_est"] = round((t_routed - t_up) * 1e6, 2)
+    progress(f"up kernel alone {t_up * 1e6:.2f} us")
     if not args.quick:
         g = torch.Generator(device=dev).manual_seed(5)
         Ws13 = (torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)
         Ws2 = (torch.randn(H, I, generator=g, device=dev) / I ** 0.5).to(torch.bfloat16)
         t_layer, _ = bench_decode(torch, dev, layers, K, W, 1, with_shared=True, shared=(Ws13, Ws2))
         extra["layer_us_with_shared_expert"] = round(t_layer * 1e6, 2)
+        progress("layer with shared expert")
         for M in (4, 8, 16):
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                                      "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4)}
+        progress("decode M = 4 / 8 / 16")
         extra["prefill_2048"] = dict(bench_prefill(torch, dev, layers[0], 2048),
                                      workload="configs[3]: 2048 tokens x top-8, Zipf(1.1) routing, full expert path")
         extra["prefill_16384_probe"] = dict(bench_prefill(torch, dev, layers[1], 16384, iters=3),
                                             workload="16,384-token probe (~341 pairs per expert)")
         ks = max(2, min(K, 10))
         t_s, b_s = bench_stack(torch, dev, layers, ks, 1)
+        progress("prefill")
         extra["stack20"] = {"workload": "configs[4]: 20 layers, batch-1 decode; per layer rmsnorm + router GEMV (one launch), then "
                                         "gate + routed experts (two launches); one graph", "steps": ks, "us_per_step": round(t_s * 1e6, 1),
                             "bytes_per_step": b_s, "GBps": round(b_s / t_s / 1e9, 1), "frac_hbm": round(b_s / t_s / HBM_PEAK, 4)}
@@ -442,10 +453,12 @@ def main():
         del src, dst
     if not args.quick:
         extra["gemv_configs0_gpu"] = bench_gemv_gpu(torch, dev, K, W)
+        progress("configs[4] stack and configs[0] GEMV")
     if args.no_cpu:
         cpu = {"value": None, "note": "skipped"}
     else:
         cpu, cpu_extra = cpu_baselines()
+        progress("CPU baselines")
         extra.update(cpu_extra)
     result = {
         "metric": "FP4 MoE decode us/layer + HBM TB/s; prefill grouped-GEMM MXFP4 TFLOPS",
