@@ -60,6 +60,83 @@ __global__ void __launch_bounds__(256) quant_fp8_kernel(const void* __restrict__
     }
 }
 
+// The same, 16 consecutive values per thread (two threads per 32-group): 16-byte loads and one 16-byte code
+// store. Used when the pointers and strides allow 16-byte access and rows * K / 16 < 2^31.
+__global__ void __launch_bounds__(256) quant_fp8_vec_kernel(const void* __restrict__ x, int x_f32, unsigned n_chunks, int K, long long ldx,
+                                                            int permuted, uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
+                                                            void* __restrict__ fq) {
+    const unsigned t = blockIdx.x * 256u + threadIdx.x;   // 16-value chunk; a 32-group's two chunks are adjacent lanes
+    if (t >= n_chunks) return;                            // n_chunks is even, so a lane pair is active together
+    const unsigned cpr = (unsigned)K >> 4;
+    const unsigned r = t / cpr, c = t - r * cpr;
+    const int k0 = (int)c * 16;
+    float f[16];
+    if (x_f32) {
+        const v4i* src = (const v4i*)((const float*)x + (long long)r * ldx + k0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const v4i w = src[j];
+            f[4 * j] = __int_as_float(w.x); f[4 * j + 1] = __int_as_float(w.y);
+            f[4 * j + 2] = __int_as_float(w.z); f[4 * j + 3] = __int_as_float(w.w);
+        }
+    } else {
+        const v4i* src = (const v4i*)((const uint16_t*)x + (long long)r * ldx + k0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const v4i w = src[j];
+            const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[8 * j + 2 * i] = bf16_to_f32(wd[i] & 0xFFFFu);
+                f[8 * j + 2 * i + 1] = bf16_to_f32(wd[i] >> 16);
+            }
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
+    const int e = fq8_exponent(amax);
+    uint32_t q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = fq8_code(f[i], e);
+    if (codes) {
+        // natural position j holds input position (j & ~7) | bitrev3(j & 7) when the input is 8-k permuted
+        uint32_t cw[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            cw[w] = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * w + b;
+                const int src = permuted ? ((j & ~7) | ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1)) : j;
+                cw[w] |= q[src] << (8 * b);
+            }
+        }
+        *(v4i*)(codes + (long long)r * K + k0) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+    }
+    if (scales && (c & 1) == 0) scales[(long long)r * (K >> 5) + (c >> 1)] = (uint8_t)(e + 127);
+    if (fq) {
+        if (x_f32) {
+            v4i* dst = (v4i*)((float*)fq + (long long)r * K + k0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                dst[j] = v4i{__float_as_int(fq8_value(q[4 * j], e)), __float_as_int(fq8_value(q[4 * j + 1], e)),
+                             __float_as_int(fq8_value(q[4 * j + 2], e)), __float_as_int(fq8_value(q[4 * j + 3], e))};
+        } else {
+            v4i* dst = (v4i*)((uint16_t*)fq + (long long)r * K + k0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t wd[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    wd[i] = f32_to_bf16_bits(fq8_value(q[8 * j + 2 * i], e)) | (f32_to_bf16_bits(fq8_value(q[8 * j + 2 * i + 1], e)) << 16);
+                dst[j] = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------ SwiGLU
 // h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) per 32 columns (fused.py:284-306; model.py:608-613).
 // gu: fp32 [rows, ld_gu] with gate in columns [0, I) and up in [I, 2I). Outputs: FP8 codes [rows, I] and E8M0
@@ -108,7 +185,15 @@ extern "C" int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, 
     if (!x || rows < 0 || K <= 0 || (K & 31) || ldx < K || (!codes && !scales && !fq)) return DSV41_EINVAL;
     const long long groups = rows * (K / 32);
     if (groups == 0) return 0;
-    quant_fp8_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(x, x_f32, rows, K, ldx, permuted, codes, scales, fq);
+    const int esz = x_f32 ? 4 : 2;
+    const bool vec = groups * 2 < (1ll << 31) && ((ldx * esz) & 15) == 0 && (((uintptr_t)x) & 15) == 0 && (((uintptr_t)codes) & 15) == 0 &&
+                     (((uintptr_t)fq) & 15) == 0 && (K & 15) == 0;
+    if (vec) {
+        const unsigned n_chunks = (unsigned)(groups * 2);
+        quant_fp8_vec_kernel<<<(n_chunks + 255) / 256, 256, 0, (hipStream_t)stream>>>(x, x_f32, n_chunks, K, ldx, permuted, codes, scales, fq);
+    } else {
+        quant_fp8_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(x, x_f32, rows, K, ldx, permuted, codes, scales, fq);
+    }
     return (int)hipGetLastError();
 }
 

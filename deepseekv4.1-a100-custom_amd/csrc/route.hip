@@ -4,10 +4,10 @@
 // gate_topk_kernel: one workgroup per token row. Scores -> softmax / sigmoid / sqrt(softplus), + bias for the
 // selection only, TOPK rounds of a block-wide arg-max (lowest index wins ties, fused2.py:441), weights
 // renormalised (+1e-20) and scaled.
-// moe_dispatch_kernel: one workgroup, any number of pairs. Histogram (LDS atomics), exclusive scan over experts,
-// then a STABLE scatter: pairs keep ascending pair order within an expert (the reference's order is arbitrary,
-// p2p.cu:91-93; a stable order makes the tables reproducible). Rounds of blockDim pairs; within a wave the rank
-// among same-expert lanes comes from ballots, across waves from per-wave counts in LDS.
+// moe_dispatch_kernel: one workgroup per 1024 pairs. Histogram (LDS atomics), exclusive scan over experts, then a
+// STABLE scatter: pairs keep ascending pair order within an expert (the reference's order is arbitrary,
+// p2p.cu:91-93; a stable order makes the tables reproducible); within a wave the rank among same-expert lanes
+// comes from ballots, across waves from per-wave counts in LDS.
 #include "common.h"
 #include "gate.h"
 
@@ -48,97 +48,95 @@ extern "C" int dsv41_gate_topk(const float* scores, long long lds, const float* 
 #define DISP_WAVES (DISP_THREADS / WAVE)
 #define DISP_MAX_E 512
 
+// exclusive scan of v over the block's threads (fixed order); the block total lands in *total
+__device__ __forceinline__ int block_exclusive_scan(int v, int* s_scan, int* total) {
+    const int tid = threadIdx.x;
+    s_scan[tid] = v;
+    __syncthreads();
+    for (int o = 1; o < DISP_THREADS; o <<= 1) {   // Hillis-Steele inclusive scan
+        const int t = tid >= o ? s_scan[tid - o] : 0;
+        __syncthreads();
+        s_scan[tid] += t;
+        __syncthreads();
+    }
+    const int incl = s_scan[tid];
+    *total = s_scan[DISP_THREADS - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+// Workgroup b places the pairs of chunk b = [b * 1024, b * 1024 + 1024). It reads every expert id (a few tens of
+// KB, L2-resident) to histogram both all pairs and the pairs before its chunk, so each workgroup knows where its
+// pairs go without a second launch or scratch memory: pos = start[e] + (pairs of e before the chunk) + (rank of
+// the pair among the chunk's pairs of e), ranks from ballots within a wave and per-wave counts across waves.
+// Workgroup 0 also writes the group tables.
 __global__ void __launch_bounds__(DISP_THREADS) moe_dispatch_kernel(const int* __restrict__ eid, const float* __restrict__ wt, int n, int topk,
                                                                     int E, int gmax, int* __restrict__ tok_sorted, float* __restrict__ wt_sorted,
                                                                     int* __restrict__ inv, int* __restrict__ grp_expert, int* __restrict__ grp_start,
                                                                     int* __restrict__ n_groups) {
-    __shared__ int s_count[DISP_MAX_E], s_start[DISP_MAX_E], s_cursor[DISP_MAX_E], s_gbase[DISP_MAX_E];
+    __shared__ int s_count[DISP_MAX_E], s_before[DISP_MAX_E], s_start[DISP_MAX_E], s_gbase[DISP_MAX_E];
     __shared__ unsigned short s_wcnt[DISP_WAVES][DISP_MAX_E];
     __shared__ int s_scan[DISP_THREADS];
-    __shared__ int s_total_groups;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += DISP_THREADS) { s_count[e] = 0; s_cursor[e] = 0; }
+    const int c0 = blockIdx.x * DISP_THREADS;
+    for (int e = tid; e < E; e += DISP_THREADS) { s_count[e] = 0; s_before[e] = 0; }
+    for (int i = tid; i < DISP_WAVES * E; i += DISP_THREADS) s_wcnt[i / E][i % E] = 0;
     __syncthreads();
     for (int p = tid; p < n; p += DISP_THREADS) {
         const int e = eid[p];
-        if (e >= 0 && e < E) atomicAdd(&s_count[e], 1);
+        if (e >= 0 && e < E) {
+            atomicAdd(&s_count[e], 1);
+            if (p < c0) atomicAdd(&s_before[e], 1);
+        }
     }
     __syncthreads();
-    // exclusive scans of counts and group counts over experts: each thread owns a contiguous run of experts
+    // exclusive scans of the counts and of the group counts over experts: thread t owns a contiguous run
     const int per = (E + DISP_THREADS - 1) / DISP_THREADS;
     const int e0 = tid * per, e1 = min(E, e0 + per);
     int cs = 0, gsum = 0;
     for (int e = e0; e < e1; ++e) { cs += s_count[e]; gsum += (s_count[e] + gmax - 1) / gmax; }
-    s_scan[tid] = cs;
-    __syncthreads();
-    for (int o = 1; o < DISP_THREADS; o <<= 1) {  // Hillis-Steele inclusive scan
-        const int v = tid >= o ? s_scan[tid - o] : 0;
-        __syncthreads();
-        s_scan[tid] += v;
-        __syncthreads();
-    }
-    int run = s_scan[tid] - cs;
-    __syncthreads();
-    s_scan[tid] = gsum;
-    __syncthreads();
-    for (int o = 1; o < DISP_THREADS; o <<= 1) {
-        const int v = tid >= o ? s_scan[tid - o] : 0;
-        __syncthreads();
-        s_scan[tid] += v;
-        __syncthreads();
-    }
-    int grun = s_scan[tid] - gsum;
+    int total_pairs, total_groups;
+    int run = block_exclusive_scan(cs, s_scan, &total_pairs);
+    int grun = block_exclusive_scan(gsum, s_scan, &total_groups);
     for (int e = e0; e < e1; ++e) {
         s_start[e] = run;
         s_gbase[e] = grun;
         run += s_count[e];
         grun += (s_count[e] + gmax - 1) / gmax;
     }
-    if (tid == DISP_THREADS - 1) s_total_groups = s_scan[tid];
     __syncthreads();
-    // stable scatter, one round of DISP_THREADS pairs at a time (E <= 512 for the per-wave count table)
+    // stable scatter of this chunk
     const unsigned long long below = (lane == 63) ? ~0ull >> 1 : ((1ull << lane) - 1ull);
-    for (int base = 0; base < n; base += DISP_THREADS) {
-        const int p = base + tid;
-        const bool valid = p < n;
-        const int e = valid ? eid[p] : -1;
-        const bool real = valid && e >= 0 && e < E;
-        // rank among this wave's lanes with the same expert, and the wave's count per expert
-        int rank = 0, cnt = 0;
-        unsigned long long todo = __ballot(real);
-        while (todo) {
-            const int leader = __ffsll((long long)todo) - 1;
-            const int le = __shfl(e, leader);
-            const unsigned long long m = __ballot(real && e == le);
-            if (real && e == le) { rank = __popcll(m & below); cnt = __popcll(m); }
-            todo &= ~m;
-        }
-        for (int i = tid; i < DISP_WAVES * E; i += DISP_THREADS) s_wcnt[i / E][i % E] = 0;
-        __syncthreads();
-        if (real && rank == 0) s_wcnt[wave][e] = (unsigned short)cnt;
-        __syncthreads();
-        if (real) {
-            int before = 0;
-            for (int w = 0; w < wave; ++w) before += s_wcnt[w][e];
-            const int pos = s_start[e] + s_cursor[e] + before + rank;
-            tok_sorted[pos] = p / topk;
-            wt_sorted[pos] = wt ? wt[p] : 1.f;
-            inv[p] = pos;
-        }
-        __syncthreads();
-        for (int ee = tid; ee < E; ee += DISP_THREADS) {
-            int add = 0;
-            for (int w = 0; w < DISP_WAVES; ++w) add += s_wcnt[w][ee];
-            s_cursor[ee] += add;
-        }
-        __syncthreads();
+    const int p = c0 + tid;
+    const bool valid = p < n;
+    const int e = valid ? eid[p] : -1;
+    const bool real = valid && e >= 0 && e < E;
+    int rank = 0, cnt = 0;
+    unsigned long long todo = __ballot(real);
+    while (todo) {
+        const int leader = __ffsll((long long)todo) - 1;
+        const int le = __shfl(e, leader);
+        const unsigned long long m = __ballot(real && e == le);
+        if (real && e == le) { rank = __popcll(m & below); cnt = __popcll(m); }
+        todo &= ~m;
     }
+    if (real && rank == 0) s_wcnt[wave][e] = (unsigned short)cnt;
+    __syncthreads();
+    if (real) {
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += s_wcnt[w][e];
+        const int pos = s_start[e] + s_before[e] + before + rank;
+        tok_sorted[pos] = p / topk;
+        wt_sorted[pos] = wt ? wt[p] : 1.f;
+        inv[p] = pos;
+    }
+    if (blockIdx.x != 0) return;
     // groups of <= gmax pairs per expert, then padding (p2p.cu:124-131)
-    for (int e = tid; e < E; e += DISP_THREADS) {
-        const int ng = (s_count[e] + gmax - 1) / gmax;
-        for (int g = 0; g < ng; ++g) { grp_expert[s_gbase[e] + g] = e; grp_start[s_gbase[e] + g] = s_start[e] + g * gmax; }
+    for (int ee = tid; ee < E; ee += DISP_THREADS) {
+        const int ng = (s_count[ee] + gmax - 1) / gmax;
+        for (int g = 0; g < ng; ++g) { grp_expert[s_gbase[ee] + g] = ee; grp_start[s_gbase[ee] + g] = s_start[ee] + g * gmax; }
     }
-    const int G = s_total_groups;
+    const int G = total_groups;
     for (int g = G + tid; g < n; g += DISP_THREADS) { grp_expert[g] = -1; grp_start[g] = n; }
     if (tid == 0) {
         grp_start[G] = n;
@@ -151,6 +149,8 @@ extern "C" int dsv41_moe_dispatch(const int* eid, const float* wt, int n, int to
                                   int* inv, int* grp_expert, int* grp_start, int* n_groups, void* stream) {
     if (!eid || !tok_sorted || !wt_sorted || !inv || !grp_expert || !grp_start || n < 0 || topk < 1 || E < 1 || E > 512 || gmax < 1)
         return DSV41_EINVAL;
-    moe_dispatch_kernel<<<1, DISP_THREADS, 0, (hipStream_t)stream>>>(eid, wt, n, topk, E, gmax, tok_sorted, wt_sorted, inv, grp_expert, grp_start, n_groups);
+    const int blocks = n > 0 ? (n + DISP_THREADS - 1) / DISP_THREADS : 1;   // one workgroup writes the (empty) tables when n == 0
+    moe_dispatch_kernel<<<blocks, DISP_THREADS, 0, (hipStream_t)stream>>>(eid, wt, n, topk, E, gmax, tok_sorted, wt_sorted, inv, grp_expert, grp_start,
+                                                                          n_groups);
     return (int)hipGetLastError();
 }

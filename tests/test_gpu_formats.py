@@ -66,6 +66,34 @@ def test_quant_permuted_input_gives_natural_codes():
     assert np.array_equal(c0.cpu().numpy(), codes) and np.array_equal(s0.cpu().numpy(), e8)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quant_fp8_vector_and_strided_paths_agree(dtype):
+    # a row stride that is not a multiple of 16 bytes takes the one-value-per-thread kernel, a packed tensor the
+    # 16-values-per-thread one; both must give the oracle's codes, scales and fake-quantised values
+    from dsv41_amd import hipkern, quant
+    g = torch.Generator().manual_seed(5)
+    base = (torch.randn(37, 2048 + 1, generator=g) * torch.logspace(-3, 3, 37).unsqueeze(1)).to(dtype).to(DEV)
+    strided, packed = base[:, 1:], base[:, 1:].contiguous()
+    for permuted in (False, True):
+        a = hipkern.permute_x(strided.contiguous())[:, :] if permuted else strided
+        if permuted:
+            a = torch.cat([torch.zeros(37, 1, dtype=dtype, device=DEV), a], 1)[:, 1:]   # strided again
+        b = a.contiguous()
+        assert a.stride(0) == 2049 and b.stride(0) == 2048
+        ca, sa = quant.quant_fp8_e8m0(a, permuted=permuted)
+        cb, sb = quant.quant_fp8_e8m0(b, permuted=permuted)
+        assert torch.equal(ca, cb) and torch.equal(sa, sb)
+    x32 = packed.float().cpu().numpy()
+    codes, e8 = O.quant_fp8_e8m0(x32)
+    assert np.array_equal(cb.cpu().numpy(), codes) and np.array_equal(sb.cpu().numpy(), e8)
+    fa, fb = quant.fake_quant_fp8(strided), quant.fake_quant_fp8(packed)
+    assert torch.equal(fa, fb)
+    ref = O.fake_quant_fp8(x32)
+    got = fb.float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.astype(np.float32).view(np.uint32)) if dtype == torch.float32 else \
+        np.array_equal(u16(fb), O.f32_to_bf16_bits(ref))
+
+
 @pytest.mark.parametrize("limit,weighted,permute", [(10.0, True, False), (0.0, True, True), (10.0, False, False)])
 def test_swiglu_quant(limit, weighted, permute):
     from dsv41_amd import fused

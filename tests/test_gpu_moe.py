@@ -145,7 +145,8 @@ def test_grouped_fp4_gemm_atomic_rows():
 
 
 # ------------------------------------------------------------------------------------------ routing
-@pytest.mark.parametrize("M,k,E,gmax", [(1, 8, 384, 64), (4, 8, 384, 64), (16, 8, 384, 64), (16, 8, 16, 4), (2048, 8, 384, 64), (300, 6, 48, 16)])
+@pytest.mark.parametrize("M,k,E,gmax", [(1, 8, 384, 64), (4, 8, 384, 64), (16, 8, 384, 64), (16, 8, 16, 4), (129, 8, 384, 64),
+                                       (2048, 8, 384, 64), (4096, 8, 384, 64), (300, 6, 48, 16)])
 def test_dispatch_tables_exact(M, k, E, gmax):
     from dsv41_amd import hipkern
     eid, wt = rand_routing(M, E, k, M * 7 + E)
