@@ -10,9 +10,10 @@
 //   MODE 1 (w2):  rows = 256 consecutive output rows; the epilogue stores fp32 y2[pair][row].
 // The weight operand is the raw E2M1 nibbles + E8M0 bytes as stored; the activation operand the E4M3 codes of the
 // group's tokens, gathered by token id.
-// Workgroup order is XCD-aware: the hardware hands workgroup i to XCD i % 8, so the linear id is remapped such
-// that each XCD walks its share of (column block, group) items group-fastest. Consecutive groups of one expert
-// (a popular expert has many) then run together on one XCD and read each weight tile from that XCD's L2.
+// Workgroup order is XCD-aware: the hardware hands workgroup i to XCD i % 8. XCD x takes the groups g = x, x + 8,
+// x + 16, ... and walks their column blocks column-block-fastest, so the column blocks of one group run together on
+// one XCD and read the group's activations from that XCD's L2 (instead of once per column block from HBM), while the
+// groups of a popular expert (full groups, the costly items) are spread over all eight XCDs.
 #include "common.h"
 
 #define PG_THREADS 512
@@ -76,9 +77,8 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     __shared__ int s_row[PG_T];
 
     const int L = blockIdx.x;
-    const int per_xcd = gridDim.x / 8;
-    const int item = (L & 7) * per_xcd + (L >> 3);
-    const int g = item % a.g_pad, cb = item / a.g_pad;
+    const int jx = L >> 3, gi = jx / a.n_cb;
+    const int g = gi * 8 + (L & 7), cb = jx - gi * a.n_cb;
     if (g >= a.G || cb >= a.n_cb) return;
     const int e = a.grp_expert[g];
     if (e < 0 || e >= a.E) return;
@@ -105,6 +105,13 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     if (tid < PG_T) {
         const int p = p0 + (tid < m ? tid : 0);
         s_row[tid] = MODE == 0 ? a.row_of_pair[p] : p;
+    }
+    // the routing weights of this lane's pairs (MODE 0 epilogue), fetched now so the epilogue does not wait on them
+    float wgt[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int pr = 64 * (wave >> 2) + 16 * u + (lane & 15);
+        wgt[u] = MODE == 0 && pr < m ? a.wt_sorted[p0 + pr] : 0.f;
     }
     __syncthreads();
 
@@ -213,8 +220,8 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
         // acc[0..1][u]: gate rows of columns cb * 128 + 32 cg + 16 j + 4 kb + i (j = 0, 1); acc[2..3][u]: up rows
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+            if (!tb_on[u]) continue;   // wave-uniform: no pair of this token block is in the group
             const int pr = 64 * ph + 16 * u + col;
-            const float wgt = pr < m ? a.wt_sorted[p0 + pr] : 0.f;
             float h[2][4];
             float mx = 0.f;
 #pragma unroll
@@ -229,7 +236,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
                         gg = fminf(gg, a.limit);
                     }
                     float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
-                    hv = bf16_round(hv * wgt);
+                    hv = bf16_round(hv * wgt[u]);
                     h[j][i] = hv;
                     mx = fmaxf(mx, fabsf(hv));
                 }
@@ -255,7 +262,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int pr = 64 * ph + 16 * u + col;
-            if (pr < m) {
+            if (tb_on[u] && pr < m) {
                 float* o = a.y + (long long)(p0 + pr) * a.ldy;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) *(v4f*)(o + block_of(slot_of[j]) * 16 + 4 * kb) = acc[j][u];
