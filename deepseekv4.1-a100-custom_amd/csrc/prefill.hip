@@ -23,6 +23,7 @@
 struct PrefillArgs {
     const uint8_t* xc; long long ldx;        // E4M3 codes [rows][ldx]: activations (MODE 0) or h (MODE 1)
     const uint8_t* xs; long long ldxs;       // E8M0 [rows][ldxs]
+    uint32_t xc_bytes, xs_bytes;             // rows * ldx, rows * ldxs (< 2^32: 32-bit buffer offsets)
     const uint8_t* W; long long stride_we;   // packed E2M1 [E][N][K/2] (tiled or row-major)
     const uint8_t* S; long long stride_se;
     int N, K, E;                              // N = weight rows (MODE 0: 2 I), K = reduction length
@@ -40,7 +41,7 @@ struct PrefillArgs {
 // A 256-row x 128-pair tile (MODE 0: 128 gate rows + the matching 128 up rows = 128 SwiGLU columns; MODE 1: 256
 // output rows). Doubling the rows per tile halves how often each activation byte is re-read (once per column
 // block), which is what bounds the kernel once many tokens share an expert.
-// Every operand moves HBM/L2 -> LDS through the load unit itself (buffer_load ... lds / global_load_lds_dwordx4):
+// Every operand moves HBM/L2 -> LDS through the load unit itself (buffer_load ... lds, all through buffer descriptors):
 // no staging registers, PV_NS k-steps (PV_NS x 33 KB) in flight per workgroup. Per k-step, with wave-uniform
 // branches only: wave w loads weight slots 2 w, 2 w + 1 (1 KB each, 16 B per lane) and token block w (two 1 KB
 // halves); waves 0-3 the E8M0 bytes of 4 weight slots each; waves 4-5 the E8M0 words of 64 pairs each.
@@ -126,9 +127,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + asr * 4) : (uint32_t)((asb * 16 + asr) * Ks);
     const int as_ks = TILED ? 64 : 4;
     // MFMA B layout of token block `wave`: half h, lane l takes pair 16 wave + l % 16, k chunk 4 h + l / 16
-    const uint8_t* b0src = a.xc + (long long)s_row[16 * wave + col] * a.ldx + kb * 16;
-    const uint8_t* b1src = b0src + 64;
-    const uint8_t* bssrc = a.xs + (long long)s_row[(64 * (wave & 1) + lane) & (PG_T - 1)] * a.ldxs;
+    // activation rows through buffer descriptors too: reads past x_rows return 0, and with no FLAT-encoded load in
+    // flight the compiler's waits on the LDS operand reads stay partial instead of draining all of them
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.xc, a.xc_bytes), xsr = buffer_rsrc(a.xs, a.xs_bytes);
+    const uint32_t b0off = (uint32_t)s_row[16 * wave + col] * (uint32_t)a.ldx + kb * 16;
+    const uint32_t bsoff = (uint32_t)s_row[(64 * (wave & 1) + lane) & (PG_T - 1)] * (uint32_t)a.ldxs;
     const bool ldb = 16 * wave < m;   // wave-uniform: the token block holds pairs of the group
     const bool lda = wave < 4, ldbs = (wave == 4 || wave == 5) && 64 * (wave & 1) < m;
     const int per_step = 2 + (lda ? 1 : 0) + (ldb ? 2 : 0) + (ldbs ? 1 : 0);
@@ -139,11 +142,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
         if (lda)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
         if (ldb) {
-            __builtin_amdgcn_global_load_lds((const void*)(b0src + kc * 128), (lds_void*)(so + PV_B + wave * 2048), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(b1src + kc * 128), (lds_void*)(so + PV_B + wave * 2048 + 1024), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048), 16, b0off, (uint32_t)(kc * 128), 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048 + 1024), 16, b0off + 64, (uint32_t)(kc * 128), 0, 0);
         }
         if (ldbs)
-            __builtin_amdgcn_global_load_lds((const void*)(bssrc + kc * 4), (lds_void*)(so + PV_BS + (wave - 4) * 256), 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xsr, (lds_void*)(so + PV_BS + (wave - 4) * 256), 4, bsoff, (uint32_t)(kc * 4), 0, 0);
     };
 
     // ---- operand registers (double-buffered) and their LDS reads
@@ -152,7 +155,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
 #pragma unroll
     for (int u = 0; u < 4; ++u) tb_on[u] = 64 * ph + 16 * u < m;
     v4i OA[2][4], OB0[2][4], OB1[2][4];
-    int OSA[2][4], OSB[2][4];
+    uint8_t OSA[2][4], OSB[2][4];   // E8M0 bytes, widened at the MFMA that uses them
     auto read_ops = [&](int kk, int r) {
         const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
 #pragma unroll
@@ -181,7 +184,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
             const v8i bv = v8i{OB0[r][u].x, OB0[r][u].y, OB0[r][u].z, OB0[r][u].w, OB1[r][u].x, OB1[r][u].y, OB1[r][u].z, OB1[r][u].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc[j][u] = mfma_fp4w_fp8x(v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], OSA[r][j], OSB[r][u]);
+                acc[j][u] = mfma_fp4w_fp8x(v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], (int)OSA[r][j], (int)OSB[r][u]);
         }
     };
     // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue) and
@@ -321,11 +324,12 @@ static int launch_prefill(PrefillArgs& a, int mode, int tiled, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, const uint8_t* W13, long long stride_we,
+extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const uint8_t* W13, long long stride_we,
                                 const uint8_t* S13, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                                 const int* grp_start, int G, const int* tok_sorted, const float* wt_sorted, float limit, uint8_t* hc,
                                 long long ldhc, uint8_t* hs, long long ldhs, void* stream) {
     if (!xc || !xs || !W13 || !S13 || !grp_expert || !grp_start || !tok_sorted || !wt_sorted || !hc || !hs) return DSV41_EINVAL;
+    if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || H < 128 * PG_PF || (H & 127) || I <= 0 || (I & 127) || G < 0 || ldx < H || (ldx & 15) || (((uintptr_t)xc) & 15) || ldxs < H / 32 ||
         (ldxs & 3) || (((uintptr_t)xs) & 3) || ldhc < I || (ldhc & 3) || (((uintptr_t)hc) & 3) || ldhs < I / 32)
         return DSV41_EINVAL;
@@ -333,15 +337,16 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
         stride_se < (long long)2 * I * (H / 32))
         return DSV41_EINVAL;
     if (G == 0) return 0;
-    PrefillArgs a{xc, ldx, xs, ldxs, W13, stride_we, S13, stride_se, 2 * I, H, E, grp_expert, grp_start, G, tok_sorted, wt_sorted, limit,
-                  hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0};
+    PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W13, stride_we, S13, stride_se, 2 * I, H, E,
+                  grp_expert, grp_start, G, tok_sorted, wt_sorted, limit, hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0};
     return launch_prefill(a, 0, tiled, (hipStream_t)stream);
 }
 
-extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, const uint8_t* W2, long long stride_we,
+extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, int h_rows, const uint8_t* W2, long long stride_we,
                                   const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                                   const int* grp_start, int G, float* y2, long long ldy, void* stream) {
     if (!hc || !hs || !W2 || !S2 || !grp_expert || !grp_start || !y2) return DSV41_EINVAL;
+    if (h_rows < 1 || (long long)h_rows * ldhc > 0xFFFFFFFFll || (long long)h_rows * ldhs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || H <= 0 || (H & 255) || I < 128 * PG_PF || (I & 127) || G < 0 || ldhc < I || (ldhc & 15) || (((uintptr_t)hc) & 15) || ldhs < I / 32 ||
         (ldhs & 3) || (((uintptr_t)hs) & 3) || ldy < H || (ldy & 3) || (((uintptr_t)y2) & 15))
         return DSV41_EINVAL;
@@ -349,8 +354,8 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
         stride_se < (long long)H * (I / 32))
         return DSV41_EINVAL;
     if (G == 0) return 0;
-    PrefillArgs a{hc, ldhc, hs, ldhs, W2, stride_we, S2, stride_se, H, I, E, grp_expert, grp_start, G, nullptr, nullptr, 0.f,
-                  nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0};
+    PrefillArgs a{hc, ldhc, hs, ldhs, (uint32_t)(h_rows * ldhc), (uint32_t)(h_rows * ldhs), W2, stride_we, S2, stride_se, H, I, E,
+                  grp_expert, grp_start, G, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0};
     return launch_prefill(a, 1, tiled, (hipStream_t)stream);
 }
 

@@ -212,7 +212,7 @@ def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Expert
     G = min(P, ex.E + (P + 127) // 128)   # groups of <= 128 pairs: at most E + P / 128 of them
     hc = torch.empty(P, I, dtype=torch.uint8, device=dev)
     hs = torch.empty(P, I // 32, dtype=torch.uint8, device=dev)
-    _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
+    _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), T, _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(grp_expert), _lib.ptr(grp_start), G, _lib.ptr(tok_sorted),
               _lib.ptr(wt_sorted), float(limit), _lib.ptr(hc), hc.stride(0), _lib.ptr(hs), hs.stride(0), _lib.stream(dev))
     return PrefillState(T=T, k=k, P=P, G=G, tok_sorted=tok_sorted, wt_sorted=wt_sorted, inv=inv, grp_expert=grp_expert,
@@ -227,7 +227,7 @@ def prefill_down(st: PrefillState, ex: ExpertWeights, ys: torch.Tensor | None = 
     H, I, T = ex.H, ex.I, st.T
     s = _lib.stream(dev)
     st.y2 = torch.empty(st.P, H, dtype=torch.float32, device=dev)
-    _lib.call("dsv41_prefill_down", _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), _lib.ptr(ex.w2), ex.w2.stride(0),
+    _lib.call("dsv41_prefill_down", _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), st.P, _lib.ptr(ex.w2), ex.w2.stride(0),
               _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), st.G,
               _lib.ptr(st.y2), st.y2.stride(0), s)
     if out is None and y32 is None:

@@ -84,17 +84,18 @@ int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, 
 
 /* Prefill w13 + SwiGLU: for every group g of <= 128 expert-sorted pairs (moe_dispatch tables with gmax 128),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;
- * x as E4M3 codes xc [rows][ldx] + E8M0 xs [rows][ldxs]; h as FP8 codes hc [P][ldhc] + E8M0 hs [P][ldhs] in
- * sorted pair order. H % 128 == 0, H >= 384, I % 64 == 0. Replaces the w13 grouped_fp4_gemm + swiglu_quant of
+ * x as E4M3 codes xc [x_rows][ldx] + E8M0 xs [x_rows][ldxs] (x_rows * ldx < 2^32); h as FP8 codes hc [P][ldhc]
+ * + E8M0 hs [P][ldhs] in sorted pair order. H % 128 == 0, H >= 384, I % 64 == 0. Replaces the w13 grouped_fp4_gemm + swiglu_quant of
  * model.MoE.__call__ (model.py:584-587; moe_kernels.py:127-151; fused.py:283-345). */
-int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, const uint8_t* W13, long long stride_we,
+int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const uint8_t* W13, long long stride_we,
                      const uint8_t* S13, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                      const int* grp_start, int G, const int* tok_sorted, const float* wt_sorted, float limit, uint8_t* hc,
                      long long ldhc, uint8_t* hs, long long ldhs, void* stream);
 
-/* Prefill w2: y2[p] = h[p] . deq(W2[e_g])^T (fp32 [P][ldy], sorted pair order) for the same groups.
+/* Prefill w2: y2[p] = h[p] . deq(W2[e_g])^T (fp32 [P][ldy], sorted pair order) for the same groups; h_rows = P
+ * (h_rows * ldhc < 2^32).
  * I % 128 == 0, I >= 384, H % 128 == 0. Replaces the w2 grouped_fp4_gemm of model.py:588. */
-int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, const uint8_t* W2, long long stride_we,
+int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, int h_rows, const uint8_t* W2, long long stride_we,
                        const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                        const int* grp_start, int G, float* y2, long long ldy, void* stream);
 
