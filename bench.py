@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
     ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
                                                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
@@ -403,6 +404,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     K, W = args.steps, args.warmup
+    if args.prefill_only:
+        layers = make_layers(torch, dev, 1, 1000)
+        print(json.dumps(dict(bench_prefill(torch, dev, layers[0], 2048, iters=K),
+                              workload="configs[3]: 2048 tokens x top-8, Zipf(1.1) routing, full expert path")))
+        return
     layers = make_layers(torch, dev, N_COPIES, 1000)
     eb = expert_bytes()
     sel_bytes = TOPK * eb
