@@ -158,10 +158,12 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     uint8_t OSA[2][4], OSB[2][4];   // E8M0 bytes, widened at the MFMA that uses them
     auto read_ops = [&](int kk, int r) {
         const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
+        if (tb_on[0]) {   // wave-uniform: a wave whose half of the group is empty runs no MFMA
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
-            OSA[r][j] = st[PV_AS + slot_of[j] * 64 + col * 4 + kb];
+            for (int j = 0; j < 4; ++j) {
+                OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
+                OSA[r][j] = st[PV_AS + slot_of[j] * 64 + col * 4 + kb];
+            }
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
