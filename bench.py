@@ -1,5 +1,5 @@
-"""Benchmark of the MI355X FP4 MoE expert path (BASELINE.json metric: FP4 MoE decode us/layer + HBM TB/s;
-prefill grouped-GEMM MXFP4 TFLOPS).
+"""Benchmark of the MI355X FP4 MoE expert path (headline metric: FP4 MoE decode us/layer + HBM TB/s; prefill
+grouped-GEMM MXFP4 TFLOPS).
 
 Step (the headline, configs[1]): one MoE decode layer at batch 1 -- softmax top-8 routing of fresh N(0,1)
 logits over 384 experts, then the routed FP4 experts (hidden 7168, intermediate 1664, packed E2M1 + E8M0,
