@@ -234,6 +234,30 @@ def test_gemv_configs0_shape(lib, mode):
         assert O.rel_l2(out.numpy(), O.deq64(w, s) @ x.astype(np.float64)) < 2e-2
 
 
+@pytest.mark.parametrize("N", [1, 8, 37, 203])
+def test_gemv_row_tails(lib, N):
+    """Row counts that are not a multiple of the rows one kernel pass takes (or smaller than one pass) go through
+    the single-row path; every row must equal the row-by-row oracle to the same tolerance in both modes, and a row's
+    value must not depend on which pass computed it."""
+    rng = np.random.default_rng(40 + N)
+    K = 512
+    w = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    s = rng.integers(119, 124, (N, K // 32), dtype=np.uint8)
+    x = O.fake_quant_fp8(O.bf16_round(rng.standard_normal((1, K)).astype(np.float32)))[0]
+    xt = torch.from_numpy(O.f32_to_bf16_bits(x).view(np.int16)).view(torch.bfloat16)
+    for mode in (2, 0):
+        lib.cpumoe_set_int8(mode)
+        try:
+            out = cpumoe.gemv(torch.from_numpy(w), torch.from_numpy(s), xt).numpy()
+            # the same rows, computed one at a time (always the single-row path)
+            single = np.concatenate([cpumoe.gemv(torch.from_numpy(w[i:i + 1]), torch.from_numpy(s[i:i + 1]), xt).numpy() for i in range(N)])
+        finally:
+            lib.cpumoe_set_int8(2)
+        want = O.w4a8_gemv(w, s, x) if mode else O.deq64(w, s) @ x.astype(np.float64)
+        assert O.rel_l2(out, want) < 1e-6, mode
+        assert np.array_equal(out, single), mode
+
+
 def test_zero_block_and_zero_scale(lib):
     """An all-zero activation block (int8 scale 1) and scale byte 0 (contributes 0) behave as the reference's."""
     rng = np.random.default_rng(31)
