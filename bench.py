@@ -257,7 +257,7 @@ def _ref_lib():
     return L
 
 
-def _time_layer_calls(L, bufs, Es, steps_cap, budget_s):
+def _time_layer_calls(L, bufs, Es, steps_cap, budget_s, it0=0):
     """Median time of forward_ids over 8 of Es resident experts, expert ids rotating every call
     (test_cpumoe.py:32-35); x is N(0,1) bf16, routing weights 1/8."""
     import numpy as np
@@ -271,7 +271,7 @@ def _time_layer_calls(L, bufs, Es, steps_cap, budget_s):
     wts = np.full(TOPK, 1.0 / TOPK, np.float32)
     times = []
     t_end = time.perf_counter() + budget_s
-    for it in range(steps_cap):
+    for it in range(it0, it0 + steps_cap):
         ids = np.array([(j * 5 + 8 * it) % Es for j in range(TOPK)], np.int32)
         t0 = time.perf_counter()
         r = L.cpumoe_forward_ids(bufs[0], bufs[1], bufs[2], bufs[3], b13, bs13, b2, bs2, ids.ctypes.data, TOPK, xb.ctypes.data,
@@ -283,7 +283,7 @@ def _time_layer_calls(L, bufs, Es, steps_cap, budget_s):
     return statistics.median(times[1:] if len(times) > 1 else times), len(times)
 
 
-def cpu_baselines(steps_cap=40):
+def cpu_baselines(steps_cap=80):
     """CPU numbers, all on the same host buffers and the same worker CPUs (this process's CPUs minus one core
     per NUMA node, as cpumoe.default_cpu_list):
       cpu_baseline  the reference's CPU MoE library (oracle/_ref), default W4A8 int8 mode (cpumoe.py:36), on a
@@ -327,15 +327,26 @@ def cpu_baselines(steps_cap=40):
               f"{len(lst)} pinned worker CPUs")
     baseline = {"value": None, "note": "oracle/_ref not built or host lacks its ISA"}
     R = _ref_lib()
+    libs = [M]
     if R is not None:
         R.cpumoe_init_list(arr, len(lst), per_node)
         R.cpumoe_set_int8(2)
-        med, n = _time_layer_calls(R, bufs, Es, steps_cap, 20.0)
+        libs = [R, M]
+    # both libraries warm up first (the host's first few hundred calls run slow: page and clock settling), then
+    # they are timed in alternating blocks of 10 calls, so neither gains from running later
+    for L in libs:
+        _time_layer_calls(L, bufs, Es, 1 << 20, 1.5)
+    meds = {id(L): [] for L in libs}
+    for blk in range(max(1, steps_cap // 10)):
+        for L in libs:
+            meds[id(L)].append(_time_layer_calls(L, bufs, Es, 11, 5.0, it0=11 * blk)[0])
+    if R is not None:
+        med = statistics.median(meds[id(R)])
         baseline = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
-                    "kind": "reference", "sample": sample + f", median of {n} calls"}
-    med, n = _time_layer_calls(M, bufs, Es, steps_cap, 20.0)
+                    "kind": "reference", "sample": sample + f", median of {len(meds[id(R)])} blocks of 10 calls, alternating with cpu_port"}
+    med = statistics.median(meds[id(M)])
     res["cpu_port"] = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
-                       "kind": "port", "sample": sample + f", median of {n} calls",
+                       "kind": "port", "sample": sample + f", median of {len(meds[id(M)])} blocks of 10 calls, alternating with cpu_baseline",
                        "note": "libdsv41_cpu.so: this build's restatement (bit-exact with the reference library in int8 mode "
                                "for inter % 256 == 0; computes the I = 1664 tail the reference skips)"}
     for p, nbytes in zip(bufs, sizes):
