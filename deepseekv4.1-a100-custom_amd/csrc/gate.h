@@ -33,12 +33,17 @@ struct GateRow {
         const int e0 = lane * PER;
         float mx = -INFINITY;
         // the logits may arrive as nparts partial sums (a split-K router GEMV), added in ascending part order.
-        // Loads go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch).
+        // Loads go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch);
+        // one part (plain logits) is a single batch of PER loads.
         constexpr int Q = PER <= 8 ? 8 : 1;
         float v[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) v[i] = 0.f;
-        for (int p0 = 0; p0 < nparts; p0 += Q) {
+        if (nparts == 1) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) v[i] = e0 + i < E ? S[e0 + i] : 0.f;
+        }
+        for (int p0 = 0; nparts > 1 && p0 < nparts; p0 += Q) {
             float t[Q][PER];
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
@@ -54,7 +59,7 @@ struct GateRow {
         }
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            s[i] = e0 + i < E ? v[i] / temp : -INFINITY;
+            s[i] = e0 + i < E ? (temp == 1.0f ? v[i] : v[i] / temp) : -INFINITY;   // x / 1 == x exactly
             mx = fmaxf(mx, s[i]);
         }
         // scoring function (mode 0 sqrt(softplus), 1 sigmoid, 2 softmax), fused2.py:433-440
