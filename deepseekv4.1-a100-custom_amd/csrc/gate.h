@@ -18,13 +18,17 @@ struct GateRow {
     int li;
     float ls;
 
-    __device__ __forceinline__ void rescan() {
+    __device__ __forceinline__ void rescan() {   // selects, not branches: no exec-mask changes per slot
         lk = 0u;
         li = 0;
         ls = 0.f;
 #pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (key[i] > lk) { lk = key[i]; li = i; ls = s[i]; }
+        for (int i = 0; i < PER; ++i) {
+            const bool gt = key[i] > lk;
+            lk = gt ? key[i] : lk;
+            li = gt ? i : li;
+            ls = gt ? s[i] : ls;
+        }
     }
 
     __device__ __forceinline__ void prepare(const float* __restrict__ S, int nparts, long long pstride, const float* __restrict__ bias, int E,
