@@ -87,8 +87,11 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         if ((q & 1) == 0) lds_s[row * Ks + (q >> 1)] = (uint8_t)(e + 127);
     };
 
-    // ---- one token: its activations are the only row, staged while the routing runs
+    // ---- one token: its activations are the only row, staged while the routing runs. The gate is the critical
+    // path, so wave 0 issues the logits loads first, before the barrier below.
     const bool early = EARLY && per_row <= (int)blockDim.x;   // host guarantees both for EARLY
+    GateRow<PER> gr;
+    if (EARLY && wave == 0 && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
     v4i xr0, xr1;
     if (early && tid < per_row) x_load(0, tid, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
@@ -129,7 +132,6 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             int ki = 0;
             float kw = 0.f;   // lane k keeps pick k
             if (a.logits) {
-                GateRow<PER> gr;
                 gr.prepare(a.logits, a.nparts, a.pstride, a.bias, E, a.temp, a.score_func);
                 float wsum = 0.f;
                 for (int k = 0; k < topk; ++k) {

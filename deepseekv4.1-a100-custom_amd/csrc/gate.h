@@ -17,6 +17,16 @@ struct GateRow {
     unsigned lk;   // the lane's best remaining key, its slot (lowest on ties) and score
     int li;
     float ls;
+    float raw[PER];   // one part of logits, loaded ahead of prepare() by load_logits()
+    bool loaded = false;
+
+    // issue the loads of one part of logits now (a caller can do this first thing, before any barrier)
+    __device__ __forceinline__ void load_logits(const float* __restrict__ S, int E) {
+        const int e0 = (threadIdx.x & 63) * PER;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) raw[i] = S[min(e0 + i, E - 1)];   // clamped: no branch per load; masked in prepare()
+        loaded = true;
+    }
 
     __device__ __forceinline__ void rescan() {   // selects, not branches: no exec-mask changes per slot
         lk = 0u;
@@ -45,7 +55,7 @@ struct GateRow {
         for (int i = 0; i < PER; ++i) v[i] = 0.f;
         if (nparts == 1) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i) v[i] = e0 + i < E ? S[e0 + i] : 0.f;
+            for (int i = 0; i < PER; ++i) v[i] = e0 + i < E ? (loaded ? raw[i] : S[e0 + i]) : 0.f;
         }
         for (int p0 = 0; nparts > 1 && p0 < nparts; p0 += Q) {
             float t[Q][PER];
