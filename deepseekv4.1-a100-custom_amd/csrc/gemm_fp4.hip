@@ -187,18 +187,25 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     const int nb = blockIdx.x;
     const int K = a.K, Ks = K >> 5, LS = K + 16;
     const int n_slots = a.n_slots;
+    // every kernel argument the prologue needs is read in one batch here (the empty asm consumes them), rather
+    // than in one scalar round trip per first use
+    __asm__ volatile("" ::"s"(a.W), "s"(a.stride_we), "s"(a.S), "s"(a.stride_se), "s"(K), "s"(n_slots), "s"(a.grp_expert),
+                     "s"(a.grp_start), "s"(a.tok_sorted), "s"(a.shard_start), "s"(a.shard_n), "s"(a.hc), "s"(a.ldh), "s"(a.zero_row));
 
-    // ---- one round trip: this wave's group experts (slot wave + 8 j in lane j), the group starts, the tokens
+    // ---- one round trip: this wave's group experts (slot wave + 8 j in lane j), the group starts, the tokens.
+    // The loads are unconditional (indices clamped, results masked), so the kernel-argument loads they need go
+    // out in one batch at entry instead of one round trip per guarded block.
     const int gslot = wave + DS_WAVES * lane;
-    int e = -1;
-    if (lane < DS_MAX_SLOTS / DS_WAVES && gslot < n_slots) {
-        const int ge = a.grp_expert[gslot];
-        e = ge < 0 ? -1 : ge - a.shard_start;
-        if (e >= a.shard_n) e = -1;
+    const bool gvalid = lane < DS_MAX_SLOTS / DS_WAVES && gslot < n_slots;
+    const int st_l = a.grp_start[min(tid, n_slots)];        // n_slots + 1 entries
+    int ge = -1, tk_l = 0;
+    if (n_slots > 0) {                                        // uniform
+        ge = a.grp_expert[min(gslot, n_slots - 1)];
+        tk_l = a.tok_sorted[min(tid, n_slots - 1)];
     }
-    int st = 0, tk = 0;
-    if (tid <= n_slots) st = a.grp_start[tid];
-    if (tid < n_slots) tk = a.tok_sorted[tid];
+    int e = gvalid && ge >= 0 ? ge - a.shard_start : -1;
+    if (e >= a.shard_n) e = -1;
+    const int st = tid <= n_slots ? st_l : 0, tk = tid < n_slots ? tk_l : 0;
     const unsigned long long vmask = __ballot(e >= 0);   // this wave's valid groups
 
     const int col = lane & 15, kb = lane >> 4;
