@@ -91,7 +91,10 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // path, so wave 0 issues the logits loads first, before the barrier below.
     const bool early = EARLY && per_row <= (int)blockDim.x;   // host guarantees both for EARLY
     GateRow<PER> gr;
-    if (EARLY && wave == 0 && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
+    // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
+    // workgroups a CU holds do not run their gates on the same SIMD
+    const int gw = (int)((blockIdx.x + blockIdx.y * gridDim.x) & 3);
+    if (EARLY && wave == gw && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
     v4i xr0, xr1;
     if (early && tid < per_row) x_load(0, tid, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
@@ -122,13 +125,13 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     };
 
     // ---- routing, identical in every workgroup.
-    // One token (early): wave 0 runs the gate; this workgroup's expert is the g-th pick, which wave 0 posts in LDS
+    // One token (early): wave gw runs the gate; this workgroup's expert is the g-th pick, which wave gw posts in LDS
     // right after round g, so every wave's weight tiles go out while the later rounds run. (Its h row is still
     // the expert's rank in ascending id order, found by the bucketing below.)
     // M tokens: one wave per token; the workgroup's expert is the g-th smallest selected id.
     int eg = -1;
     if (early) {
-        if (wave == 0) {
+        if (wave == gw) {
             int ki = 0;
             float kw = 0.f;   // lane k keeps pick k
             if (a.logits) {
@@ -159,9 +162,9 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 s_wt[lane] = kw;
             }
         }
-        if (!a.logits || wave != 0) {
+        if (!a.logits || wave != gw) {
             if (a.logits) {
-                // the pick, posted by wave 0 (s_pick starts at -2, before the first barrier)
+                // the pick, posted by wave gw (s_pick starts at -2, before the first barrier)
                 while ((eg = __hip_atomic_load(&s_pick, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == -2) __builtin_amdgcn_s_sleep(1);
                 eg = __builtin_amdgcn_readfirstlane(eg);
             } else {
