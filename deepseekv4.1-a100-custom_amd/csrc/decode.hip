@@ -88,7 +88,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     };
 
     // ---- one token: its activations are the only row, staged while the routing runs. The gate is the critical
-    // path, so wave 0 issues the logits loads first, before the barrier below.
+    // path, so the gate wave issues the logits loads first, before the barrier below.
     const bool early = EARLY && per_row <= (int)blockDim.x;   // host guarantees both for EARLY
     GateRow<PER> gr;
     // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
