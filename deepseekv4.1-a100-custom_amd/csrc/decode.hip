@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ unsigned long long s_bits[UP_MAXE / 64];   // selected experts
     __shared__ int s_tok[UP_MAXM * UP_MAXK], s_slot[UP_MAXM * UP_MAXK];   // members of this workgroup's group
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
-    __shared__ int s_mg, s_pick;
+    __shared__ int s_mg, s_pick, s_xready;
     __shared__ v4f s_acc[UP_WAVES][64];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -87,19 +87,24 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         if ((q & 1) == 0) lds_s[row * Ks + (q >> 1)] = (uint8_t)(e + 127);
     };
 
-    // ---- one token: its activations are the only row, staged while the routing runs. The gate is the critical
-    // path, so the gate wave issues the logits loads first, before the barrier below.
-    const bool early = EARLY && per_row <= (int)blockDim.x;   // host guarantees both for EARLY
+    // ---- one token (EARLY): wave gw runs the gate while the other seven waves stage the token's activations in LDS
+    // row 0. The gate is the critical path, so wave gw issues the logits loads first, before the barrier below.
+    const bool early = EARLY && per_row <= (UP_WAVES - 1) * 64;   // host guarantees both for EARLY
     GateRow<PER> gr;
     // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
     // workgroups a CU holds do not run their gates on the same SIMD
     const int gw = (int)((blockIdx.x + blockIdx.y * gridDim.x) & 3);
-    if (EARLY && wave == gw && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
+    const bool gwave = early && wave == gw;
+    if (gwave && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
+    const int xq = (wave - (wave > gw ? 1 : 0)) * 64 + lane;   // early: the lane's 16 values of row 0 among the stagers
     v4i xr0, xr1;
-    if (early && tid < per_row) x_load(0, tid, xr0, xr1);
+    if (early && !gwave && xq < per_row) x_load(0, xq, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
-    if (tid == 0) s_pick = -2;
-    if (early) __syncthreads();   // s_pick is set before any wave polls it
+    if (tid == 0) {
+        s_pick = -2;
+        s_xready = 0;
+    }
+    if (early) __syncthreads();   // s_pick, s_xready and s_bits are set before any wave uses them
 
     // ---- this wave's weight stream: row block rb of {gate c0, gate c0 + 16, up c0, up c0 + 16}, K-half kh; the
     // expert (the buffer descriptors) comes from the routing
@@ -127,12 +132,12 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // ---- routing, identical in every workgroup.
     // One token (early): wave gw runs the gate; this workgroup's expert is the g-th pick, which wave gw posts in LDS
     // right after round g, so every wave's weight tiles go out while the later rounds run. (Its h row is still
-    // the expert's rank in ascending id order, found by the bucketing below.)
+    // the expert's rank in ascending id order, which wave gw finds once all rounds are done.)
     // M tokens: one wave per token; the workgroup's expert is the g-th smallest selected id.
     int eg = -1;
     if (early) {
-        if (wave == gw) {
-            int ki = 0;
+        if (gwave) {
+            int ki = -1;
             float kw = 0.f;   // lane k keeps pick k
             if (a.logits) {
                 gr.prepare(a.logits, a.nparts, a.pstride, a.bias, E, a.temp, a.score_func);
@@ -153,16 +158,37 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                     if (lane == k) { ki = id; kw = w; }
                 }
                 kw = gate_weight(kw, wsum, a.route_scale, a.norm);
-            } else if (lane < topk) {
-                ki = a.eid_in[lane];
-                kw = a.wt_in[lane];
+            } else {
+                if (lane < topk) {
+                    ki = a.eid_in[lane];
+                    kw = a.wt_in[lane];
+                }
+                eg = __builtin_amdgcn_readfirstlane(a.eid_in[g]);
+                if (!(eg >= 0 && eg < E)) eg = -1;
+                if (eg >= 0) {
+                    set_expert(eg);
+                    pipeline_start<PF>(nk_w, load);
+                }
             }
+            // the routing of the token, the selected-expert mask, and this workgroup's member: its h row is the
+            // expert's rank among the selected ids (ascending), its weight that of the first pair holding the expert
+            const bool kv = lane < topk && ki >= 0 && ki < E;   // out-of-range ids are dropped, never read
             if (lane < topk) {
-                s_eid[lane] = (ki >= 0 && ki < E) ? ki : -1;   // out-of-range ids are dropped, never read
+                s_eid[lane] = kv ? ki : -1;
                 s_wt[lane] = kw;
             }
-        }
-        if (!a.logits || wave != gw) {
+            if (kv) atomicOr(&s_bits[ki >> 6], 1ull << (ki & 63));
+            const int rank = __popcll(__ballot(kv && ki < eg));
+            const unsigned long long mine = __ballot(kv && ki == eg);
+            const float pw = __shfl(kw, mine ? (int)__builtin_ctzll(mine) : 0);
+            if (lane == 0) {
+                s_slot[0] = rank;
+                s_pw[0] = pw;
+            }
+        } else {
+            // stage this wave's part of row 0 (the loads went out at kernel start), release it, then follow the pick
+            if (xq < per_row) x_store(0, xq, xr0, xr1);
+            if (lane == 0) __hip_atomic_fetch_add(&s_xready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (a.logits) {
                 // the pick, posted by wave gw (s_pick starts at -2, before the first barrier)
                 while ((eg = __hip_atomic_load(&s_pick, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == -2) __builtin_amdgcn_s_sleep(1);
@@ -193,53 +219,56 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             }
         }
     }
-    if (early && tid < per_row) x_store(0, tid, xr0, xr1);
-    __syncthreads();
-    for (int p = tid; p < P; p += blockDim.x) {
-        const int e = s_eid[p];
-        if (e >= 0) atomicOr(&s_bits[e >> 6], 1ull << (e & 63));
-    }
-    __syncthreads();
-
-    // ---- the selected experts (groups are in ascending expert order)
-    int U = 0, eg_sorted = -1;
-#pragma unroll
-    for (int w = 0; w < UP_MAXE / 64; ++w) {
-        unsigned long long bits = s_bits[w];
-        bits = ((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(bits >> 32)) << 32) |
-               (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)bits);
-        const int c = __popcll(bits);
-        if (!early && eg_sorted < 0 && g < U + c) {
-            for (int r = g - U; r > 0; --r) bits &= bits - 1ull;   // drop the lower set bits
-            eg_sorted = 64 * w + (int)__builtin_ctzll(bits);
-        }
-        U += c;
-    }
-    if (!early) eg = eg_sorted;
     const bool publish = blockIdx.x == 0 && g == 0;
-    const bool work = early ? eg >= 0 : g < U;
-    if (!work && !publish) return;   // uniform: fewer experts than slots
-    if (!early && work) set_expert(eg);
+    int mg = 1;
+    if (early) {
+        if (eg < 0 && !publish) return;   // uniform: an invalid id (given routing only)
+    } else {
+        __syncthreads();
+        for (int p = tid; p < P; p += blockDim.x) {
+            const int e = s_eid[p];
+            if (e >= 0) atomicOr(&s_bits[e >> 6], 1ull << (e & 63));
+        }
+        __syncthreads();
 
-    // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
-    if (tid == 0) s_mg = 0;
-    __syncthreads();
-    if (work)
-        for (int p = tid; p < P; p += blockDim.x)
-            if (s_eid[p] == eg) {
-                int lt = 0, same = 0;
-                for (int q = 0; q < P; ++q) {
-                    const int eq = s_eid[q];
-                    lt += (eq >= 0 && eq < eg) ? 1 : 0;
-                    same += (eq == eg && q < p) ? 1 : 0;   // pairs are token-major: q < p = earlier token (or slot)
-                }
-                s_tok[same] = p / topk;
-                s_slot[same] = lt + same;
-                s_pw[same] = s_wt[p];
-                atomicAdd(&s_mg, 1);
+        // ---- the selected experts (groups are in ascending expert order); this workgroup's is the g-th
+        int U = 0;
+#pragma unroll
+        for (int w = 0; w < UP_MAXE / 64; ++w) {
+            unsigned long long bits = s_bits[w];
+            bits = ((unsigned long long)(unsigned)__builtin_amdgcn_readfirstlane((int)(bits >> 32)) << 32) |
+                   (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)bits);
+            const int c = __popcll(bits);
+            if (eg < 0 && g < U + c) {
+                for (int r = g - U; r > 0; --r) bits &= bits - 1ull;   // drop the lower set bits
+                eg = 64 * w + (int)__builtin_ctzll(bits);
             }
-    __syncthreads();
-    const int mg = __builtin_amdgcn_readfirstlane(s_mg);
+            U += c;
+        }
+        if (g >= U && !publish) return;   // uniform: fewer experts than slots
+        if (g < U) set_expert(eg);
+
+        // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
+        if (tid == 0) s_mg = 0;
+        __syncthreads();
+        if (g < U)
+            for (int p = tid; p < P; p += blockDim.x)
+                if (s_eid[p] == eg) {
+                    int lt = 0, same = 0;
+                    for (int q = 0; q < P; ++q) {
+                        const int eq = s_eid[q];
+                        lt += (eq >= 0 && eq < eg) ? 1 : 0;
+                        same += (eq == eg && q < p) ? 1 : 0;   // pairs are token-major: q < p = earlier token (or slot)
+                    }
+                    s_tok[same] = p / topk;
+                    s_slot[same] = lt + same;
+                    s_pw[same] = s_wt[p];
+                    atomicAdd(&s_mg, 1);
+                }
+        __syncthreads();
+        mg = g < U ? __builtin_amdgcn_readfirstlane(s_mg) : 0;
+    }
+    const bool work = eg >= 0;
 
     const uint8_t* xl;
     const uint8_t* xsl;
@@ -285,13 +314,18 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         }
     };
 
-    if (EARLY) {
-        // one token: its codes are in LDS row 0 already and the first tiles are in flight (a token's expert ids
-        // are distinct, as the gate guarantees, so the group has one member)
+    if (early) {
+        // one token: the first tiles are in flight; the stream starts once the seven stagers have released row 0,
+        // without waiting for the rest of the top-k (the gate wave joins when its rounds are done). A token's
+        // expert ids are distinct, as the gate guarantees, so the group has one member, whose h row and weight the
+        // gate wave has written before it reaches the epilogue's barrier.
         if (work) {
+            while (__hip_atomic_load(&s_xready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < UP_WAVES - 1) __builtin_amdgcn_s_sleep(1);
             start_pass(1);
             pipeline_finish<PF>(nk_w, load, use);
             epilogue(0, 1);
+        } else {
+            __syncthreads();   // (publishing workgroup only) the gate wave's routing and mask are visible
         }
     } else {
         // passes of up to a.rows members (16 B columns); a group with more members than LDS rows holds (possible
@@ -316,6 +350,9 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // ---- workgroup (0, 0) publishes the routing and the tables of the down projection (off the critical path:
     // the down projection is the next launch)
     if (publish) {
+        int U = 0;   // selected experts
+#pragma unroll
+        for (int w = 0; w < UP_MAXE / 64; ++w) U += __popcll(s_bits[w]);
         int valid = 0;
         for (int p = 0; p < P; ++p) valid += s_eid[p] >= 0 ? 1 : 0;
         for (int p = tid; p < P; p += blockDim.x) {
@@ -360,11 +397,12 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
         stride_we < (long long)2 * I * (H / 2) || stride_se < (long long)2 * I * (H / 32)) return DSV41_EINVAL;
-    // M = 1: the single token's codes are staged while the routing runs (one LDS row, H / 16 <= 512 lanes).
+    // M = 1: the single token's codes are staged while the routing runs (one LDS row, H / 16 <= 448 lanes: the
+    // seven waves besides the gate's).
     // M > 1: members are staged after the bucketing, up to `rows` per pass, as many as fit in 60 KiB of LDS
     // (two workgroups per CU)
     const size_t row_bytes = (size_t)(H + 16) + (size_t)(H / 32);
-    const bool early = M == 1 && H / 16 <= UP_WAVES * 64;
+    const bool early = M == 1 && H / 16 <= (UP_WAVES - 1) * 64;
     int rows = early ? 1 : (int)((60 * 1024) / row_bytes);
     rows = rows > 16 ? 16 : (rows > M ? M : rows);
     if (rows < 1) return DSV41_EINVAL;
