@@ -89,7 +89,9 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
 
     // ---- one token (EARLY): wave gw runs the gate while the other seven waves stage the token's activations in LDS
     // row 0. The gate is the critical path, so wave gw issues the logits loads first, before the barrier below.
-    const bool early = EARLY && per_row <= (UP_WAVES - 1) * 64;   // host guarantees both for EARLY
+    // compile-time, so the one-token instantiation holds none of the member-pass code: the host launches EARLY only
+    // for M == 1 and per_row <= (UP_WAVES - 1) * 64
+    constexpr bool early = EARLY != 0;
     GateRow<PER> gr;
     // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
     // workgroups a CU holds do not run their gates on the same SIMD
