@@ -19,6 +19,7 @@
 #define UP_MAXM 16
 #define UP_MAXK 16
 #define UP_MAXE 512
+#define UP_WSC 2048   // one token: E8M0 bytes of a wave's weight stream staged in LDS (<= 32 k-chunks of 64 bytes)
 
 struct DecodeUpArgs {
     const float* logits; long long ldl;      // fp32 [M][E] router logits (or NULL: eid_in / wt_in given)
@@ -46,6 +47,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
     __shared__ int s_mg, s_pick, s_xready;
     __shared__ v4f s_acc[UP_WAVES][64];
+    __shared__ __align__(16) uint8_t s_wsc[EARLY ? UP_WAVES * UP_WSC : 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform values kept in scalar registers
@@ -128,7 +130,38 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     int SA[PF];
     auto load = [&](int slot, int kc) {
         A[slot] = buffer_load_tile(wr, wv, (uint32_t)(kc * ws));
-        SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
+        if (!early) SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
+    };
+    // One token: a wave's E8M0 bytes (16 rows x nk_w k-chunks) are fetched with a few wide loads when its expert is
+    // known, ahead of its first tiles, and kept in LDS in MFMA order (k-chunk j at 64 j, row r's byte for k-block kb
+    // at 4 r + kb), so each k-step reads its scale from LDS instead of issuing a byte load per lane: the byte loads
+    // cost as much load-unit time as the weight tiles themselves.
+    uint8_t* const wsc = s_wsc + (EARLY ? wave * UP_WSC : 0);
+    v4i SC[TILED ? 2 : 8];
+    auto scale_load = [&]() {
+        if (TILED) {   // the stream's bytes are contiguous: (nb nk + k0c) 64 .. + 64 nk_w
+            const uint32_t b = (uint32_t)stile_off<1>(nb, k0c, nk, Ks, 0) + lane * 16;
+            SC[0] = buffer_load_tile(sr, b, 0);
+            SC[1] = buffer_load_tile(sr, b, 1024);
+        } else {       // row r's bytes k0c 4 .. are contiguous: one dword (4 k-blocks) per (row, k-chunk)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int idx = 64 * i + lane, r = idx & 15, j = idx >> 4;
+                SC[i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)((nb * 16 + r) * Ks + (k0c + j) * 4), 0, 0);
+            }
+        }
+    };
+    auto scale_store = [&]() {
+        if (TILED) {
+            *(v4i*)(wsc + lane * 16) = SC[0];
+            *(v4i*)(wsc + 1024 + lane * 16) = SC[1];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int idx = 64 * i + lane, r = idx & 15, j = idx >> 4;
+                *(int*)(wsc + j * 64 + r * 4) = SC[i].x;
+            }
+        }
     };
 
     // ---- routing, identical in every workgroup.
@@ -154,6 +187,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                         if (lane == 0) __hip_atomic_store(&s_pick, eg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                         if (eg >= 0) {
                             set_expert(eg);
+                            scale_load();
                             pipeline_start<PF>(nk_w, load);
                         }
                     }
@@ -169,6 +203,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 if (!(eg >= 0 && eg < E)) eg = -1;
                 if (eg >= 0) {
                     set_expert(eg);
+                    scale_load();
                     pipeline_start<PF>(nk_w, load);
                 }
             }
@@ -187,6 +222,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 s_slot[0] = rank;
                 s_pw[0] = pw;
             }
+            if (eg >= 0) scale_store();   // its scale loads went out with the first tiles, at the pick
         } else {
             // stage this wave's part of row 0 (the loads went out at kernel start), release it, then follow the pick
             if (xq < per_row) x_store(0, xq, xr0, xr1);
@@ -201,7 +237,17 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             }
             if (eg >= 0) {
                 set_expert(eg);
-                pipeline_start<PF>(nk_w, load);
+                // the first PF tiles, issued as pipeline_start does but without its short-stream branch, so the store
+                // below sits in the same block and waits for the two scale loads only (older than every tile). With
+                // fewer than PF k-chunks (small K) the extra loads read other bytes of the expert or zeros past its
+                // end, and pipeline_finish's unpipelined path loads what it uses again.
+                scale_load();
+#pragma unroll
+                for (int i = 0; i < PF; ++i) {
+                    load(i, i);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                scale_store();
             }
         }
     } else {
@@ -274,15 +320,18 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
 
     const uint8_t* xl;
     const uint8_t* xsl;
+    const uint8_t* wsl = wsc + (lane & 15) * 4 + kb;   // one token: this lane's weight scale of k-chunk 0
     v4f acc;
     auto use = [&](int slot) {
         const v4i b0 = *(const v4i*)(xl);
         const v4i b1 = *(const v4i*)(xl + 64);
         const int sb = *xsl;
+        const int sa = early ? (int)*wsl : SA[slot];
         xl += 128;
         xsl += 4;
+        if (early) wsl += 64;
         acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
-                             v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, SA[slot], sb);
+                             v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, sa, sb);
     };
     // B column c = member base + c of the pass (columns past the pass read row 0; their results are unused)
     auto start_pass = [&](int mp) {
