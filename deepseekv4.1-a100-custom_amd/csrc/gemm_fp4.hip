@@ -166,22 +166,30 @@ struct DownSumArgs {
 
 #define DS_MAX_SLOTS 256
 #define DS_WAVES 8
+#define DS_HV 8          // H_LDS: h code vectors (16 bytes) per thread: 60 KiB of rows / 512 threads, rounded up
+#define DS_HS 4          // H_LDS: h E8M0 bytes per thread (rows * K / 32 <= 2048 whenever the rows fit 60 KiB)
+#define DS_SCG 2         // SCL: groups per wave whose weight scales are staged in LDS
+#define DS_SCW 2048      // SCL: LDS bytes per wave for them (<= 32 k-chunks of 64 bytes)
 
 // One workgroup per 16-row block of the output; its 8 waves split the selected experts (group slots g = wave,
 // wave + 8, ...), each accumulating sum over its experts and k of W2[e] . h in one MFMA accumulator whose
 // column t is token t; a token absent from a group reads the zero row. The partial accumulators are summed in
 // a fixed order through LDS. A wave walks its (group, k-chunk) space with a scalar iterator, so the weight
 // pipeline runs across expert boundaries without branches.
-// Prologue: every table is fetched in one round trip. H_LDS: all h rows (+ the zero row) are staged in LDS and
-// the weight tiles go out before that staging (their addresses need only the group experts), so the first
-// tiles are in flight while the tables and h are prepared; the vector memory queue then holds weight tiles only.
-template <int TILED, int PF, int NKC, int H_LDS>
+// Prologue: every table is fetched in one round trip. H_LDS: all h rows (+ the zero row) are staged in LDS. Their
+// loads go out right behind the tables and ahead of the weight tiles: loads complete in issue order, so the LDS copy
+// of h then waits for h alone, not for the tiles; the tiles (their addresses need only the group experts) follow as
+// soon as the tables are in. SCL (at most DS_SCG groups per wave, <= 32 k-chunks): each wave's weight scales are
+// fetched with a few wide loads ahead of its tiles and read from LDS per k-step, instead of a one-byte load per
+// lane with every tile (those cost the load unit as much time as the tiles).
+template <int TILED, int PF, int NKC, int H_LDS, int SCL>
 __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_kernel(const DownSumArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ short s_pair[DS_MAX_SLOTS][16];        // pair row of token t in group slot g (zero row if absent)
     __shared__ int s_start[DS_MAX_SLOTS + 1];
     __shared__ short s_tok[DS_MAX_SLOTS];
     __shared__ v4f s_red[DS_WAVES][64];
+    __shared__ __align__(16) uint8_t s_sc[SCL ? DS_WAVES * DS_SCW : 16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nb = blockIdx.x;
@@ -190,7 +198,8 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     // every kernel argument the prologue needs is read in one batch here (the empty asm consumes them), rather
     // than in one scalar round trip per first use
     __asm__ volatile("" ::"s"(a.W), "s"(a.stride_we), "s"(a.S), "s"(a.stride_se), "s"(K), "s"(n_slots), "s"(a.grp_expert),
-                     "s"(a.grp_start), "s"(a.tok_sorted), "s"(a.shard_start), "s"(a.shard_n), "s"(a.hc), "s"(a.ldh), "s"(a.zero_row));
+                     "s"(a.grp_start), "s"(a.tok_sorted), "s"(a.shard_start), "s"(a.shard_n), "s"(a.hc), "s"(a.ldh), "s"(a.zero_row),
+                     "s"(a.hs), "s"(a.ldhs));
 
     // ---- one round trip: this wave's group experts (slot wave + 8 j in lane j), the group starts, the tokens.
     // The loads are unconditional (indices clamped, results masked), so the kernel-argument loads they need go
@@ -202,6 +211,27 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     if (n_slots > 0) {                                        // uniform
         ge = a.grp_expert[min(gslot, n_slots - 1)];
         tk_l = a.tok_sorted[min(tid, n_slots - 1)];
+    }
+    // H_LDS: h rows 0 .. zero_row into registers now (buffer loads: a vector past the rows reads 0 and is not
+    // stored); waves past the last vector issue none
+    const int vpr = K >> 4, n_hv = (a.zero_row + 1) * vpr, n_hs = (a.zero_row + 1) * Ks;
+    v4i HV[H_LDS ? DS_HV : 1];
+    int HS[H_LDS ? DS_HS : 1];
+    if (H_LDS) {
+        const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(a.hc, (uint32_t)((long long)a.zero_row * a.ldh + K));
+        const __amdgpu_buffer_rsrc_t hsr = buffer_rsrc(a.hs, (uint32_t)((long long)a.zero_row * a.ldhs + Ks));
+#pragma unroll
+        for (int i = 0; i < DS_HV; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
+            if (i * DS_WAVES * 64 + wave * 64 < n_hv)   // wave-uniform
+                HV[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(hr, idx < n_hv ? (uint32_t)(r * a.ldh + v * 16) : 0xFFFFFFF0u, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < DS_HS; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid, r = idx / Ks, v = idx - r * Ks;
+            if (i * DS_WAVES * 64 + wave * 64 < n_hs)
+                HS[i] = buffer_load_byte(hsr, idx < n_hs ? (uint32_t)(r * a.ldhs + v) : 0xFFFFFFF0u, 0);
+        }
     }
     int e = gvalid && ge >= 0 ? ge - a.shard_start : -1;
     if (e >= a.shard_n) e = -1;
@@ -231,8 +261,11 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     };
     auto load = [&](int slot, int) {
         // one expert's tiles through a buffer descriptor: scalar base, 32-bit lane offset, scalar k offset
-        A[slot] = buffer_load_tile(buffer_rsrc(a.W + pe * a.stride_we, (uint32_t)a.stride_we), w0, (uint32_t)(pkc * ws));
-        SA[slot] = buffer_load_byte(buffer_rsrc(a.S + pe * a.stride_se, (uint32_t)a.stride_se), s0, (uint32_t)(pkc * ss));
+        // once the wave's groups are exhausted (H_LDS issues its first PF tiles unconditionally) the descriptor is
+        // empty: the load returns zeros without touching memory, and the slot is never consumed
+        const uint32_t wb = pm ? (uint32_t)a.stride_we : 0u, sbn = pm ? (uint32_t)a.stride_se : 0u;
+        A[slot] = buffer_load_tile(buffer_rsrc(a.W + pe * a.stride_we, wb), w0, (uint32_t)(pkc * ws));
+        if (!SCL) SA[slot] = buffer_load_byte(buffer_rsrc(a.S + pe * a.stride_se, sbn), s0, (uint32_t)(pkc * ss));
         if (!H_LDS) {
             B0[slot] = *(const v4i*)phb;
             B1[slot] = *(const v4i*)(phb + 64);
@@ -257,14 +290,18 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
         hb = smem + q * LS + kb * 16;
         hsb = hs_l + q * Ks + kb;
     };
+    // SCL: the wave's staged scales in consume order (group j of the wave at 64 nk j, k-chunk kc at 64 kc within it)
+    const uint8_t* wscl = s_sc + (SCL ? wave * DS_SCW : 0) + col * 4 + kb;
     auto use = [&](int slot) {
         if (H_LDS) {
             const v4i b0 = *(const v4i*)hb;
             const v4i b1 = *(const v4i*)(hb + 64);
             const int sb = *hsb;
+            const int sa = SCL ? (int)*wscl : SA[slot];
             hb += 128;
             hsb += 4;
-            acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
+            if (SCL) wscl += 64;
+            acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, sa, sb);
         } else {
             acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
         }
@@ -274,21 +311,68 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             if (H_LDS) group_rows();
         }
     };
-    if (H_LDS) pipeline_start<PF>(total, load);
+    // SCL: the scales of the wave's first DS_SCG groups (16 rows x nk k-chunks each), older than every tile. A missing
+    // group reads through an empty descriptor (zeros) and is never consumed.
+    v4i SC[SCL ? (TILED ? DS_SCG : 4 * DS_SCG) : 1];
+    if (SCL) {
+        unsigned long long m = vmask;
+#pragma unroll
+        for (int j = 0; j < DS_SCG; ++j) {
+            const int lj = m ? (int)__builtin_ctzll(m) : 0;
+            const long long ej = m ? __builtin_amdgcn_readlane(e, lj) : 0;
+            const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + ej * a.stride_se, m ? (uint32_t)a.stride_se : 0u);
+            if (TILED) {   // the group's bytes are contiguous: 64 nb nk .. + 64 nk
+                SC[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)(nb * nk * 64 + lane * 16), 0, 0));
+            } else {       // row r's bytes are contiguous: one dword (4 k-blocks) per (row, k-chunk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    SC[4 * j + i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)((nb * 16 + r) * Ks + kc * 4), 0, 0);
+                }
+            }
+            m &= m - 1ull;
+        }
+    }
+    if (H_LDS) {
+        // the first PF tiles, unconditionally (pipeline_start's short-stream branch would leave the stores below
+        // after a merge, where the wait count falls back to draining the tiles too)
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            load(i, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
 
-    // ---- tables -> LDS (and h rows 0 .. zero_row when H_LDS), then the pair rows of every valid group
+    // ---- tables -> LDS (and h rows 0 .. zero_row when H_LDS: their loads are older than every tile), the wave's
+    // weight scales (SCL), then the pair rows of every valid group
     if (tid <= n_slots) s_start[tid] = st;
     if (tid < n_slots) s_tok[tid] = (short)tk;
     if (H_LDS) {
-        const int vpr = K >> 4;
-        for (int i = tid; i < (a.zero_row + 1) * vpr; i += blockDim.x) {
-            const int r = i / vpr, v = i - r * vpr;
-            *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.hc + (long long)r * a.ldh + v * 16);
+#pragma unroll
+        for (int i = 0; i < DS_HV; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
+            if (i * DS_WAVES * 64 + wave * 64 < n_hv && idx < n_hv) *(v4i*)(smem + r * LS + v * 16) = HV[i];
         }
         uint8_t* hsw = smem + (size_t)(a.zero_row + 1) * LS;
-        for (int i = tid; i < (a.zero_row + 1) * Ks; i += blockDim.x) {
-            const int r = i / Ks, v = i - r * Ks;
-            hsw[r * Ks + v] = a.hs[(long long)r * a.ldhs + v];
+#pragma unroll
+        for (int i = 0; i < DS_HS; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid;
+            if (i * DS_WAVES * 64 + wave * 64 < n_hs && idx < n_hs) hsw[idx] = (uint8_t)HS[i];
+        }
+    }
+    if (SCL) {
+        uint8_t* w = s_sc + wave * DS_SCW;
+#pragma unroll
+        for (int j = 0; j < DS_SCG; ++j) {
+            if (TILED) {
+                if (lane * 16 < nk * 64) *(v4i*)(w + j * nk * 64 + lane * 16) = SC[j];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    if (kc < nk) *(int*)(w + (j * nk + kc) * 64 + r * 4) = SC[4 * j + i].x;
+                }
+            }
         }
     }
     __syncthreads();
@@ -301,7 +385,13 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     __syncthreads();
     if (H_LDS) {
         group_rows();
-        pipeline_finish<PF>(total, load, use);
+        if (total >= PF) {
+            pipeline_finish<PF>(total, load, use);
+        } else {   // every tile of the wave is in slots 0 .. total - 1 already
+#pragma unroll
+            for (int i = 0; i < PF; ++i)
+                if (i < total) use(i);
+        }
     } else {
         prod_rows();
         pipelined<PF>(total, load, use);
@@ -382,9 +472,14 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
     const bool h_lds = lds <= 60 * 1024;
     const dim3 grid(N / 16), block(DS_WAVES * 64);
-#define DS_LAUNCH(T, PF, NK, HL) moe_down_sum_kernel<T, PF, NK, HL><<<grid, block, HL ? lds : 0, st>>>(a)
-    if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1); else DS_LAUNCH(0, 12, 0, 1); }
-    else { if (tiled) DS_LAUNCH(1, 8, 0, 0); else DS_LAUNCH(0, 8, 0, 0); }
+    // weight scales through LDS when every wave holds at most DS_SCG groups of <= 16 k-chunks and the scale rows are
+    // 16-byte aligned for the wide loads
+    const bool scl = h_lds && (n_slots + DS_WAVES - 1) / DS_WAVES <= DS_SCG && K / 128 <= 16 && (((uintptr_t)S) & 15) == 0 &&
+                     (stride_se & 15) == 0;
+#define DS_LAUNCH(T, PF, NK, HL, SC) moe_down_sum_kernel<T, PF, NK, HL, SC><<<grid, block, HL ? lds : 0, st>>>(a)
+    if (scl) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 1); else DS_LAUNCH(0, 12, 0, 1, 1); }
+    else if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 0); else DS_LAUNCH(0, 12, 0, 1, 0); }
+    else { if (tiled) DS_LAUNCH(1, 8, 0, 0, 0); else DS_LAUNCH(0, 8, 0, 0, 0); }
 #undef DS_LAUNCH
     return (int)hipGetLastError();
 }
