@@ -140,14 +140,15 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     v4i SC[TILED ? 2 : 8];
     auto scale_load = [&]() {
         if (TILED) {   // the stream's bytes are contiguous: (nb nk + k0c) 64 .. + 64 nk_w
+            // lanes past the stream's nk_w * 64 bytes get an offset past the descriptor: no fetch, zeros
             const uint32_t b = (uint32_t)stile_off<1>(nb, k0c, nk, Ks, 0) + lane * 16;
-            SC[0] = buffer_load_tile(sr, b, 0);
-            SC[1] = buffer_load_tile(sr, b, 1024);
+            SC[0] = buffer_load_tile(sr, lane * 16 < nk_w * 64 ? b : 0xFFFFFFF0u, 0);
+            SC[1] = buffer_load_tile(sr, 1024 + lane * 16 < nk_w * 64 ? b + 1024 : 0xFFFFFFF0u, 0);
         } else {       // row r's bytes k0c 4 .. are contiguous: one dword (4 k-blocks) per (row, k-chunk)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int idx = 64 * i + lane, r = idx & 15, j = idx >> 4;
-                SC[i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)((nb * 16 + r) * Ks + (k0c + j) * 4), 0, 0);
+                SC[i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, j < nk_w ? (uint32_t)((nb * 16 + r) * Ks + (k0c + j) * 4) : 0xFFFFFFF0u, 0, 0);
             }
         }
     };

@@ -322,12 +322,13 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             const long long ej = m ? __builtin_amdgcn_readlane(e, lj) : 0;
             const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + ej * a.stride_se, m ? (uint32_t)a.stride_se : 0u);
             if (TILED) {   // the group's bytes are contiguous: 64 nb nk .. + 64 nk
-                SC[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)(nb * nk * 64 + lane * 16), 0, 0));
+                SC[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                    sr, lane * 16 < nk * 64 ? (uint32_t)(nb * nk * 64 + lane * 16) : 0xFFFFFFF0u, 0, 0));   // past the group: no fetch
             } else {       // row r's bytes are contiguous: one dword (4 k-blocks) per (row, k-chunk)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
-                    SC[4 * j + i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, (uint32_t)((nb * 16 + r) * Ks + kc * 4), 0, 0);
+                    SC[4 * j + i].x = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, kc < nk ? (uint32_t)((nb * 16 + r) * Ks + kc * 4) : 0xFFFFFFF0u, 0, 0);
                 }
             }
             m &= m - 1ull;
