@@ -37,7 +37,7 @@ struct DecodeUpArgs {
     int* grp_expert; int* grp_start; int* tok_sorted; float* wt_sorted;   // tables, P = M * topk slots
 };
 
-template <int TILED, int PF, int PER, int EARLY>
+template <int TILED, int PF, int PER, int EARLY, int SCL>
 __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const DecodeUpArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];   // staged activation rows (codes) then their E8M0 bytes
     __shared__ int s_eid[UP_MAXM * UP_MAXK];
@@ -47,7 +47,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
     __shared__ int s_mg, s_pick, s_xready;
     __shared__ v4f s_acc[UP_WAVES][64];
-    __shared__ __align__(16) uint8_t s_wsc[EARLY ? UP_WAVES * UP_WSC : 16];
+    __shared__ __align__(16) uint8_t s_wsc[SCL ? UP_WAVES * UP_WSC : 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform values kept in scalar registers
@@ -130,13 +130,14 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     int SA[PF];
     auto load = [&](int slot, int kc) {
         A[slot] = buffer_load_tile(wr, wv, (uint32_t)(kc * ws));
-        if (!early) SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
+        if (!SCL) SA[slot] = buffer_load_byte(sr, sv, (uint32_t)(kc * ss));
     };
-    // One token: a wave's E8M0 bytes (16 rows x nk_w k-chunks) are fetched with a few wide loads when its expert is
-    // known, ahead of its first tiles, and kept in LDS in MFMA order (k-chunk j at 64 j, row r's byte for k-block kb
-    // at 4 r + kb), so each k-step reads its scale from LDS instead of issuing a byte load per lane: the byte loads
-    // cost as much load-unit time as the weight tiles themselves.
-    uint8_t* const wsc = s_wsc + (EARLY ? wave * UP_WSC : 0);
+    // SCL (always for one token; for M tokens when a wave's stream has <= 32 k-chunks): a wave's E8M0 bytes (16
+    // rows x nk_w k-chunks) are fetched with a few wide loads when its expert is known, ahead of its first tiles,
+    // and kept in LDS in MFMA order (k-chunk j at 64 j, row r's byte for k-block kb at 4 r + kb), so each k-step
+    // reads its scale from LDS instead of issuing a byte load per lane: the byte loads cost as much load-unit
+    // time as the weight tiles themselves.
+    uint8_t* const wsc = s_wsc + (SCL ? wave * UP_WSC : 0);
     v4i SC[TILED ? 2 : 8];
     auto scale_load = [&]() {
         if (TILED) {   // the stream's bytes are contiguous: (nb nk + k0c) 64 .. + 64 nk_w
@@ -295,7 +296,10 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             U += c;
         }
         if (g >= U && !publish) return;   // uniform: fewer experts than slots
-        if (g < U) set_expert(eg);
+        if (g < U) {
+            set_expert(eg);
+            if (SCL) scale_load();   // lands while the members are found and their rows staged
+        }
 
         // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
         if (tid == 0) s_mg = 0;
@@ -321,16 +325,16 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
 
     const uint8_t* xl;
     const uint8_t* xsl;
-    const uint8_t* wsl = wsc + (lane & 15) * 4 + kb;   // one token: this lane's weight scale of k-chunk 0
+    const uint8_t* wsl;   // SCL: this lane's weight scale of the next k-chunk
     v4f acc;
     auto use = [&](int slot) {
         const v4i b0 = *(const v4i*)(xl);
         const v4i b1 = *(const v4i*)(xl + 64);
         const int sb = *xsl;
-        const int sa = early ? (int)*wsl : SA[slot];
+        const int sa = SCL ? (int)*wsl : SA[slot];
         xl += 128;
         xsl += 4;
-        if (early) wsl += 64;
+        if (SCL) wsl += 64;
         acc = mfma_fp4w_fp8x(v8i{A[slot].x, A[slot].y, A[slot].z, A[slot].w, 0, 0, 0, 0},
                              v8i{b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w}, acc, sa, sb);
     };
@@ -339,6 +343,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         const int brow = col < mp ? col : 0;
         xl = smem + brow * LS + k0c * 128 + kb * 16;
         xsl = lds_s + brow * Ks + k0c * 4 + kb;
+        wsl = wsc + (lane & 15) * 4 + kb;
         acc = v4f{0.f, 0.f, 0.f, 0.f};
     };
     // SwiGLU epilogue: half-wave i handles member base + i; lane c of it handles column c0 + c
@@ -382,9 +387,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     } else {
         // passes of up to a.rows members (16 B columns); a group with more members than LDS rows holds (possible
         // only when many tokens share an expert) streams the expert's weights once per pass
-        for (int base = 0; base < mg; base += a.rows) {
-            const int mp = min(a.rows, mg - base);
-            if (base > 0) __syncthreads();   // LDS rows are reused
+        auto stage = [&](int base, int mp) {
 #pragma unroll 1
             for (int i = tid; i < mp * per_row; i += blockDim.x) {
                 const int r = i / per_row, q = i - r * per_row;
@@ -392,10 +395,25 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 x_load(s_tok[base + r], q, r0, r1);
                 x_store(r, q, r0, r1);
             }
+            if (SCL && base == 0) scale_store();   // its loads are older than the rows just staged
             __syncthreads();
-            start_pass(mp);
+        };
+        // (M tokens keep 4 tiles in flight per wave: in-process A/B at M = 4 / 16, 8 tiles in the one-pass case
+        // ran 1.7 % / 2.5 % slower)
+        if (work && mg <= a.rows) {   // one pass (the common case), outside the pass loop
+            stage(0, mg);
+            start_pass(mg);
             pipelined<PF>(nk_w, load, use);
-            epilogue(base, mp);
+            epilogue(0, mg);
+        } else if (work) {
+            for (int base = 0; base < mg; base += a.rows) {
+                const int mp = min(a.rows, mg - base);
+                if (base > 0) __syncthreads();   // LDS rows are reused
+                stage(base, mp);
+                start_pass(mp);
+                pipelined<PF>(nk_w, load, use);
+                epilogue(base, mp);
+            }
         }
     }
 
@@ -451,11 +469,14 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
         stride_we < (long long)2 * I * (H / 2) || stride_se < (long long)2 * I * (H / 32)) return DSV41_EINVAL;
     // M = 1: the single token's codes are staged while the routing runs (one LDS row, H / 16 <= 448 lanes: the
     // seven waves besides the gate's).
-    // M > 1: members are staged after the bucketing, up to `rows` per pass, as many as fit in 60 KiB of LDS
-    // (two workgroups per CU)
+    // M > 1: members are staged after the bucketing, up to `rows` per pass, as many as fit in 44 KiB of LDS (60 KiB
+    // without the staged weight scales), so two workgroups fit per CU
     const size_t row_bytes = (size_t)(H + 16) + (size_t)(H / 32);
     const bool early = M == 1 && H / 16 <= (UP_WAVES - 1) * 64;
-    int rows = early ? 1 : (int)((60 * 1024) / row_bytes);
+    // M tokens: weight scales through LDS (16 KiB per workgroup) when a wave's stream has <= 32 k-chunks; the rows
+    // then get 44 KiB, so two workgroups still fit per CU
+    const bool scl = early || (H / 128 + 1) / 2 <= UP_WSC / 64;
+    int rows = early ? 1 : (int)(((scl ? 44 : 60) * 1024) / row_bytes);
     rows = rows > 16 ? 16 : (rows > M ? M : rows);
     if (rows < 1) return DSV41_EINVAL;
     DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
@@ -465,8 +486,9 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
     hipStream_t st = (hipStream_t)stream;
 #define UP_LAUNCH(T, PER)                                                                                         \
     do {                                                                                                      \
-        if (early) moe_decode_up_kernel<T, 8, PER, 1><<<grid, block, lds, st>>>(a);                           \
-        else moe_decode_up_kernel<T, 4, PER, 0><<<grid, block, lds, st>>>(a);                                 \
+        if (early) moe_decode_up_kernel<T, 8, PER, 1, 1><<<grid, block, lds, st>>>(a);                        \
+        else if (scl) moe_decode_up_kernel<T, 4, PER, 0, 1><<<grid, block, lds, st>>>(a);                     \
+        else moe_decode_up_kernel<T, 4, PER, 0, 0><<<grid, block, lds, st>>>(a);                              \
     } while (0)
     if (E <= 256) { if (tiled) UP_LAUNCH(1, 4); else UP_LAUNCH(0, 4); }
     else if (E <= 384) { if (tiled) UP_LAUNCH(1, 6); else UP_LAUNCH(0, 6); }

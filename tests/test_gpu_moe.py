@@ -282,6 +282,27 @@ def test_decode_full_batched_equals_single(full_layer, M):
     close(yb[t:t + 1].cpu().numpy(), ref, f"decode configs[2] M={M} token {t}")
 
 
+def test_decode_full_shared_experts_multipass(full_layer):
+    """Every token of a 16-token step picks the same 8 experts: each group holds 16 members, more than the LDS rows
+    the up kernel stages at hidden 7168, so it streams each expert in several passes (and the down kernel takes
+    its unstaged path). Batched equals single-token steps, and one token matches the oracle."""
+    from dsv41_amd import moe, quant
+    E, H, I, ws, ex = full_layer
+    M = 16
+    eid1, _ = rand_routing(1, E, 8, 77)
+    eid = np.repeat(eid1, M, axis=0)
+    wt = np.random.default_rng(78).random((M, 8)).astype(np.float32)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 79).to(DEV))
+    ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
+    yb = moe.moe_experts(xq, ed, wd, ex, 10.0).clone()
+    for t in (0, 7, 15):
+        ys = moe.moe_experts(xq[t:t + 1].contiguous(), ed[t:t + 1].contiguous(), wd[t:t + 1].contiguous(), ex, 10.0)
+        assert O.rel_l2(yb[t].cpu().numpy(), ys[0].cpu().numpy()) < 1e-5
+    W13, S13, W2, S2 = host_subset(ws, set(eid1[0].tolist()))
+    ref = O.moe_layer_routed(bf16_vals(xq[9:10]), eid[9:10], wt[9:10], W13, S13, W2, S2, I, 10.0)
+    close(yb[9:10].cpu().numpy(), ref, "decode configs[2] shape, 16 members per group, token 9")
+
+
 def test_decode_layer_with_shared_expert_and_router(full_layer):
     """Whole layer: router GEMV (bf16 [384, 7168]) -> softmax top-8 -> shared bf16 SwiGLU + routed experts ->
     bf16(sum + ys). Each stage against the oracle in fp32 (the tolerance is defined on fp32 outputs), and the
