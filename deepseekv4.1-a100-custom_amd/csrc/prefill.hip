@@ -44,7 +44,8 @@ struct PrefillArgs {
 // Every operand moves HBM/L2 -> LDS through the load unit itself (buffer_load ... lds, all through buffer descriptors):
 // no staging registers, PV_NS k-steps (PV_NS x 33 KB) in flight per workgroup. Per k-step, with wave-uniform
 // branches only: wave w loads weight slots 2 w, 2 w + 1 (1 KB each, 16 B per lane) and token block w (two 1 KB
-// halves); waves 0-3 the E8M0 bytes of 4 weight slots each; waves 4-5 the E8M0 words of 64 pairs each.
+// halves); the E8M0 bytes of the 16 weight slots (tiled: wave 0, 16 B per lane; row-major: waves 0-3, 4 slots each);
+// waves 4-5 the E8M0 words of 64 pairs each.
 // A wave waits for its own loads with vmcnt (they complete in order), then a barrier makes every wave's part
 // visible. The load unit writes lane l's 16 bytes to LDS offset 16 l, and each lane chooses which 16 global
 // bytes it fetches, so the tiles land in MFMA operand order: weight slot s holds, at 16 l, the 16 bytes lane l
@@ -123,8 +124,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     };
     const uint32_t a_voff0 = a_off(nbw0), a_voff1 = a_off(nbw1);
     const int a_ks = TILED ? 1024 : 64;
-    const int asb = block_of(4 * (wave & 3) + (lane >> 4)), asr = lane & 15;   // waves 0-3: 4 slots' scales
-    const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + asr * 4) : (uint32_t)((asb * 16 + asr) * Ks);
+    // weight scales of the 16 slots (64 bytes each per k-step). Tiled: a slot's 64 bytes are contiguous, so wave 0
+    // fetches all 1 KB with 16 bytes per lane (lane l: slot l / 4, bytes 16 (l % 4)). Row-major: 4 bytes per row,
+    // waves 0-3 fetch 4 slots each with 4 bytes per lane (lane l: slot 4 w + l / 16, row l % 16).
+    const int asb = TILED ? block_of(lane >> 2) : block_of(4 * (wave & 3) + (lane >> 4)), asr = lane & 15;
+    const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + (lane & 3) * 16) : (uint32_t)((asb * 16 + asr) * Ks);
     const int as_ks = TILED ? 64 : 4;
     // MFMA B layout of token block `wave`: half h, lane l takes pair 16 wave + l % 16, k chunk 4 h + l / 16
     // activation rows through buffer descriptors too: reads past x_rows return 0, and with no FLAT-encoded load in
@@ -133,14 +137,16 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     const uint32_t b0off = (uint32_t)s_row[16 * wave + col] * (uint32_t)a.ldx + kb * 16;
     const uint32_t bsoff = (uint32_t)s_row[(64 * (wave & 1) + lane) & (PG_T - 1)] * (uint32_t)a.ldxs;
     const bool ldb = 16 * wave < m;   // wave-uniform: the token block holds pairs of the group
-    const bool lda = wave < 4, ldbs = (wave == 4 || wave == 5) && 64 * (wave & 1) < m;
+    const bool lda = TILED ? wave == 0 : wave < 4, ldbs = (wave == 4 || wave == 5) && 64 * (wave & 1) < m;
     const int per_step = 2 + (lda ? 1 : 0) + (ldb ? 2 : 0) + (ldbs ? 1 : 0);
     auto issue = [&](int kc, int st) {
         uint8_t* so = smem + st * PV_STAGE;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + 2 * wave * 1024), 16, a_voff0, (uint32_t)(kc * a_ks), 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + (2 * wave + 1) * 1024), 16, a_voff1, (uint32_t)(kc * a_ks), 0, 0);
-        if (lda)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
+        if (lda) {
+            if (TILED) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS), 16, as_voff, (uint32_t)(kc * as_ks), 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
+        }
         if (ldb) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048), 16, b0off, (uint32_t)(kc * 128), 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048 + 1024), 16, b0off + 64, (uint32_t)(kc * 128), 0, 0);
