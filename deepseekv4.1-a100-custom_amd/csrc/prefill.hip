@@ -73,6 +73,16 @@ __device__ __forceinline__ void wait_vm(int n) {   // s_waitcnt vmcnt(n), 0 <= n
 #undef PV_W
 }
 
+template <int N>
+__device__ __forceinline__ void wait_vm_c() {   // s_waitcnt vmcnt(N), N a compile-time constant
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+template <int N>
+struct IntC {
+    static constexpr int value = N;
+};
+
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];   // PV_NS stages of PV_STAGE bytes
@@ -195,35 +205,49 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
                 acc[j][u] = mfma_fp4w_fp8x(v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], (int)OSA[r][j], (int)OSB[r][u]);
         }
     };
-    // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue) and
-    // one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, nk - 1) for kk = 0 and
-    // min(PV_NS - 2, nk - 1 - kk) after that.
-    auto sync_step = [&](int kk) {
-        const int after = kk == 0 ? min(PV_NS - 1, nk - 1) : min(PV_NS - 2, nk - 1 - kk);
-        wait_vm(per_step * after);
-        __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    };
+    // The k-loop, instantiated per value of this wave's DMA count per step (2 .. 5, fixed for the item), so the
+    // steady-state wait below is one constant s_waitcnt instead of a compare-and-branch tree on a runtime count.
+    auto kloop = [&](auto ps_c) {
+        constexpr int PS = decltype(ps_c)::value;
+        // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue)
+        // and one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, nk - 1) for kk = 0
+        // and min(PV_NS - 2, nk - 1 - kk) after that.
+        auto sync_step = [&](int kk) {
+            const int after = kk == 0 ? min(PV_NS - 1, nk - 1) : min(PV_NS - 2, nk - 1 - kk);
+            if (after == PV_NS - 2) wait_vm_c<PS * (PV_NS - 2)>();
+            else wait_vm(PS * after);
+            __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        };
 
-    for (int s0 = 0; s0 < PV_NS; ++s0)
-        if (s0 < nk) issue(s0, s0);
-    sync_step(0);
-    read_ops(0, 0);
-    for (int kk = 0; kk < nk; kk += 2) {
-        if (kk + 1 < nk) {
-            sync_step(kk + 1);                                    // every wave has read step kk: refill its stage
-            if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS);
-            read_ops(kk + 1, 1);
+        for (int s0 = 0; s0 < PV_NS; ++s0)
+            if (s0 < nk) issue(s0, s0);
+        sync_step(0);
+        read_ops(0, 0);
+        for (int kk = 0; kk < nk; kk += 2) {
+            if (kk + 1 < nk) {
+                sync_step(kk + 1);                                    // every wave has read step kk: refill its stage
+                if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS);
+                read_ops(kk + 1, 1);
+            }
+            mfmas(0);
+            if (kk + 1 >= nk) break;
+            if (kk + 2 < nk) {
+                sync_step(kk + 2);
+                if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS);
+                read_ops(kk + 2, 0);
+            }
+            mfmas(1);
         }
-        mfmas(0);
-        if (kk + 1 >= nk) break;
-        if (kk + 2 < nk) {
-            sync_step(kk + 2);
-            if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS);
-            read_ops(kk + 2, 0);
-        }
-        mfmas(1);
+    };
+    // per_step = 2 (weight tiles) + 1 (weight scales: wave 0 tiled, waves 0-3 row-major) + 2 (a token block) + 1
+    // (token scales: waves 4-5), never both scale streams in one wave: 2 .. 5
+    switch (per_step) {
+        case 2: kloop(IntC<2>{}); break;
+        case 3: kloop(IntC<3>{}); break;
+        case 4: kloop(IntC<4>{}); break;
+        default: kloop(IntC<5>{}); break;
     }
     __syncthreads();
 
