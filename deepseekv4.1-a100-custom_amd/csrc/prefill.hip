@@ -149,7 +149,9 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     const bool ldb = 16 * wave < m;   // wave-uniform: the token block holds pairs of the group
     const bool lda = TILED ? wave == 0 : wave < 4, ldbs = (wave == 4 || wave == 5) && 64 * (wave & 1) < m;
     const int per_step = 2 + (lda ? 1 : 0) + (ldb ? 2 : 0) + (ldbs ? 1 : 0);
-    auto issue = [&](int kc, int st) {
+    // `full` (a compile-time flag inside the k-loop): the group holds all 128 pairs, so every wave loads its token
+    // block and computes all four of its blocks, and the per-step checks of tb_on / ldb drop out
+    auto issue = [&](int kc, int st, auto full_c) {
         uint8_t* so = smem + st * PV_STAGE;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + 2 * wave * 1024), 16, a_voff0, (uint32_t)(kc * a_ks), 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + (2 * wave + 1) * 1024), 16, a_voff1, (uint32_t)(kc * a_ks), 0, 0);
@@ -157,7 +159,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
             if (TILED) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS), 16, as_voff, (uint32_t)(kc * as_ks), 0, 0);
             else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
         }
-        if (ldb) {
+        if (decltype(full_c)::value || ldb) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048), 16, b0off, (uint32_t)(kc * 128), 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048 + 1024), 16, b0off + 64, (uint32_t)(kc * 128), 0, 0);
         }
@@ -172,9 +174,10 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     for (int u = 0; u < 4; ++u) tb_on[u] = 64 * ph + 16 * u < m;
     v4i OA[2][4], OB0[2][4], OB1[2][4];
     uint8_t OSA[2][4], OSB[2][4];   // E8M0 bytes, widened at the MFMA that uses them
-    auto read_ops = [&](int kk, int r) {
+    auto read_ops = [&](int kk, int r, auto full_c) {
+        constexpr bool full = decltype(full_c)::value;
         const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
-        if (tb_on[0]) {   // wave-uniform: a wave whose half of the group is empty runs no MFMA
+        if (full || tb_on[0]) {   // wave-uniform: a wave whose half of the group is empty runs no MFMA
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
@@ -183,7 +186,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            if (!tb_on[u]) continue;
+            if (!full && !tb_on[u]) continue;
             const uint8_t* bt = st + PV_B + (4 * ph + u) * 2048 + lofs;
             OB0[r][u] = *(const v4i*)bt;
             OB1[r][u] = *(const v4i*)(bt + 1024);
@@ -195,10 +198,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc[j][u] = v4f{0.f, 0.f, 0.f, 0.f};
-    auto mfmas = [&](int r) {
+    auto mfmas = [&](int r, auto full_c) {
+        constexpr bool full = decltype(full_c)::value;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            if (!tb_on[u]) continue;
+            if (!full && !tb_on[u]) continue;
             const v8i bv = v8i{OB0[r][u].x, OB0[r][u].y, OB0[r][u].z, OB0[r][u].w, OB1[r][u].x, OB1[r][u].y, OB1[r][u].z, OB1[r][u].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -207,7 +211,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     };
     // The k-loop, instantiated per value of this wave's DMA count per step (2 .. 5, fixed for the item), so the
     // steady-state wait below is one constant s_waitcnt instead of a compare-and-branch tree on a runtime count.
-    auto kloop = [&](auto ps_c) {
+    auto kloop = [&](auto ps_c, auto full_c) {
         constexpr int PS = decltype(ps_c)::value;
         // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue)
         // and one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, nk - 1) for kk = 0
@@ -222,32 +226,38 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
         };
 
         for (int s0 = 0; s0 < PV_NS; ++s0)
-            if (s0 < nk) issue(s0, s0);
+            if (s0 < nk) issue(s0, s0, full_c);
         sync_step(0);
-        read_ops(0, 0);
+        read_ops(0, 0, full_c);
         for (int kk = 0; kk < nk; kk += 2) {
             if (kk + 1 < nk) {
                 sync_step(kk + 1);                                    // every wave has read step kk: refill its stage
-                if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS);
-                read_ops(kk + 1, 1);
+                if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS, full_c);
+                read_ops(kk + 1, 1, full_c);
             }
-            mfmas(0);
+            mfmas(0, full_c);
             if (kk + 1 >= nk) break;
             if (kk + 2 < nk) {
                 sync_step(kk + 2);
-                if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS);
-                read_ops(kk + 2, 0);
+                if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS, full_c);
+                read_ops(kk + 2, 0, full_c);
             }
-            mfmas(1);
+            mfmas(1, full_c);
         }
     };
     // per_step = 2 (weight tiles) + 1 (weight scales: wave 0 tiled, waves 0-3 row-major) + 2 (a token block) + 1
-    // (token scales: waves 4-5), never both scale streams in one wave: 2 .. 5
-    switch (per_step) {
-        case 2: kloop(IntC<2>{}); break;
-        case 3: kloop(IntC<3>{}); break;
-        case 4: kloop(IntC<4>{}); break;
-        default: kloop(IntC<5>{}); break;
+    // (token scales: waves 4-5), never both scale streams in one wave: 2 .. 5; a full group loads every token
+    // block (4 or 5)
+    if (m == PG_T) {
+        if (per_step == 4) kloop(IntC<4>{}, IntC<1>{});
+        else kloop(IntC<5>{}, IntC<1>{});
+    } else {
+        switch (per_step) {
+            case 2: kloop(IntC<2>{}, IntC<0>{}); break;
+            case 3: kloop(IntC<3>{}, IntC<0>{}); break;
+            case 4: kloop(IntC<4>{}, IntC<0>{}); break;
+            default: kloop(IntC<5>{}, IntC<0>{}); break;
+        }
     }
     __syncthreads();
 
