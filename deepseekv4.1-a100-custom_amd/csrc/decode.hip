@@ -19,7 +19,7 @@
 #define UP_MAXM 16
 #define UP_MAXK 16
 #define UP_MAXE 512
-#define UP_WSC 2048   // one token: E8M0 bytes of a wave's weight stream staged in LDS (<= 32 k-chunks of 64 bytes)
+#define UP_WSC 2048   // SCL: E8M0 bytes of a wave's weight stream staged in LDS (<= 32 k-chunks of 64 bytes)
 
 struct DecodeUpArgs {
     const float* logits; long long ldl;      // fp32 [M][E] router logits (or NULL: eid_in / wt_in given)
@@ -91,8 +91,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
 
     // ---- one token (EARLY): wave gw runs the gate while the other seven waves stage the token's activations in LDS
     // row 0. The gate is the critical path, so wave gw issues the logits loads first, before the barrier below.
-    // compile-time, so the one-token instantiation holds none of the member-pass code: the host launches EARLY only
-    // for M == 1 and per_row <= (UP_WAVES - 1) * 64
+    // `early` is compile-time, so the one-token instantiation holds none of the member-pass code (the host launches
+    // EARLY only for M == 1 and per_row <= (UP_WAVES - 1) * 64).
     constexpr bool early = EARLY != 0;
     GateRow<PER> gr;
     // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
