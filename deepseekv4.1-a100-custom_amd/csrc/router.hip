@@ -8,7 +8,8 @@
 // write xn and xq = fake_quant_fp8(xn) (quant.py:34-54) for the experts and the next step: the workgroups of
 // row block 0 each write their own k range.
 // Each workgroup recomputes the rms statistics of all M rows (M x 28 KB of L2 reads, one round trip per row)
-// rather than waiting on another launch; its 16 x 512 weight tile is in flight meanwhile.
+// rather than waiting on another launch; its 16 x 512 weight tile and its slice of the norm weight are in flight
+// meanwhile, and the threads that hold its own k range of r keep it in LDS, so nothing is loaded twice.
 #include "common.h"
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -53,6 +54,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     __shared__ float s_ss[RT_THREADS / 64][RT_MAXM];
     __shared__ float s_inv[RT_MAXM];
     __shared__ __align__(16) uint16_t s_xn[RT_MAXM][RT_KC + 8];
+    __shared__ __align__(16) float s_r[RT_MAXM][RT_KC];   // this workgroup's k range of r
     __shared__ v4f s_acc[RT_THREADS / 64][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -66,6 +68,12 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     const uint16_t* gp = a.G + (long long)(rb * 16 + col) * a.ldg + k0 + kg * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) A[i] = __builtin_nontemporal_load((const v4i*)(gp + i * 32));
+    // the norm weight of this workgroup's k range: thread tid < 128 holds 8 values
+    const int nkv = RT_KC / 8;
+    float wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wv[j] = 1.f;
+    if (a.w && tid < nkv) load8(a.w + ks * RT_KC + tid * 8, wv);
 
     // ---- sum of squares of r per row. A thread owns vectors tid, tid + 512, ... (at most 2 for H <= 8192);
     // their loads are issued together (indices clamped, out-of-range vectors weighted 0), one round trip per row.
@@ -80,15 +88,18 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
 #pragma unroll
             for (int j = 0; j < 8; ++j) ss += m * f[u][j] * f[u][j];
         }
+        // vectors ks * 128 .. + 127 of the row are this workgroup's k range: kept for the normalisation below
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int v = tid + u * RT_THREADS - ks * nkv;
+            if (v >= 0 && v < nkv) {
+                *(v4f*)&s_r[t][v * 8] = v4f{f[u][0], f[u][1], f[u][2], f[u][3]};
+                *(v4f*)&s_r[t][v * 8 + 4] = v4f{f[u][4], f[u][5], f[u][6], f[u][7]};
+            }
+        }
         ss = wave_reduce_sum(ss);
         if (lane == 0) s_ss[wave][t] = ss;
     }
-    // this workgroup's k range of r (128 vectors per row) is loaded before the reduction completes
-    const int nkv = RT_KC / 8;
-    const bool kmine = tid < M * nkv;       // M <= 4: one vector per thread
-    float rk[8];
-    const int kt = kmine ? tid / nkv : 0, kv = tid - kt * nkv;
-    if (M * nkv <= RT_THREADS && kmine) load_r8(a, kt, ks * RT_KC + kv * 8, rk);
     __syncthreads();
     if (tid < M) {
         float tot = 0.f;
@@ -98,21 +109,21 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     }
     __syncthreads();
 
-    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there
+    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there. Thread
+    // tid handles vector tid % 128 of rows tid / 128, tid / 128 + 4, ... (the vector its norm weight slice covers
+    // when tid < 128; the others read it from LDS)
+    __shared__ __align__(16) float s_w[RT_KC];
+    if (tid < nkv) {
+        *(v4f*)&s_w[tid * 8] = v4f{wv[0], wv[1], wv[2], wv[3]};
+        *(v4f*)&s_w[tid * 8 + 4] = v4f{wv[4], wv[5], wv[6], wv[7]};
+    }
+    __syncthreads();
     for (int i = tid; i < M * nkv; i += RT_THREADS) {
         const int t = i / nkv, v = i - t * nkv;
         const int k = ks * RT_KC + v * 8;
-        float f[8], wv[8];
-        if (M * nkv <= RT_THREADS) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) f[j] = rk[j];
-        } else {
-            load_r8(a, t, k, f);
-        }
-        if (a.w) load8(a.w + k, wv);
         float n[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) n[j] = bf16_round(f[j] * s_inv[t] * (a.w ? wv[j] : 1.f));
+        for (int j = 0; j < 8; ++j) n[j] = bf16_round(s_r[t][v * 8 + j] * s_inv[t] * s_w[v * 8 + j]);
         uint32_t on[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) on[j] = f32_to_bf16_bits(n[2 * j]) | (f32_to_bf16_bits(n[2 * j + 1]) << 16);
