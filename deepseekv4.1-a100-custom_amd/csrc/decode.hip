@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // workgroups a CU holds do not run their gates on the same SIMD
     const int gw = (int)((blockIdx.x + blockIdx.y * gridDim.x) & 3);
     const bool gwave = early && wave == gw;
-    if (gwave && a.logits && a.nparts == 1) gr.load_logits(a.logits, E);
+    if (gwave && a.logits) gr.load_logits(a.logits, E, a.nparts, a.pstride);
     const int xq = (wave - (wave > gw ? 1 : 0)) * 64 + lane;   // early: the lane's 16 values of row 0 among the stagers
     v4i xr0, xr1;
     if (early && !gwave && xq < per_row) x_load(0, xq, xr0, xr1);

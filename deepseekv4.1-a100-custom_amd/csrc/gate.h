@@ -17,14 +17,21 @@ struct GateRow {
     unsigned lk;   // the lane's best remaining key, its slot (lowest on ties) and score
     int li;
     float ls;
-    float raw[PER];   // one part of logits, loaded ahead of prepare() by load_logits()
+    // the logits may arrive as nparts partial sums (a split-K router GEMV); loads go out Q parts at a time
+    static constexpr int Q = PER <= 8 ? 8 : 1;
+    float raw[Q][PER];   // the first batch of parts, loaded ahead of prepare() by load_logits()
     bool loaded = false;
 
-    // issue the loads of one part of logits now (a caller can do this first thing, before any barrier)
-    __device__ __forceinline__ void load_logits(const float* __restrict__ S, int E) {
+    // issue the loads of the first Q parts of logits now (a caller can do this first thing, before any barrier).
+    // Addresses are clamped (to the last entry, the last part), so no branch splits the batch; prepare() masks.
+    __device__ __forceinline__ void load_logits(const float* __restrict__ S, int E, int nparts, long long pstride) {
         const int e0 = (threadIdx.x & 63) * PER;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) raw[i] = S[min(e0 + i, E - 1)];   // clamped: no branch per load; masked in prepare()
+        for (int q = 0; q < (nparts == 1 ? 1 : Q); ++q) {
+            const long long off = (long long)min(q, nparts - 1) * pstride;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) raw[q][i] = S[off + min(e0 + i, E - 1)];
+        }
         loaded = true;
     }
 
@@ -46,16 +53,13 @@ struct GateRow {
         const int lane = threadIdx.x & 63;
         const int e0 = lane * PER;
         float mx = -INFINITY;
-        // the logits may arrive as nparts partial sums (a split-K router GEMV), added in ascending part order.
-        // Loads go out Q parts at a time (addresses clamped to the last part, so no branch splits the batch);
-        // one part (plain logits) is a single batch of PER loads.
-        constexpr int Q = PER <= 8 ? 8 : 1;
+        // partial sums are added in ascending part order; one part (plain logits) is a single batch of PER loads
         float v[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) v[i] = 0.f;
         if (nparts == 1) {
 #pragma unroll
-            for (int i = 0; i < PER; ++i) v[i] = e0 + i < E ? (loaded ? raw[i] : S[e0 + i]) : 0.f;
+            for (int i = 0; i < PER; ++i) v[i] = e0 + i < E ? (loaded ? raw[0][i] : S[e0 + i]) : 0.f;
         }
         for (int p0 = 0; nparts > 1 && p0 < nparts; p0 += Q) {
             float t[Q][PER];
@@ -63,7 +67,7 @@ struct GateRow {
             for (int q = 0; q < Q; ++q) {
                 const long long off = (long long)min(p0 + q, nparts - 1) * pstride;
 #pragma unroll
-                for (int i = 0; i < PER; ++i) t[q][i] = e0 + i < E ? S[off + e0 + i] : 0.f;
+                for (int i = 0; i < PER; ++i) t[q][i] = e0 + i < E ? (loaded && p0 == 0 ? raw[q][i] : S[off + e0 + i]) : 0.f;
             }
 #pragma unroll
             for (int q = 0; q < Q; ++q)
