@@ -55,6 +55,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     __shared__ float s_inv[RT_MAXM];
     __shared__ __align__(16) uint16_t s_xn[RT_MAXM][RT_KC + 8];
     __shared__ __align__(16) float s_r[RT_MAXM][RT_KC];   // this workgroup's k range of r
+    __shared__ __align__(16) float s_w[RT_KC];            // and of the norm weight
     __shared__ v4f s_acc[RT_THREADS / 64][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -100,6 +101,10 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
         ss = wave_reduce_sum(ss);
         if (lane == 0) s_ss[wave][t] = ss;
     }
+    if (tid < nkv) {   // its loads went out at entry, ahead of the rows'
+        *(v4f*)&s_w[tid * 8] = v4f{wv[0], wv[1], wv[2], wv[3]};
+        *(v4f*)&s_w[tid * 8 + 4] = v4f{wv[4], wv[5], wv[6], wv[7]};
+    }
     __syncthreads();
     if (tid < M) {
         float tot = 0.f;
@@ -109,15 +114,7 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     }
     __syncthreads();
 
-    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there. Thread
-    // tid handles vector tid % 128 of rows tid / 128, tid / 128 + 4, ... (the vector its norm weight slice covers
-    // when tid < 128; the others read it from LDS)
-    __shared__ __align__(16) float s_w[RT_KC];
-    if (tid < nkv) {
-        *(v4f*)&s_w[tid * 8] = v4f{wv[0], wv[1], wv[2], wv[3]};
-        *(v4f*)&s_w[tid * 8 + 4] = v4f{wv[4], wv[5], wv[6], wv[7]};
-    }
-    __syncthreads();
+    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there
     for (int i = tid; i < M * nkv; i += RT_THREADS) {
         const int t = i / nkv, v = i - t * nkv;
         const int k = ks * RT_KC + v * 8;
