@@ -52,7 +52,6 @@ __device__ __forceinline__ void load_r8(const RouterArgs& a, int t, int k, float
 
 __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArgs a) {
     __shared__ float s_ss[RT_THREADS / 64][RT_MAXM];
-    __shared__ float s_inv[RT_MAXM];
     __shared__ __align__(16) uint16_t s_xn[RT_MAXM][RT_KC + 8];
     __shared__ __align__(16) float s_r[RT_MAXM][RT_KC];   // this workgroup's k range of r
     __shared__ __align__(16) float s_w[RT_KC];            // and of the norm weight
@@ -106,21 +105,19 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
         *(v4f*)&s_w[tid * 8 + 4] = v4f{wv[4], wv[5], wv[6], wv[7]};
     }
     __syncthreads();
-    if (tid < M) {
-        float tot = 0.f;
-#pragma unroll
-        for (int i = 0; i < RT_THREADS / 64; ++i) tot += s_ss[i][tid];
-        s_inv[tid] = 1.0f / sqrtf(tot / (float)H + a.eps);
-    }
-    __syncthreads();
 
-    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there
+    // ---- xn of this workgroup's k range into LDS; workgroups of row block 0 also write xn and xq there. Each
+    // thread sums its row's eight wave partials itself (same order everywhere), so no further barrier is needed.
     for (int i = tid; i < M * nkv; i += RT_THREADS) {
         const int t = i / nkv, v = i - t * nkv;
         const int k = ks * RT_KC + v * 8;
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < RT_THREADS / 64; ++w) tot += s_ss[w][t];
+        const float inv = 1.0f / sqrtf(tot / (float)H + a.eps);
         float n[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) n[j] = bf16_round(s_r[t][v * 8 + j] * s_inv[t] * s_w[v * 8 + j]);
+        for (int j = 0; j < 8; ++j) n[j] = bf16_round(s_r[t][v * 8 + j] * inv * s_w[v * 8 + j]);
         uint32_t on[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) on[j] = f32_to_bf16_bits(n[2 * j]) | (f32_to_bf16_bits(n[2 * j + 1]) << 16);
