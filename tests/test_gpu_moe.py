@@ -200,6 +200,22 @@ def test_decode_experts_small(tiled, M, limit):
     close(y.cpu().numpy(), ref, f"decode small M={M} tiled={tiled} L={limit}")
 
 
+@pytest.mark.parametrize("tiled", [True, False])
+@pytest.mark.parametrize("M", [1, 3])
+def test_decode_experts_wide_hidden(tiled, M):
+    """Hidden 8448: a wave's weight stream has 33 k-chunks, more than the up kernel stages scales for in LDS, and
+    one token no longer fits the one-token path, so both take the member-pass path with per-tile scale loads."""
+    from dsv41_amd import moe, quant
+    E, H, I, k = 12, 8448, 256, 4
+    ws = make_experts(E, H, I, 500 + M)
+    ex = to_ex(*ws, tiled)
+    eid, wt = rand_routing(M, E, k, 600 + M)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 700 + M).to(DEV))
+    y = moe.moe_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, 10.0)
+    ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, *[w.cpu().numpy() for w in ws], I, 10.0)
+    close(y.cpu().numpy(), ref, f"decode hidden 8448 M={M} tiled={tiled}")
+
+
 @pytest.mark.parametrize("M,func,norm", [(1, "softmax", True), (3, "sigmoid", True), (16, "sqrtsoftplus", True), (5, "softmax", False)])
 def test_decode_up_routing_and_tables(M, func, norm):
     """The fused decode entry routes from the logits: its ids / weights equal the standalone gate kernel's (the
