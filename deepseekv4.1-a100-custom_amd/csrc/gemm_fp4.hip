@@ -471,7 +471,9 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n};
     hipStream_t st = (hipStream_t)stream;
     const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
-    const bool h_lds = lds <= 60 * 1024;
+    // staged h: at most 60 KiB, which also bounds the per-thread load registers (DS_HV vectors, DS_HS bytes)
+    const bool h_lds = lds <= 60 * 1024 && (long long)(zero_row + 1) * (K / 16) <= DS_HV * DS_WAVES * 64 &&
+                       (long long)(zero_row + 1) * (K / 32) <= DS_HS * DS_WAVES * 64;
     const dim3 grid(N / 16), block(DS_WAVES * 64);
     // weight scales through LDS when every wave holds at most DS_SCG groups of <= 16 k-chunks and the scale rows are
     // 16-byte aligned for the wide loads
