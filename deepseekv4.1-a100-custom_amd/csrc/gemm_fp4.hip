@@ -170,6 +170,7 @@ struct DownSumArgs {
 #define DS_HS 4          // H_LDS: h E8M0 bytes per thread (rows * K / 32 <= 2048 whenever the rows fit 60 KiB)
 #define DS_SCG 2         // SCL: groups per wave whose weight scales are staged in LDS
 #define DS_SCW 2048      // SCL: LDS bytes per wave for them (<= 32 k-chunks of 64 bytes)
+                         // SCL == 2: the current group's weight scales (<= 1 KiB) + its 16 h scale rows (64 bytes each)
 
 // One workgroup per 16-row block of the output; its 8 waves split the selected experts (group slots g = wave,
 // wave + 8, ...), each accumulating sum over its experts and k of W2[e] . h in one MFMA accumulator whose
@@ -182,6 +183,10 @@ struct DownSumArgs {
 // soon as the tables are in. SCL (at most DS_SCG groups per wave, <= 32 k-chunks): each wave's weight scales are
 // fetched with a few wide loads ahead of its tiles and read from LDS per k-step, instead of a one-byte load per
 // lane with every tile (those cost the load unit as much time as the tiles).
+// SCL == 2 (h rows from global, <= 16 k-chunks): a group's weight scales and the h scales of its 16 rows are fetched
+// with one wide load each when the producer enters the group, into registers of the tile slot that starts it; the
+// consumer copies them into the wave's LDS region when it reaches that tile and reads its bytes there per k-step.
+// Three loads per tile remain (weights, two h vectors) instead of five.
 template <int TILED, int PF, int NKC, int H_LDS, int SCL>
 __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_kernel(const DownSumArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -254,22 +259,49 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     // !H_LDS: the lane's h row (global) of the producer's current group, set at group boundaries
     const uint8_t* phb = a.hc;
     const uint8_t* phs = a.hs;
+    // SCL == 2: lane (col, kb) fetches 16 bytes of its row's h scales at min(16 kb, Ks - 16) (the row's Ks bytes,
+    // Ks >= 16, overlaps repeat the same bytes); the descriptor ends at the zero row's last scale
+    constexpr bool GS = SCL == 2;
+    const int gsb = min(kb * 16, Ks - 16);
+    uint32_t pso = 0;
     auto prod_rows = [&]() {
         const long long q = pm ? s_pair[wave + DS_WAVES * (int)__builtin_ctzll(pm)][col] : a.zero_row;
         phb = a.hc + q * a.ldh + kb * 16;
         phs = a.hs + q * a.ldhs + kb;
+        if (GS) pso = (uint32_t)(q * a.ldhs + gsb);
     };
+    // SCL == 2: the group scale registers of each tile slot (written only by the tile that starts a group)
+    v4i GA[GS ? PF : 1], GB[GS ? PF : 1];
     auto load = [&](int slot, int) {
         // one expert's tiles through a buffer descriptor: scalar base, 32-bit lane offset, scalar k offset
         // once the wave's groups are exhausted (H_LDS issues its first PF tiles unconditionally) the descriptor is
         // empty: the load returns zeros without touching memory, and the slot is never consumed
         const uint32_t wb = pm ? (uint32_t)a.stride_we : 0u, sbn = pm ? (uint32_t)a.stride_se : 0u;
+        if (GS && pkc == 0) {
+            // the producer enters a group: its weight scales (16 rows x nk k-chunks) and its rows' h scales, older
+            // than the tile loads of this slot, so the wait for the slot covers them
+            const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + pe * a.stride_se, sbn);
+            if (TILED) {   // contiguous: 64 nb nk .. + 64 nk
+                GA[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                    sr, lane * 16 < nk * 64 ? (uint32_t)(nb * nk * 64 + lane * 16) : 0xFFFFFFF0u, 0, 0));
+            } else {       // one dword (4 k-blocks) per (row, k-chunk)
+                int g[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    g[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, kc < nk ? (uint32_t)((nb * 16 + r) * Ks + kc * 4) : 0xFFFFFFF0u, 0, 0);
+                }
+                GA[slot] = v4i{g[0], g[1], g[2], g[3]};
+            }
+            GB[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                buffer_rsrc(a.hs, (uint32_t)((long long)a.zero_row * a.ldhs + Ks)), pso, 0, 0));
+        }
         A[slot] = buffer_load_tile(buffer_rsrc(a.W + pe * a.stride_we, wb), w0, (uint32_t)(pkc * ws));
         if (!SCL) SA[slot] = buffer_load_byte(buffer_rsrc(a.S + pe * a.stride_se, sbn), s0, (uint32_t)(pkc * ss));
         if (!H_LDS) {
             B0[slot] = *(const v4i*)phb;
             B1[slot] = *(const v4i*)(phb + 64);
-            SB[slot] = *phs;
+            if (!GS) SB[slot] = *phs;
             phb += 128;
             phs += 4;
         }
@@ -292,7 +324,26 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     };
     // SCL: the wave's staged scales in consume order (group j of the wave at 64 nk j, k-chunk kc at 64 kc within it)
     const uint8_t* wscl = s_sc + (SCL ? wave * DS_SCW : 0) + col * 4 + kb;
+    // SCL == 2: weight scale of (col, kb) at k-chunk kc: 64 kc + 4 col + kb; h scale: 1024 + 64 col + 4 kc + kb
+    const uint8_t* gsw = s_sc + (GS ? wave * DS_SCW : 0);
     auto use = [&](int slot) {
+        if (GS && ckc == 0) {
+            // the consumer enters a group (the previous group's reads were issued before, and one wave's LDS
+            // operations complete in order)
+            uint8_t* w = s_sc + wave * DS_SCW;
+            if (TILED) {
+                if (lane * 16 < nk * 64) *(v4i*)(w + lane * 16) = GA[slot];
+            } else {
+                const int g[4] = {GA[slot].x, GA[slot].y, GA[slot].z, GA[slot].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    if (kc < nk) *(int*)(w + kc * 64 + r * 4) = g[i];
+                }
+            }
+            int* hw = (int*)(w + 1024 + col * 64 + gsb);   // 4-byte aligned: Ks % 4 == 0
+            hw[0] = GB[slot].x; hw[1] = GB[slot].y; hw[2] = GB[slot].z; hw[3] = GB[slot].w;
+        }
         if (H_LDS) {
             const v4i b0 = *(const v4i*)hb;
             const v4i b1 = *(const v4i*)(hb + 64);
@@ -303,7 +354,9 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             if (SCL) wscl += 64;
             acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, sa, sb);
         } else {
-            acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
+            const int sa = GS ? (int)gsw[ckc * 64 + col * 4 + kb] : SA[slot];
+            const int sb = GS ? (int)gsw[1024 + col * 64 + ckc * 4 + kb] : SB[slot];
+            acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, sa, sb);
         }
         if (++ckc == nk) {
             ckc = 0;
@@ -313,8 +366,8 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     };
     // SCL: the scales of the wave's first DS_SCG groups (16 rows x nk k-chunks each), older than every tile. A missing
     // group reads through an empty descriptor (zeros) and is never consumed.
-    v4i SC[SCL ? (TILED ? DS_SCG : 4 * DS_SCG) : 1];
-    if (SCL) {
+    v4i SC[SCL == 1 ? (TILED ? DS_SCG : 4 * DS_SCG) : 1];
+    if (SCL == 1) {
         unsigned long long m = vmask;
 #pragma unroll
         for (int j = 0; j < DS_SCG; ++j) {
@@ -361,7 +414,7 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             if (i * DS_WAVES * 64 + wave * 64 < n_hs && idx < n_hs) hsw[idx] = (uint8_t)HS[i];
         }
     }
-    if (SCL) {
+    if (SCL == 1) {
         uint8_t* w = s_sc + wave * DS_SCW;
 #pragma unroll
         for (int j = 0; j < DS_SCG; ++j) {
@@ -479,9 +532,14 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     // 16-byte aligned for the wide loads
     const bool scl = h_lds && (n_slots + DS_WAVES - 1) / DS_WAVES <= DS_SCG && K / 128 <= 16 && (((uintptr_t)S) & 15) == 0 &&
                      (stride_se & 15) == 0;
+    // h rows from global: per-group scale loads when a group's scales fit the wave's LDS region (<= 16 k-chunks), the
+    // h scale rows hold >= 16 bytes and every wide load is aligned (16 bytes for the weight scales, 4 for h's)
+    const bool gs = !h_lds && K / 128 <= 16 && K >= 512 && (((uintptr_t)S) & 15) == 0 && (stride_se & 15) == 0 &&
+                    (ldhs & 3) == 0 && (((uintptr_t)hs) & 3) == 0;
 #define DS_LAUNCH(T, PF, NK, HL, SC) moe_down_sum_kernel<T, PF, NK, HL, SC><<<grid, block, HL ? lds : 0, st>>>(a)
     if (scl) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 1); else DS_LAUNCH(0, 12, 0, 1, 1); }
     else if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 0); else DS_LAUNCH(0, 12, 0, 1, 0); }
+    else if (gs) { if (tiled) DS_LAUNCH(1, 6, 0, 0, 2); else DS_LAUNCH(0, 6, 0, 0, 2); }
     else { if (tiled) DS_LAUNCH(1, 8, 0, 0, 0); else DS_LAUNCH(0, 8, 0, 0, 0); }
 #undef DS_LAUNCH
     return (int)hipGetLastError();

@@ -216,6 +216,39 @@ def test_decode_experts_wide_hidden(tiled, M):
     close(y.cpu().numpy(), ref, f"decode hidden 8448 M={M} tiled={tiled}")
 
 
+@pytest.mark.parametrize("tiled", [True, False])
+@pytest.mark.parametrize("M,I", [(16, 640), (16, 512), (8, 1024), (16, 2048), (16, 2560)])
+def test_decode_down_h_rows_global(tiled, M, I):
+    """Pair rows too large for LDS (M * 8 + 1 rows of I + I / 32 bytes > 60 KiB): the down projection reads h from
+    global memory. I <= 2048 takes the per-group scale loads (I = 640: 20 scale bytes per row, so the 16-byte h scale
+    loads of a row overlap; I = 512: exactly 16); I = 2560 (20 k-chunks) the per-tile scale bytes. Checked against the
+    oracle's w2 on the kernel's own h (the up projection's FP8 rounding is covered by the tests above), and bit for bit
+    against the per-tile scale path on the same h (forced by a 4-byte-misaligned h scale row stride)."""
+    import copy
+    from dsv41_amd import moe, quant
+    E, H, k = 24, 1024, 8
+    P, Ks = M * k, I // 32
+    w = make_experts(E, H, I, 700 + I + M)
+    ex = to_ex(*w, tiled)
+    eid, wt = rand_routing(M, E, k, 7 * M)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 7 * M).to(DEV))
+    ws = moe.decode_up(xq, ex, 10.0, k, eid=torch.from_numpy(eid).to(DEV), wt=torch.from_numpy(wt).to(DEV))
+    y = moe.decode_down(ws, ex).clone()
+    ge, gs, tok = ws.grp_expert.cpu().numpy(), ws.grp_start.cpu().numpy(), ws.tok_sorted.cpu().numpy()
+    h = _e4m3_values(ws.hc[:P], ws.hs[:P])
+    y2 = O.grouped_gemm(h, w[2].cpu().numpy(), w[3].cpu().numpy(), ge, gs, np.arange(P, dtype=np.int32), int(np.count_nonzero(ge >= 0)))
+    ref = np.zeros((M, H), np.float64)
+    np.add.at(ref, tok[:P], y2)
+    close(y.cpu().numpy(), ref, f"decode down, h rows from global, M={M} I={I} tiled={tiled}")
+    hs_wide = torch.zeros(P + 1, Ks + 1, dtype=torch.uint8, device=DEV)
+    hs_wide[:, :Ks] = ws.hs
+    ws2 = copy.copy(ws)
+    ws2.hs = hs_wide[:, :Ks]
+    y_tile = torch.empty(M, H, dtype=torch.float32, device=DEV)
+    moe.decode_down(ws2, ex, y32=y_tile)
+    assert torch.equal(y, y_tile), f"per-group vs per-tile scale loads differ: max {float((y - y_tile).abs().max())}"
+
+
 @pytest.mark.parametrize("M,func,norm", [(1, "softmax", True), (3, "sigmoid", True), (16, "sqrtsoftplus", True), (5, "softmax", False)])
 def test_decode_up_routing_and_tables(M, func, norm):
     """The fused decode entry routes from the logits: its ids / weights equal the standalone gate kernel's (the
