@@ -519,13 +519,17 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
         stride_se < (long long)N * (K / 32))
         return DSV41_EINVAL;
-    if ((ldh & 15) || (((uintptr_t)hc) & 15)) return DSV41_EINVAL;
+    if ((ldh & 15) || (((uintptr_t)hc) & 15) || ldh < K || ldhs < K / 32) return DSV41_EINVAL;
+    if ((y && ldy < N) || (yb && ldyb < N) || (yb && ys && ldys < N)) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n};
     hipStream_t st = (hipStream_t)stream;
     const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
+    // the h buffer descriptors (staged h, per-group scale loads) take 32-bit sizes and offsets; otherwise h is read
+    // through 64-bit pointers
+    const bool h32 = (long long)zero_row * ldh + K <= 0xFFFFFFFFll && (long long)zero_row * ldhs + K / 32 <= 0xFFFFFFFFll;
     // staged h: at most 60 KiB, which also bounds the per-thread load registers (DS_HV vectors, DS_HS bytes)
-    const bool h_lds = lds <= 60 * 1024 && (long long)(zero_row + 1) * (K / 16) <= DS_HV * DS_WAVES * 64 &&
+    const bool h_lds = h32 && lds <= 60 * 1024 && (long long)(zero_row + 1) * (K / 16) <= DS_HV * DS_WAVES * 64 &&
                        (long long)(zero_row + 1) * (K / 32) <= DS_HS * DS_WAVES * 64;
     const dim3 grid(N / 16), block(DS_WAVES * 64);
     // weight scales through LDS when every wave holds at most DS_SCG groups of <= 16 k-chunks and the scale rows are
@@ -534,7 +538,7 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                      (stride_se & 15) == 0;
     // h rows from global: per-group scale loads when a group's scales fit the wave's LDS region (<= 16 k-chunks), the
     // h scale rows hold >= 16 bytes and every wide load is aligned (16 bytes for the weight scales, 4 for h's)
-    const bool gs = !h_lds && K / 128 <= 16 && K >= 512 && (((uintptr_t)S) & 15) == 0 && (stride_se & 15) == 0 &&
+    const bool gs = !h_lds && h32 && K / 128 <= 16 && K >= 512 && (((uintptr_t)S) & 15) == 0 && (stride_se & 15) == 0 &&
                     (ldhs & 3) == 0 && (((uintptr_t)hs) & 3) == 0;
 #define DS_LAUNCH(T, PF, NK, HL, SC) moe_down_sum_kernel<T, PF, NK, HL, SC><<<grid, block, HL ? lds : 0, st>>>(a)
     if (scl) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 1); else DS_LAUNCH(0, 12, 0, 1, 1); }

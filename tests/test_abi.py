@@ -50,3 +50,10 @@ def test_invalid_arguments_are_rejected_without_launch():
     assert L.dsv41_quant_fp8(ctypes.c_void_p(16), 0, 4, 33, 33, 0, ctypes.c_void_p(16), None, None, None) == -1  # K % 32
     assert L.dsv41_moe_dispatch(ctypes.c_void_p(16), None, 8, 8, 1000, 64, *[ctypes.c_void_p(16)] * 5, None, None) == -1  # E > 512
     assert L.dsv41_dense_gemv_bf16(ctypes.c_void_p(16), 64, 16, 64, ctypes.c_void_p(16), 64, 17, ctypes.c_void_p(16), 16, None, 0, None) == -1
+    # decode down projection: h rows shorter than K (codes or scales), an output row stride below N
+    p = ctypes.c_void_p(16)
+    down = lambda ldh, ldhs, ldy: L.dsv41_moe_down_sum(p, 7168 * 832, p, 7168 * 52, 1, 7168, 1664, p, ldh, p, ldhs, 8, p, p, p, 8, 1,
+                                                      p, ldy, None, 7168, None, 7168, 0, 384, None)
+    assert down(1600, 52, 7168) == -1
+    assert down(1664, 51, 7168) == -1
+    assert down(1664, 52, 7000) == -1
