@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
+    ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
     ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
                                                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
@@ -422,6 +423,12 @@ def main():
         return
     layers = make_layers(torch, dev, N_COPIES, 1000)
     eb = expert_bytes()
+    if args.decode_m:
+        M = args.decode_m
+        t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
+        print(json.dumps({"workload": f"configs[2] decode, M = {M}", "us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
+                          "TBps": round(uniq * eb / t_m / 1e12, 3), "w2_bytes_per_expert": H * (I // 2) + H * (I // 32)}))
+        return
     sel_bytes = TOPK * eb
 
     progress("layers resident")
