@@ -464,6 +464,8 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
         return DSV41_EINVAL;
     if (logits && (nparts < 1 || (nparts > 1 && part_stride < (long long)M * ldl))) return DSV41_EINVAL;
     if (H <= 0 || (H & 255) || I <= 0 || (I & 31) || ldx < H || (ldx & 7) || (((uintptr_t)x) & 15) || (logits && ldl < E)) return DSV41_EINVAL;
+    // every h row holds I codes and I / 32 scale bytes (the epilogue writes columns 0 .. I - 1 of each)
+    if (ldhc < I || ldhs < I / 32) return DSV41_EINVAL;
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
         stride_we < (long long)2 * I * (H / 2) || stride_se < (long long)2 * I * (H / 32)) return DSV41_EINVAL;

@@ -139,10 +139,11 @@ __global__ void __launch_bounds__(256) quant_fp8_vec_kernel(const void* __restri
 
 // ------------------------------------------------------------------------------------------ SwiGLU
 // h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) per 32 columns (fused.py:284-306; model.py:608-613).
-// gu: fp32 [rows, ld_gu] with gate in columns [0, I) and up in [I, 2I). Outputs: FP8 codes [rows, I] and E8M0
+// gu: fp32 or bf16 (gu_bf16) [rows, ld_gu] with gate in columns [0, I) and up in [I, 2I) (fused.swiglu_quant takes
+// both: the routed path's fp32 GEMM output and the shared expert's bf16 linear output). Outputs: FP8 codes [rows, I] and E8M0
 // [rows, I/32] (the down-projection operand), and optionally the bf16 values (fused.swiglu_quant's result,
 // 8-k permuted when `permute`, fused.py:303-305).
-__global__ void __launch_bounds__(256) swiglu_quant_kernel(const float* __restrict__ gu, long long ld_gu, const float* __restrict__ wt,
+__global__ void __launch_bounds__(256) swiglu_quant_kernel(const void* __restrict__ gu, int gu_bf16, long long ld_gu, const float* __restrict__ wt,
                                                            int rows, int inter, float limit, uint8_t* __restrict__ codes,
                                                            uint8_t* __restrict__ scales, uint16_t* __restrict__ hb, int permute) {
     const long long gidx = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 5;
@@ -151,8 +152,9 @@ __global__ void __launch_bounds__(256) swiglu_quant_kernel(const float* __restri
     if (gidx >= (long long)rows * gpr) return;
     const int r = (int)(gidx / gpr);
     const int c = (int)(gidx - (long long)r * gpr) * 32 + lane;
-    float g = gu[(long long)r * ld_gu + c];
-    float u = gu[(long long)r * ld_gu + inter + c];
+    const long long ig = (long long)r * ld_gu + c, iu = ig + inter;
+    float g = gu_bf16 ? bf16_to_f32(((const uint16_t*)gu)[ig]) : ((const float*)gu)[ig];
+    float u = gu_bf16 ? bf16_to_f32(((const uint16_t*)gu)[iu]) : ((const float*)gu)[iu];
     if (limit > 0.f) {
         u = fminf(fmaxf(u, -limit), limit);
         g = fminf(g, limit);
@@ -197,11 +199,11 @@ extern "C" int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, 
     return (int)hipGetLastError();
 }
 
-extern "C" int dsv41_swiglu_quant(const float* gu, long long ld_gu, const float* wt, int rows, int inter, float limit,
+extern "C" int dsv41_swiglu_quant(const void* gu, int gu_bf16, long long ld_gu, const float* wt, int rows, int inter, float limit,
                                   uint8_t* codes, uint8_t* scales, uint16_t* h_bf16, int permute, void* stream) {
     if (!gu || rows < 0 || inter <= 0 || (inter & 31) || ld_gu < 2LL * inter || (!codes && !scales && !h_bf16)) return DSV41_EINVAL;
     const long long groups = (long long)rows * (inter / 32);
     if (groups == 0) return 0;
-    swiglu_quant_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(gu, ld_gu, wt, rows, inter, limit, codes, scales, h_bf16, permute);
+    swiglu_quant_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(gu, gu_bf16, ld_gu, wt, rows, inter, limit, codes, scales, h_bf16, permute);
     return (int)hipGetLastError();
 }

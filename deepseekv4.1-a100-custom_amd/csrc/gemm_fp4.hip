@@ -24,10 +24,13 @@ struct GroupedArgs {
     const uint8_t* W; long long stride_we;   // [E][N][K/2] packed E2M1 (expert stride in bytes)
     const uint8_t* S; long long stride_se;   // [E][N][K/32] E8M0
     int N, K;
-    const uint8_t* xc; long long ldx;        // FP8 codes [rows][K], row stride in bytes
-    const uint8_t* xs; long long ldxs;       // E8M0 [rows][K/32], row stride in bytes
+    const uint8_t* xc; long long ldx;        // FP8 codes [x_rows][K], row stride in bytes
+    const uint8_t* xs; long long ldxs;       // E8M0 [x_rows][K/32], row stride in bytes
+    int x_rows;                              // pair_tok values outside [0, x_rows) contribute zeros
     const int* grp_expert; const int* grp_start; const int* pair_tok;
-    float* out; long long ldo;               // fp32 [rows][ldo]
+    int n_pairs;                             // group ranges are clamped to [0, n_pairs)
+    float* out; long long ldo;               // fp32 [out_rows][ldo]
+    int out_rows;                            // output rows outside [0, out_rows) are not written
     const int* out_row;                      // optional: output row of pair p (default p)
     const float* pair_wt;                    // optional per-pair factor
     int shard_start, shard_n, zero_out, min_tok, max_tok, vec_store;
@@ -51,16 +54,21 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     const int nb = blockIdx.x * 4 + wave;
     const int g = blockIdx.y;
     const bool active = nb * 16 < a.N;
-    const int p0 = a.grp_start[g], p1 = a.grp_start[g + 1];
+    // the group's pair range, clamped to the n_pairs pairs the tables hold
+    const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), p1 = min(max(a.grp_start[g + 1], p0), a.n_pairs);
     const int m = p1 - p0;
     if (m <= 0 || m < a.min_tok || m > a.max_tok) return;       // uniform over the workgroup
     const int col = lane & 15, kb = lane >> 4;
     const int row0 = nb * 16 + 4 * kb;   // this lane's 4 output rows
-    const int e = a.grp_expert[g] - a.shard_start;
-    if (e < 0 || e >= a.shard_n) {       // another GPU's expert (cukern.py:244-246): skip, optionally zero
-        if (active && a.zero_out && a.accum == 0)
+    const int ge = a.grp_expert[g];
+    const int e = ge - a.shard_start;
+    // W holds experts shard_start .. shard_start + shard_n - 1 (all of them when unsharded); a group of another
+    // GPU's expert (cukern.py:244-246) is skipped and, with zero_out, its rows zeroed; padding (-1) is skipped
+    if (ge < 0 || e < 0 || e >= a.shard_n) {
+        if (ge >= 0 && active && a.zero_out && a.accum == 0)
             for (int q = p0 + col; q < p1; q += 16) {
                 const long long orow = a.out_row ? a.out_row[q] : q;
+                if (orow < 0 || orow >= a.out_rows) continue;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) a.out[orow * a.ldo + row0 + i] = 0.f;
             }
@@ -81,8 +89,12 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     for (int base = p0; base < p1; base += PW) {
         const int mp = min(PW, p1 - base);
         const int brow = col < mp ? col : 0;
-        const uint8_t* xg = a.xc + (long long)a.pair_tok[base + brow] * a.ldx + kb * 16;
-        const uint8_t* xsg = a.xs + (long long)a.pair_tok[base + brow] * a.ldxs + kb;
+        // a pair whose token row is outside [0, x_rows) reads row 0 here and stores zeros below (global B path);
+        // the LDS path stages a zero row for it
+        const int tk = a.pair_tok[base + brow];
+        const bool tok_ok = tk >= 0 && tk < a.x_rows;
+        const uint8_t* xg = a.xc + (long long)(tok_ok ? tk : 0) * a.ldx + kb * 16;
+        const uint8_t* xsg = a.xs + (long long)(tok_ok ? tk : 0) * a.ldxs + kb;
         const uint8_t* xl = smem + brow * LS + kb * 16;
         const uint8_t* xsl = lds_s + brow * Ks + kb;
         v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
@@ -117,23 +129,26 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
                 const int vpr = K >> 4;
                 for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
                     const int r = i / vpr, v = i - r * vpr;
-                    const long long src = (long long)a.pair_tok[base + r] * a.ldx + v * 16;
-                    *(v4i*)(smem + r * LS + v * 16) = *(const v4i*)(a.xc + src);
+                    const int t = a.pair_tok[base + r];
+                    *(v4i*)(smem + r * LS + v * 16) =
+                        (t >= 0 && t < a.x_rows) ? *(const v4i*)(a.xc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
                 }
                 for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
                     const int r = i / Ks, v = i - r * Ks;
-                    lds_s[r * Ks + v] = a.xs[(long long)a.pair_tok[base + r] * a.ldxs + v];
+                    const int t = a.pair_tok[base + r];
+                    lds_s[r * Ks + v] = (t >= 0 && t < a.x_rows) ? a.xs[(long long)t * a.ldxs + v] : (uint8_t)127;
                 }
             }
             __syncthreads();
         }
         if (!active) continue;
         pipeline_finish<PF>(nk, load, use);
-        if (col < mp) {
+        const long long orow = a.out_row ? (long long)a.out_row[base + brow] : (long long)(base + brow);
+        if (col < mp && orow >= 0 && orow < a.out_rows) {
             const int q = base + col;
             const float f = a.pair_wt ? a.pair_wt[q] : 1.f;
-            float* o = a.out + (a.out_row ? (long long)a.out_row[q] : (long long)q) * a.ldo + row0;
-            const v4f v = acc * f;
+            float* o = a.out + orow * a.ldo + row0;
+            const v4f v = (B_LDS || tok_ok) ? acc * f : v4f{0.f, 0.f, 0.f, 0.f};
             if (a.accum == 2) {
                 atomicAdd(o + 0, v.x); atomicAdd(o + 1, v.y); atomicAdd(o + 2, v.z); atomicAdd(o + 3, v.w);
             } else if (a.accum == 1) {
@@ -484,16 +499,19 @@ static void launch_grouped(const GroupedArgs& a, int G, size_t lds, hipStream_t 
 }
 
 extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
-                                      int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs,
-                                      const int* grp_expert, const int* grp_start, int G, const int* pair_tok,
-                                      float* out, long long ldo, const int* out_row, const float* pair_wt, int accum, int max_tokens,
-                                      int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream) {
+                                      int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                      const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
+                                      float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
+                                      int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream) {
     if (!W || !S || !xc || !xs || !grp_expert || !grp_start || !pair_tok || !out) return DSV41_EINVAL;
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || G < 0 || ldo < N || ldx < K || ldxs < K / 32 || max_tokens < 1) return DSV41_EINVAL;
-    if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15)) return DSV41_EINVAL;
-    if (G == 0) return 0;
-    GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, grp_expert, grp_start, pair_tok, out, ldo, out_row, pair_wt,
-                  shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0};
+    if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15) || x_rows < 0 || n_pairs < 0 || out_rows < 0 || shard_n < 0)
+        return DSV41_EINVAL;
+    // every expert W holds has N rows of K / 2 weight bytes and K / 32 scale bytes
+    if (stride_we < (long long)N * (K / 2) || stride_se < (long long)N * (K / 32)) return DSV41_EINVAL;
+    if (G == 0 || n_pairs == 0) return 0;
+    GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, x_rows, grp_expert, grp_start, pair_tok, n_pairs, out, ldo, out_rows,
+                  out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0};
     a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
     const int rows = max_tokens < 16 ? max_tokens : 16;
@@ -514,7 +532,9 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                                   float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                                   int shard_start, int shard_n, void* stream) {
     if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb)) return DSV41_EINVAL;
-    if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0) return DSV41_EINVAL;
+    // zero_row is kept in the kernel's 16-bit pair table
+    if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0 || zero_row > 32767)
+        return DSV41_EINVAL;
     // one expert's weights are addressed with 32-bit offsets and hold N rows of K / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
         stride_se < (long long)N * (K / 32))

@@ -331,17 +331,17 @@ __global__ void __launch_bounds__(256) combine_pairs_kernel(const float* __restr
         // each index before its row); summed in slot order as below
         int r[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = j < topk ? inv[t * topk + j] : 0;
+        for (int j = 0; j < 8; ++j) r[j] = j < topk ? inv[t * topk + j] : -1;
         v4f v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = j < topk ? *(const v4f*)(y2 + (long long)r[j] * ldy2 + n) : v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 8; ++j) v[j] = r[j] >= 0 ? *(const v4f*)(y2 + (long long)r[j] * ldy2 + n) : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            if (j < topk) s += v[j];
+            if (r[j] >= 0) s += v[j];
     } else {
         for (int j = 0; j < topk; ++j) {
-            const int r = inv[t * topk + j];
-            s += *(const v4f*)(y2 + (long long)r * ldy2 + n);
+            const int r = inv[t * topk + j];   // -1: a pair the dispatch dropped (expert id outside [0, E))
+            if (r >= 0) s += *(const v4f*)(y2 + (long long)r * ldy2 + n);
         }
     }
     if (y32) *(v4f*)(y32 + (long long)t * ld32 + n) = s;

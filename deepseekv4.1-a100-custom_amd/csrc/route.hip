@@ -130,17 +130,21 @@ __global__ void __launch_bounds__(DISP_THREADS) moe_dispatch_kernel(const int* _
         wt_sorted[pos] = wt ? wt[p] : 1.f;
         inv[p] = pos;
     }
+    if (valid && !real) inv[p] = -1;   // a dropped pair (id outside [0, E)) has no sorted slot
     if (blockIdx.x != 0) return;
-    // groups of <= gmax pairs per expert, then padding (p2p.cu:124-131)
+    // groups of <= gmax pairs per expert, then padding (p2p.cu:124-131). The padding starts at the number of
+    // placed pairs (n when every id is valid, as in the reference), so the last group ends there; the sorted slots
+    // past it (left by dropped pairs) hold token 0 with weight 0.
     for (int ee = tid; ee < E; ee += DISP_THREADS) {
         const int ng = (s_count[ee] + gmax - 1) / gmax;
         for (int g = 0; g < ng; ++g) { grp_expert[s_gbase[ee] + g] = ee; grp_start[s_gbase[ee] + g] = s_start[ee] + g * gmax; }
     }
     const int G = total_groups;
-    for (int g = G + tid; g < n; g += DISP_THREADS) { grp_expert[g] = -1; grp_start[g] = n; }
+    for (int g = G + tid; g < n; g += DISP_THREADS) { grp_expert[g] = -1; grp_start[g] = total_pairs; }
+    for (int q = total_pairs + tid; q < n; q += DISP_THREADS) { tok_sorted[q] = 0; wt_sorted[q] = 0.f; }
     if (tid == 0) {
-        grp_start[G] = n;
-        grp_start[n] = n;
+        grp_start[G] = total_pairs;
+        grp_start[n] = total_pairs;
         if (n_groups) *n_groups = G;
     }
 }

@@ -27,8 +27,8 @@ F = ctypes.c_float
 SIGNATURES = {
     "dsv41_dequant_fp4": [P, P, LL, I, I, P, P],
     "dsv41_quant_fp8": [P, I, LL, I, LL, I, P, P, P, P],
-    "dsv41_swiglu_quant": [P, LL, P, I, I, F, P, P, P, I, P],
-    "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, P, P, I, P, P, LL, P, P, I, I, I, I, I, I, I, P],
+    "dsv41_swiglu_quant": [P, I, LL, P, I, I, F, P, P, P, I, P],
+    "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
     "dsv41_moe_decode_up": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P, P],
     "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P],
     "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],

@@ -38,7 +38,7 @@ def grouped_gemm_codes(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: t
                        grp_start: torch.Tensor, pair_tok: torch.Tensor, out: torch.Tensor, max_tokens: int, tiled: bool,
                        pair_wt: torch.Tensor | None = None, out_row: torch.Tensor | None = None, accum: int = 0,
                        shard_start: int = 0, shard_n: int = 1 << 30, zero_out: bool = False, n_cols: int | None = None,
-                       min_tok: int = 0, max_tok: int = 1 << 30) -> torch.Tensor:
+                       min_tok: int = 0, max_tok: int = 1 << 30, n_pairs: int | None = None) -> torch.Tensor:
     """Core launcher: out[out_row[p], :N] (=, +=, atomic +=) wt[p] * codes(x)[pair_tok[p]] . deq(W[e_g])^T.
     xc/xs: FP8 codes [rows, K] / E8M0 [rows, K/32]; w/s: [E, N, K/2] / [E, N, K/32] (may be a column slice)."""
     dev = _lib.require_cuda(xc, xs, w, s, grp_expert, grp_start, pair_tok, out)
@@ -52,10 +52,14 @@ def grouped_gemm_codes(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: t
     for t in (grp_expert, grp_start, pair_tok):
         assert t.dtype == torch.int32 and t.is_contiguous()
     G = grp_expert.numel()
+    n_pairs = pair_tok.numel() if n_pairs is None else min(int(n_pairs), pair_tok.numel())
+    assert grp_start.numel() >= G + 1 and (pair_wt is None or pair_wt.numel() >= n_pairs)
+    assert out_row is not None or out.shape[0] >= n_pairs
+    # W holds experts shard_start .. shard_start + E - 1 of the sharded id space (all E when unsharded)
     _lib.call("dsv41_fp4_grouped_gemm", _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 1 if tiled else 0, N, K,
-              _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), _lib.ptr(grp_expert), _lib.ptr(grp_start), G, _lib.ptr(pair_tok),
-              _lib.ptr(out), out.stride(0), _lib.ptr(out_row), _lib.ptr(pair_wt), accum, max(1, int(max_tokens)),
-              shard_start, min(shard_n, E), 1 if zero_out else 0, min_tok, max_tok, _lib.stream(dev))
+              _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), xc.shape[0], _lib.ptr(grp_expert), _lib.ptr(grp_start), G,
+              _lib.ptr(pair_tok), n_pairs, _lib.ptr(out), out.stride(0), out.shape[0], _lib.ptr(out_row), _lib.ptr(pair_wt), accum,
+              max(1, int(max_tokens)), shard_start, min(shard_n, E), 1 if zero_out else 0, min_tok, max_tok, _lib.stream(dev))
     return out
 
 
@@ -95,7 +99,7 @@ def fp4_gemm_tc(xp: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: 
     target = out[:, out_col:] if out_col else out
     grouped_gemm_codes(xc, xs, w, s, grp_expert.to(torch.int32).contiguous(), grp_start.to(torch.int32).contiguous(),
                        pair_tok.to(torch.int32).contiguous(), target, max_tokens, FP4_TILED, shard_start=shard_start,
-                       shard_n=shard_n, zero_out=zero_out, n_cols=N)
+                       shard_n=shard_n, zero_out=zero_out, n_cols=N, n_pairs=n_pairs)
     return out
 
 

@@ -281,7 +281,7 @@ def router_logits(x: torch.Tensor, y: torch.Tensor | None, G: torch.Tensor, w: t
 
 class _SharedWs:
     def __init__(self, dev, M, H, I):
-        self.gu = torch.empty(M, 2 * I, dtype=torch.float32, device=dev)
+        self.gu = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)
         self.h = torch.empty(M, I, dtype=torch.bfloat16, device=dev)
         self.ys = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
 
@@ -290,8 +290,9 @@ _SWS: dict = {}
 
 
 def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit: float, ys: torch.Tensor | None = None) -> torch.Tensor:
-    """Shared expert with bf16 weights (model.py:409-412, decode.py:369-371): gu = xq . Ws13^T (fp32),
-    h = swiglu_quant(gu, no weight) (bf16 on the FP8 grid), ys = bf16(h . Ws2^T). Ws13 = [w1; w3] bf16 [2I, H]."""
+    """Shared expert with bf16 weights (model.py:409-412, decode.py:368-370): gu = linear_w(xq, Ws13) is bf16 (one
+    rounding of the fp32-accumulated product), h = swiglu_quant(gu, no weight) (bf16 on the FP8 grid),
+    ys = bf16(h . Ws2^T). Ws13 = [w1; w3] bf16 [2I, H]."""
     dev = _lib.require_cuda(xq, Ws13, Ws2)
     M, H = xq.shape
     I = Ws2.shape[1]
@@ -300,7 +301,7 @@ def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit
     if sw is None:
         sw = _SWS[key] = _SharedWs(dev, M, H, I)
     dense_gemv(Ws13, xq, out=sw.gu)
-    _lib.call("dsv41_swiglu_quant", _lib.ptr(sw.gu), sw.gu.stride(0), None, M, I, float(limit), None, None, _lib.ptr(sw.h), 0, _lib.stream(dev))
+    _lib.call("dsv41_swiglu_quant", _lib.ptr(sw.gu), 1, sw.gu.stride(0), None, M, I, float(limit), None, None, _lib.ptr(sw.h), 0, _lib.stream(dev))
     out = sw.ys if ys is None else ys
     dense_gemv(Ws2, sw.h, out=out)
     return out

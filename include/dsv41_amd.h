@@ -32,10 +32,11 @@ int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, long long l
                     uint8_t* codes, uint8_t* scales, void* fq, void* stream);
 
 /* h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) per 32 (fused.swiglu_quant, fused.py:283-345).
- * gu: fp32 [rows][ld_gu], gate columns [0, inter), up [inter, 2 inter). wt: fp32 [rows] or NULL. Outputs (any
+ * gu: fp32 [rows][ld_gu] (gu_bf16 = 0) or bf16 (gu_bf16 = 1, as fused.py:294 accepts), gate columns [0, inter), up
+ * [inter, 2 inter); ld_gu in elements. wt: fp32 [rows] or NULL. Outputs (any
  * may be NULL, not all): FP8 codes [rows][inter] + E8M0 [rows][inter/32]; bf16 values [rows][inter]
  * (8-k permuted when permute = 1, fused.py:303-305). */
-int dsv41_swiglu_quant(const float* gu, long long ld_gu, const float* wt, int rows, int inter, float limit,
+int dsv41_swiglu_quant(const void* gu, int gu_bf16, long long ld_gu, const float* wt, int rows, int inter, float limit,
                        uint8_t* codes, uint8_t* scales, uint16_t* h_bf16, int permute, void* stream);
 
 /* Grouped FP4 x FP8 GEMM on block-scaled MFMA: for each group g (expert grp_expert[g], pairs
@@ -43,14 +44,18 @@ int dsv41_swiglu_quant(const float* gu, long long ld_gu, const float* wt, int ro
  * accum 0 / 1 / 2) (pair_wt ? pair_wt[p] : 1) * sum_k x[pair_tok[p]][k] * deq(W[e])[n][k].
  * Replaces cukern.fp4_gemm_tc (cukern.py:238-276, fp4_tcw.cu / fp4_tc.cu), cukern.fp4_gemv_pairs
  * (cukern.py:60-77, fp4_gemv.cu) and moe_kernels.grouped_fp4_gemm (moe_kernels.py:127-200).
- * Groups of any size (max_tokens selects the pass width); groups whose expert is outside
- * [shard_start, shard_start + shard_n) are skipped and, with zero_out, their rows zeroed (cukern.py:244-246);
- * groups with fewer than min_tok or more than max_tok pairs are skipped. N % 16 == 0, K % 128 == 0. */
+ * W / S hold the experts shard_start .. shard_start + shard_n - 1 (shard_n = the experts W holds when unsharded),
+ * stride_we >= N * K / 2 and stride_se >= N * K / 32 bytes apart. Groups of any size (max_tokens selects the
+ * pass width); groups whose expert is outside [shard_start, shard_start + shard_n) are skipped and, with
+ * zero_out, their rows zeroed (cukern.py:244-246); padding groups (expert < 0) and groups with fewer than min_tok
+ * or more than max_tok pairs are skipped. Bounds: group ranges are clamped to [0, n_pairs); pairs whose token is
+ * outside [0, x_rows) contribute zeros; output rows outside [0, out_rows) are not written. N % 16 == 0,
+ * K % 128 == 0. */
 int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
-                           int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs,
-                           const int* grp_expert, const int* grp_start, int G, const int* pair_tok,
-                           float* out, long long ldo, const int* out_row, const float* pair_wt, int accum, int max_tokens,
-                           int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
+                           int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                           const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
+                           float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
+                           int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
 
 /* Decode routing + up projection + SwiGLU in one launch (M <= 16 tokens, topk <= 16, E <= 512):
  * routing from fp32 logits [M][ldl] (gate_topk semantics, score_func 0 sqrt(softplus) / 1 sigmoid / 2 softmax;
@@ -101,7 +106,7 @@ int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, lon
 
 /* Combine: y[t] = sum_j y2[inv[t * topk + j]] for j ascending (model.py:589, view(n, k, dim).sum(1)), fp32 into
  * y32 and/or bf16(y + ys) into out (model.py:590-591; ys NULL: no shared expert). inv: moe_dispatch's inverse
- * permutation. N % 4 == 0. */
+ * permutation; an entry of -1 (a dropped pair) contributes nothing. N % 4 == 0. */
 int dsv41_combine_pairs(const float* y2, long long ldy2, const int* inv, int topk, int T, int N, const uint16_t* ys, long long ldys,
                         uint16_t* out, long long ldo, float* y32, long long ld32, void* stream);
 
@@ -136,8 +141,10 @@ int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B
                     int score_func, int norm, int* eid, float* wt, int nparts, long long part_stride, void* stream);
 
 /* Expert bucketing of n = tokens * topk pairs: tok_sorted, wt_sorted, inv, grp_expert (-1 padded), grp_start
- * (n padded), groups of <= gmax pairs per expert; n_groups (optional) receives the group count. Pairs keep
- * ascending order within an expert. cukern.moe_dispatch (cukern.py:323-337, p2p.cu:90-132); E <= 512. */
+ * (padded with the number of placed pairs, n when every id is valid), groups of <= gmax pairs per expert;
+ * n_groups (optional) receives the group count. Pairs keep ascending order within an expert. Ids outside [0, E)
+ * are dropped: their inv entry is -1 and the sorted slots past the placed pairs hold token 0, weight 0.
+ * cukern.moe_dispatch (cukern.py:323-337, p2p.cu:90-132); E <= 512. */
 int dsv41_moe_dispatch(const int* eid, const float* wt, int n, int topk, int E, int gmax, int* tok_sorted, float* wt_sorted,
                        int* inv, int* grp_expert, int* grp_start, int* n_groups, void* stream);
 

@@ -34,7 +34,15 @@ PINS = {
     "gate_topk": "brute force (sort) on random and tied inputs",
     "moe_dispatch": "invariants + brute force on tiny inputs",
     "grouped_gemm": "textbook matmul against dense fp64 on tiny inputs",
-    "moe_layer": "compiled reference CPU library (oracle/_ref, bf16 mode) on I = 256",
+    "moe_layer_routed": "compiled reference CPU library (oracle/_ref, bf16 mode) on I = 256",
+    "moe_layer": "composition check: with the shared expert equal to a routed expert (one-hot off-grid x), "
+                 "bf16(moe_layer_routed(fq8 x) + bf16(the expert's moe_layer_routed row)), the reference's order "
+                 "(model.py:565-591)",
+    "linear_bf16": "torch F.linear on bf16 CPU tensors (the op linear_w runs for bf16 weights, w8.py:102-103)",
+    "shared_expert": "torch F.linear (bf16) for both GEMVs + golden/library-pinned swiglu_quant; structure (w1/w3 "
+                     "halves, no routing weight, limit) against moe_layer_routed with the expert's dequantised weights "
+                     "and a one-hot x (gu exact in bf16)",
+    "gemv_pairs": "wt x grouped_gemm on singleton groups + scalar brute force on a tiny case",
     "residual_rmsnorm_quant": "torch.nn.functional.rms_norm (fp32, CPU) + golden-pinned fake_quant_fp8",
     "int8_quant_blocks": "closed form (|v - q s| <= s / 2, q range, zero block) + compiled reference CPU library (int8 mode) layer output",
     "w4a8_gemv": "brute force on tiny inputs (integer dot by hand) + compiled reference CPU library (int8 mode) layer output",
@@ -307,12 +315,18 @@ def moe_dispatch(eid, wt, topk: int, n_experts: int, gmax: int):
     eid = np.asarray(eid, dtype=np.int64).reshape(-1)
     wt = np.asarray(wt, dtype=F32).reshape(-1)
     n = eid.size
-    order = np.argsort(eid, kind="stable")
-    tok_sorted = (order // topk).astype(np.int32)
-    wt_sorted = wt[order]
-    inv = np.empty(n, np.int32)
-    inv[order] = np.arange(n, dtype=np.int32)
-    counts = np.bincount(eid, minlength=n_experts)
+    # ids outside [0, n_experts) are dropped (the reference indexes its histogram with them, p2p.cu:106: undefined);
+    # a dropped pair has inv = -1, and the slots past the placed pairs hold token 0 / weight 0
+    keep = (eid >= 0) & (eid < n_experts)
+    order = np.argsort(np.where(keep, eid, n_experts), kind="stable")[: int(keep.sum())]
+    placed = order.size
+    tok_sorted = np.zeros(n, np.int32)
+    wt_sorted = np.zeros(n, F32)
+    tok_sorted[:placed] = order // topk
+    wt_sorted[:placed] = wt[order]
+    inv = np.full(n, -1, np.int32)
+    inv[order] = np.arange(placed, dtype=np.int32)
+    counts = np.bincount(eid[keep], minlength=n_experts)
     starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
     ge, gs = [], []
     for e in range(n_experts):
@@ -321,7 +335,7 @@ def moe_dispatch(eid, wt, topk: int, n_experts: int, gmax: int):
             gs.append(starts[e] + t)
     G = len(ge)
     grp_expert = np.full(n, -1, np.int32)
-    grp_start = np.full(n + 1, n, np.int32)
+    grp_start = np.full(n + 1, placed, np.int32)
     grp_expert[:G] = ge
     grp_start[:G] = gs
     return tok_sorted, wt_sorted, inv, grp_expert, grp_start, G
@@ -373,14 +387,20 @@ def deq64(w, s):
     return dense_weights(w, s).astype(np.float64)
 
 
+def linear_bf16(x, W_bits) -> np.ndarray:
+    """F.linear of bf16 x and bf16 W (W given as bf16 bit patterns [N, K]) with a bf16 result: fp32 accumulation,
+    one rounding (what linear_w does for a bf16 weight, w8.py:102-103). Returns fp32 values of the bf16 result."""
+    W = bf16_bits_to_f32(W_bits)
+    return bf16_round((np.asarray(x, F32) @ W.T).astype(F32))
+
+
 def shared_expert(xq, Ws13, Ws2, inter: int, limit: float) -> np.ndarray:
-    """Shared expert with bf16 weights (model.py:409-412, decode.py:369-371): gu = xq . Ws13^T (fp32),
-    h = swiglu_quant(gu, no weight), ys = bf16(h . Ws2^T). Returns fp32 values of the bf16 ys [M, H]."""
-    Ws13 = bf16_bits_to_f32(Ws13)
-    Ws2 = bf16_bits_to_f32(Ws2)
-    gu = (np.asarray(xq, F32) @ Ws13.T).astype(F32)
+    """Shared expert with bf16 weights (model.py:409-412, decode.py:368-370): gu = linear_w(xq, Ws13) is a bf16
+    tensor (F.linear on bf16), h = swiglu_quant(gu, no weight) (bf16 on the FP8 grid), ys = linear_w(h, Ws2),
+    bf16. Ws13 = [w1; w3] and Ws2 as bf16 bit patterns. Returns fp32 values of the bf16 ys [M, H]."""
+    gu = linear_bf16(xq, Ws13)
     h = swiglu_quant(gu, None, inter, limit)
-    return bf16_round((h @ Ws2.T).astype(F32))
+    return linear_bf16(h, Ws2)
 
 
 def moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter: int, limit: float) -> np.ndarray:

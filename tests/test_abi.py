@@ -57,3 +57,44 @@ def test_invalid_arguments_are_rejected_without_launch():
     assert down(1600, 52, 7168) == -1
     assert down(1664, 51, 7168) == -1
     assert down(1664, 52, 7000) == -1
+
+
+def test_bound_checks_reject_oversized_shapes_without_launch():
+    """Host-side bounds of the grouped GEMM (an N or K larger than one expert's bytes), the decode up projection (h rows
+    narrower than I) and the decode down projection (a zero row beyond the kernel's 16-bit pair table): -1, nothing
+    launched (the pointers are never dereferenced)."""
+    import ctypes
+    from dsv41_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    N, K = 3328, 7168
+    we, se = N * K // 2, N * K // 32
+
+    def grouped(n, k, stride_we, stride_se, x_rows=1, n_pairs=8, out_rows=8, shard_n=384):
+        return L.dsv41_fp4_grouped_gemm(p, stride_we, p, stride_se, 1, n, k, p, k, p, k // 32, x_rows, p, p, 8, p, n_pairs, p, n, out_rows,
+                                        None, None, 0, 1, 0, shard_n, 0, 0, 1 << 30, None)
+    assert grouped(2 * N, K, we, se) == -1           # N rows past one expert's weight bytes
+    assert grouped(N, 2 * K, we, 2 * se) == -1       # K past the weight bytes
+    assert grouped(N, K, we, se - 1) == -1           # scales shorter than N K / 32
+    assert grouped(N, K, we, se, x_rows=-1) == -1
+    assert grouped(N, K, we, se, n_pairs=-1) == -1
+    assert grouped(N, K, we, se, out_rows=-1) == -1
+    assert grouped(N, K, we, se, shard_n=-1) == -1
+    assert grouped(N, K, we, se, n_pairs=0) == 0     # nothing to do: returns before any launch
+
+    H, I = 7168, 1664
+
+    def up(ldhc, ldhs):
+        return L.dsv41_moe_decode_up(None, 0, 1, 0, None, 1.0, 1.0, 2, 1, p, p, 1, 8, 384, p, H, p, 2 * I * H // 2, p, 2 * I * H // 32,
+                                     1, H, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p, None)
+    assert up(I - 32, I // 32) == -1
+    assert up(I, I // 32 - 1) == -1
+
+    def down(zero_row):
+        return L.dsv41_moe_down_sum(p, H * (I // 2), p, H * (I // 32), 1, H, I, p, I, p, I // 32, zero_row, p, p, p, 8, 1,
+                                    p, H, None, H, None, H, 0, 384, None)
+    assert down(32768) == -1
+    assert down(-1) == -1
+

@@ -113,6 +113,20 @@ def test_swiglu_quant(limit, weighted, permute):
     assert np.array_equal(vals, got if not permute else O.unpermute_x(got))
 
 
+def test_swiglu_quant_bf16_input():
+    """bf16 gate/up (the shared expert's linear output, fused.py:294): the same values as the fp32 path on the
+    bf16 values, bit for bit."""
+    from dsv41_amd import fused
+    g = torch.Generator().manual_seed(5)
+    gu = (torch.randn(5, 2 * 1664, generator=g) * 4).to(torch.bfloat16)
+    hb = fused.swiglu_quant(gu.to(DEV), None, 1664, 10.0)
+    hf = fused.swiglu_quant(gu.float().to(DEV), None, 1664, 10.0)
+    assert torch.equal(hb, hf)
+    ref = O.swiglu_quant(gu.float().numpy(), None, 1664, 10.0)
+    got = O.bf16_bits_to_f32(u16(hb))
+    assert (got == ref).mean() > 0.995 and O.rel_l2(got, ref) < 2e-3
+
+
 @pytest.mark.parametrize("M,H,weighted", [(1, 7168, False), (4, 7168, True), (3, 256, True)])
 def test_residual_rmsnorm_quant(M, H, weighted):
     """The stack's layer-to-layer step against the oracle: xn within one bf16 ulp (fp32 sum order of the

@@ -519,3 +519,176 @@ def test_prefill_layer_vs_oracle():
     y = moe.prefill_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, 10.0)
     ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, *[w.cpu().numpy() for w in ws], I, 10.0)
     close(y.cpu().numpy(), ref, "prefill layer I=1664")
+
+
+# ------------------------------------------------------------------------------------------ benchmark configs at full shape
+def test_configs0_single_gemv_full_shape():
+    """one FP4 GEMV, W [2048 x 4096] E2M1 (uniform nibbles), E8M0 scale bytes 119..123, x [1 x 4096] N(0,1)
+    bf16 -> fq8, fp32 accumulation -> bf16 output, through the reference's fp4_gemv_pairs surface (one pair), both
+    weight layouts."""
+    from dsv41_amd import hipkern, quant
+    N, K = 2048, 4096
+    g = torch.Generator(device=DEV).manual_seed(2048)
+    w = torch.randint(0, 256, (1, N, K // 2), generator=g, dtype=torch.uint8, device=DEV)
+    s = torch.randint(119, 124, (1, N, K // 32), generator=g, dtype=torch.uint8, device=DEV)
+    x = quant.fake_quant_fp8(rand_x(1, K, 4096).to(DEV))
+    one = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ref = O.gemv_pairs(bf16_vals(x), w.cpu().numpy(), s.cpu().numpy(), [0], [0], [1.0])
+    for tiled in (False, True):
+        wk = quant.tile_fp4(w) if tiled else w
+        sk = quant.tile_fp4_scales(s) if tiled else s
+        out = hipkern.fp4_gemv_pairs(x, wk, sk, one, one, torch.ones(1, device=DEV), 1, tiled=tiled)
+        close(out.cpu().numpy(), ref, f"configs[0] GEMV tiled={tiled}")
+        # the bf16 output: fp32 summation order may move a value across a rounding boundary, so outputs agree
+        # bit for bit except for rare differences of one bf16 ulp plus the fp32 error (which dominates near zero)
+        ob, rb = O.bf16_round(out.cpu().numpy()), O.bf16_round(ref)
+        tol = np.maximum(np.abs(ob), np.abs(rb)) * 2.0 ** -7 + 1e-4 * np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+        assert (ob == rb).mean() > 0.99 and np.all(np.abs(ob - rb) <= tol)
+
+
+def test_configs3_prefill_full_shape(full_layer):
+    """2048 tokens x top-8 over 384 experts with Zipf(1.1) popularity (the benchmark's own routing),
+    hidden 7168, intermediate 1664, tiled weights: every expert touched, the busiest spread over many 128-pair groups
+    (56-step k-loops). Sampled tokens (including tokens of the busiest expert) against the oracle, and against the
+    decode path on the same token."""
+    from bench import zipf_routing
+    from dsv41_amd import moe, quant
+    E, H, I, ws, ex = full_layer
+    T, k = 2048, 8
+    eid, wt = zipf_routing(T, 31)
+    counts = np.bincount(eid.reshape(-1), minlength=E)
+    hot = int(counts.argmax())
+    assert counts[hot] > 1000 and (counts > 0).sum() == E
+    xq = quant.fake_quant_fp8(rand_x(T, H, 3100).to(DEV))
+    ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
+    y = moe.prefill_experts(xq, ed, wd, ex, 10.0).cpu().numpy()
+    hot_toks = np.nonzero((eid == hot).any(1))[0]
+    sample = sorted(set([int(hot_toks[0]), int(hot_toks[len(hot_toks) // 2]), int(hot_toks[-1]), 0, 777, T - 1]))
+    ids = set(eid[sample].reshape(-1).tolist())
+    W13, S13, W2, S2 = host_subset(ws, ids)
+    xv = bf16_vals(xq[sample])
+    ref = O.moe_layer_routed(xv, eid[sample], wt[sample], W13, S13, W2, S2, I, 10.0)
+    for i, t in enumerate(sample):
+        close(y[t], ref[i], f"configs[3] prefill token {t}")
+    # the decode path (M <= 16) on the sampled tokens agrees within the same tolerance
+    yd = moe.moe_experts(xq[sample].contiguous(), ed[sample].contiguous(), wd[sample].contiguous(), ex, 10.0).cpu().numpy()
+    close(y[sample], yd, "configs[3] prefill vs decode on the sampled tokens")
+
+
+def test_configs4_stack_graph_equals_eager():
+    """configs[4] shape (4 independent 384-expert layers here; the benchmark runs 20): per layer the fused router
+    launch (residual + RMSNorm + FP8 quant + split-K logits, 7 partial sums) then the routed experts with the routing
+    done inside the up launch from those partial sums (the M = 1 early path). The captured graph equals eager
+    layer-by-layer on every replay; layer 0's routing equals the oracle gate on the summed parts and its output the
+    oracle layer."""
+    from dsv41_amd import moe
+    E, H, I, L, k = 384, 7168, 1664, 4, 8
+    layers, raw0 = [], None
+    for l in range(L):
+        w = make_experts(E, H, I, 4000 + l)
+        if l == 0:
+            raw0 = w
+        layers.append(to_ex(*w, True))
+    g = torch.Generator(device=DEV).manual_seed(4100)
+    routers = [(torch.randn(E, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16) for _ in range(L)]
+    x0 = rand_x(1, H, 4101).to(DEV)
+    xs = [x0.clone(), torch.empty_like(x0)]
+    xq = torch.empty_like(x0)
+    y = torch.zeros_like(x0)
+    part = torch.empty(H // 1024, 1, E, dtype=torch.float32, device=DEV)
+    eids = torch.empty(L, 1, k, dtype=torch.int32, device=DEV)
+    wts = torch.empty(L, 1, k, dtype=torch.float32, device=DEV)
+    parts0 = torch.empty_like(part)
+    xq0 = torch.empty_like(x0)
+    y0_32 = torch.empty(1, H, device=DEV)
+    outs = torch.empty(L, 1, H, dtype=torch.bfloat16, device=DEV)
+
+    def run():
+        xs[0].copy_(x0)
+        y.zero_()
+        for l in range(L):
+            moe.router_logits(xs[l % 2], y, routers[l], None, 1e-6, part=part, xn=xs[(l + 1) % 2], xq=xq)
+            if l == 0:
+                parts0.copy_(part)
+                xq0.copy_(xq)
+            moe.moe_route_experts(xq, part, None, 1.0, k, 1.0, "softmax", True, layers[l], 10.0, out=y, eid_out=eids[l], wt_out=wts[l],
+                                  y32=y0_32 if l == 0 else None)
+            outs[l].copy_(y)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.synchronize()
+    eager = (outs.clone(), eids.clone(), wts.clone())
+    # layer 0 routing: the up launch's gate over the 7 partial sums equals the oracle gate on the summed parts
+    pp = parts0.cpu().numpy()
+    summed = np.zeros((1, E), np.float32)
+    for p in range(pp.shape[0]):
+        summed = (summed + pp[p]).astype(np.float32)
+    ref_i, ref_w = O.gate_topk(summed, None, 1.0, k, 1.0, "softmax", True)
+    assert np.array_equal(eids[0].cpu().numpy(), ref_i)
+    assert np.allclose(wts[0].cpu().numpy(), ref_w, rtol=4e-6, atol=0)
+    W13, S13, W2, S2 = host_subset(raw0, set(ref_i.reshape(-1).tolist()))
+    ref0 = O.moe_layer_routed(bf16_vals(xq0), ref_i, wts[0].cpu().numpy(), W13, S13, W2, S2, I, 10.0)
+    close(y0_32.cpu().numpy(), ref0, "configs[4] layer 0")   # the spec tolerance is on the fp32 output
+    assert np.array_equal(bf16_vals(outs[0]), O.bf16_round(y0_32.cpu().numpy()))
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=s):
+        run()
+    for i in range(3):
+        outs.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs, eager[0]) and torch.equal(eids, eager[1]) and torch.equal(wts, eager[2]), f"replay {i}"
+        moe.router_logits(x0, None, routers[0], None, 1e-6)   # eager work between replays
+        torch.cuda.synchronize()
+    del layers
+
+
+def test_dispatch_drops_invalid_ids_and_combine_skips_them():
+    """Ids outside [0, E) are dropped by the dispatch: tables equal the oracle's (inv = -1, padding at the placed
+    count), and the combine leaves dropped pairs out of a token's sum."""
+    from dsv41_amd import _lib, hipkern
+    E, k, T = 16, 4, 300
+    rng = np.random.default_rng(5)
+    eid = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    eid[3, 1] = -1
+    eid[10, 0] = E
+    eid[299, 3] = 1 << 20
+    wt = rng.random((T, k)).astype(np.float32)
+    got = hipkern.moe_dispatch(torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), k, E, 64, DEV)
+    ref = O.moe_dispatch(eid, wt, k, E, 64)
+    for a, b in zip(got, ref[:5]):
+        assert np.array_equal(a.cpu().numpy(), b)
+    tok, wts, inv, ge, gs = got
+    H = 64
+    y2 = torch.randn(T * k, H, device=DEV)
+    y = torch.empty(T, H, device=DEV)
+    _lib.call("dsv41_combine_pairs", _lib.ptr(y2), H, _lib.ptr(inv), k, T, H, None, H, None, H, _lib.ptr(y), H, _lib.stream(DEV))
+    invn, y2n = inv.cpu().numpy().reshape(T, k), y2.cpu().numpy()
+    ref_y = np.zeros((T, H), np.float32)
+    for j in range(k):
+        ref_y = (ref_y + np.where(invn[:, j:j + 1] >= 0, y2n[np.maximum(invn[:, j], 0)], 0)).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy(), ref_y)
+
+
+def test_grouped_gemm_bounds():
+    """The generic grouped GEMM's bounds: a pair whose token row is outside [0, x_rows) gives zeros, a group whose
+    expert is outside the shard is skipped (rows untouched without zero_out), ranges past n_pairs are clamped."""
+    from dsv41_amd import hipkern, quant
+    E, N, K = 6, 64, 256
+    w, s, _, _ = make_experts(E, K, N // 2, 13)
+    x = quant.fake_quant_fp8(rand_x(4, K, 14).to(DEV))
+    xc, xs = quant.quant_fp8_e8m0(x)
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=DEV)
+    ge, gs, tok = t([1, 9, 3]), t([0, 2, 3, 100]), t([0, 7, 2, 3, 1])
+    out = torch.full((5, N), 5.0, device=DEV)
+    hipkern.grouped_gemm_codes(xc, xs, w, s, ge, gs, tok, out, 16, False)
+    ref = O.grouped_gemm(bf16_vals(x), w.cpu().numpy(), s.cpu().numpy(), np.array([1, 1, 3]), np.array([0, 2, 3, 5]),
+                         np.array([0, 0, 2, 3, 1]), 3)
+    got = out.cpu().numpy()
+    close(got[0], ref[0], "in-range pair")
+    assert np.all(got[1] == 0.0)          # token 7 of 4 rows: zeros
+    assert np.all(got[2] == 5.0)          # expert 9 of 6: skipped, untouched
+    close(got[3:5], ref[3:5], "range clamped to n_pairs")

@@ -205,3 +205,127 @@ def test_residual_rmsnorm_quant_matches_torch_rms_norm():
     assert np.all(np.abs(xn - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
     assert (xn == ref).mean() > 0.99
     assert np.array_equal(xq, O.fake_quant_fp8(xn))
+
+
+def test_moe_dispatch_drops_invalid_ids():
+    """Ids outside [0, E) are dropped: brute force on a tiny case (the placed pairs in expert order, ascending pair
+    order inside an expert; dropped pairs have inv -1; padding starts at the number of placed pairs)."""
+    E, k = 8, 3
+    eid = np.array([[3, -1, 5], [700, 3, 1], [8, 0, 3]], np.int32)
+    wt = np.arange(9, dtype=np.float32).reshape(3, 3) + 1
+    tok, wts, inv, ge, gs, G = O.moe_dispatch(eid, wt, k, E, 2)
+    flat = eid.reshape(-1)
+    kept = [p for p in range(9) if 0 <= flat[p] < E]
+    order = sorted(kept, key=lambda p: (flat[p], p))
+    assert len(order) == 6
+    assert tok[:6].tolist() == [p // k for p in order] and tok[6:].tolist() == [0, 0, 0]
+    assert wts[:6].tolist() == [float(wt.reshape(-1)[p]) for p in order] and wts[6:].tolist() == [0.0, 0.0, 0.0]
+    assert [inv[p] for p in range(9)] == [order.index(p) if p in order else -1 for p in range(9)]
+    # experts 0, 1, 3 (3 pairs -> groups of 2 + 1), 5
+    assert G == 5 and ge[:5].tolist() == [0, 1, 3, 3, 5] and gs[:5].tolist() == [0, 1, 2, 4, 5]
+    assert np.all(ge[5:] == -1) and np.all(gs[5:] == 6)
+
+
+def test_linear_bf16_matches_torch_linear():
+    """linear_bf16 against torch's F.linear on bf16 CPU tensors (the op linear_w runs for a bf16 weight,
+    w8.py:102-103): one bf16 rounding of an fp32-accumulated product. fp32 summation order may move a value across a
+    rounding boundary, so almost all outputs are bit-equal and none is more than one bf16 ulp away; without the
+    rounding step no output would be bf16."""
+    import torch
+    g = torch.Generator().manual_seed(21)
+    x = O.fake_quant_fp8(torch.randn(3, 1024, generator=g).to(torch.bfloat16).float().numpy())
+    W = (torch.randn(256, 1024, generator=g) / 32).to(torch.bfloat16)
+    got = O.linear_bf16(x, W.view(torch.int16).numpy().view(np.uint16))
+    ref = torch.nn.functional.linear(torch.from_numpy(x).to(torch.bfloat16), W).float().numpy()
+    assert np.array_equal(got, O.bf16_round(got))
+    assert (got == ref).mean() > 0.98
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+
+
+def _one_hot_x(dim, k0, v):
+    x = np.zeros((1, dim), np.float32)
+    x[0, k0] = v
+    return x
+
+
+def test_shared_expert_structure_against_routed_expert():
+    """With the shared expert's weights equal to the dequantised FP4 weights of one routed expert (bf16-exact) and a
+    one-hot activation (every gu value is one product of <= 6 significant bits, so the bf16 rounding of gu is exact),
+    shared_expert must equal the library-pinned moe_layer_routed of that expert with weight 1, rounded to bf16: this
+    pins the w1 / w3 halves, the SwiGLU limit, the absent routing weight and the final bf16 rounding."""
+    rng = np.random.default_rng(31)
+    E, inter, dim = 3, 128, 256
+    w13 = rng.integers(0, 256, (E, 2 * inter, dim // 2), dtype=np.uint8)
+    s13 = rng.integers(124, 130, (E, 2 * inter, dim // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, (E, dim, inter // 2), dtype=np.uint8)
+    s2 = rng.integers(118, 124, (E, dim, inter // 32), dtype=np.uint8)
+    e = 1
+    Ws13 = O.dequant_fp4(w13[e], s13[e])
+    Ws2 = O.dequant_fp4(w2[e], s2[e])
+    for limit, (k0, v) in [(10.0, (37, 2.5)), (0.0, (200, -1.75)), (10.0, (5, 6.0))]:
+        xq = O.fake_quant_fp8(_one_hot_x(dim, k0, v))
+        ys = O.shared_expert(xq, Ws13, Ws2, inter, limit)
+        routed = O.moe_layer_routed(xq, np.array([[e]]), np.array([[1.0]], np.float32), w13, s13, w2, s2, inter, limit)
+        assert np.abs(routed).max() > 0
+        assert np.array_equal(ys, O.bf16_round(routed))
+    # swapping the halves changes the result (the check above is sensitive to it)
+    xq = O.fake_quant_fp8(_one_hot_x(dim, 37, 2.5))
+    swapped = np.concatenate([Ws13[inter:], Ws13[:inter]])
+    assert not np.array_equal(O.shared_expert(xq, swapped, Ws2, inter, 10.0), O.shared_expert(xq, Ws13, Ws2, inter, 10.0))
+
+
+def test_moe_layer_composition():
+    """moe_layer = bf16(routed sum + shared), with x FP8-fake-quantised first (model.py:565-591). With the shared
+    expert equal to routed expert e' and an off-grid one-hot x (fq8 moves it), it must equal
+    bf16(moe_layer_routed(fq8 x) + bf16(moe_layer_routed row of e' with weight 1))."""
+    rng = np.random.default_rng(33)
+    E, inter, dim = 6, 128, 256
+    w13 = rng.integers(0, 256, (E, 2 * inter, dim // 2), dtype=np.uint8)
+    s13 = rng.integers(124, 130, (E, 2 * inter, dim // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, (E, dim, inter // 2), dtype=np.uint8)
+    s2 = rng.integers(118, 124, (E, dim, inter // 32), dtype=np.uint8)
+    x = _one_hot_x(dim, 77, 3.3)
+    xq = O.fake_quant_fp8(x)
+    assert not np.array_equal(xq, x)
+    eid = np.array([[0, 2, 4]])
+    wt = np.array([[0.5, 0.3, 0.2]], np.float32)
+    es = 5
+    got = O.moe_layer(x, eid, wt, w13, s13, w2, s2, O.dequant_fp4(w13[es], s13[es]), O.dequant_fp4(w2[es], s2[es]), inter, 10.0)
+    routed = O.moe_layer_routed(xq, eid, wt, w13, s13, w2, s2, inter, 10.0)
+    shared = O.bf16_round(O.moe_layer_routed(xq, np.array([[es]]), np.array([[1.0]], np.float32), w13, s13, w2, s2, inter, 10.0))
+    assert np.array_equal(got, O.bf16_round(routed + shared))
+
+
+def test_gemv_pairs_pins():
+    """gemv_pairs = wt x grouped_gemm on singleton groups (the textbook-pinned function), and a scalar brute-force
+    sum on a tiny case (cukern.py:60-77: out[p] = wt[p] * x[row_in[p]] . deq(W[expert[p]]))."""
+    rng = np.random.default_rng(41)
+    E, N, K = 4, 32, 128
+    w = rng.integers(0, 256, (E, N, K // 2), dtype=np.uint8)
+    s = rng.integers(120, 130, (E, N, K // 32), dtype=np.uint8)
+    x = O.fake_quant_fp8(rng.standard_normal((3, K)).astype(np.float32))
+    row_in = np.array([2, 0, 2, 1], np.int32)
+    expert = np.array([3, 3, 0, 1], np.int32)
+    wt = np.array([0.5, -1.25, 2.0, 1.0], np.float32)
+    got = O.gemv_pairs(x, w, s, row_in, expert, wt)
+    single = O.grouped_gemm(x, w, s, expert, np.arange(5, dtype=np.int32), row_in, 4)
+    assert np.allclose(got, wt[:, None] * single, rtol=1e-6, atol=1e-6)
+    for p in range(4):
+        for n in (0, 13, 31):
+            acc = 0.0
+            for kk in range(K):
+                code = (int(w[expert[p], n, kk // 2]) >> (4 * (kk % 2))) & 15
+                acc += float(x[row_in[p], kk]) * float(O.FP4_TABLE[code]) * 2.0 ** (int(s[expert[p], n, kk // 32]) - 127)
+            assert abs(got[p, n] - wt[p] * acc) <= 1e-5 * max(1.0, abs(wt[p] * acc))
+
+
+def test_every_oracle_function_has_a_pin():
+    """Every public function of the oracle that computes a result is listed in PINS (helpers excepted)."""
+    import inspect
+    helpers = {"f32_bits", "bits_f32", "f32_to_bf16_bits", "bf16_bits_to_f32", "bf16_round", "e4m3_encode", "e4m3_decode", "unpack_fp4",
+               "dequant_fp4_f32", "dequant_fp4_values", "untile_fp4", "untile_fp4_scales", "quant_fp8_e8m0", "pow2_scale", "unpermute_x",
+               "sigmoid_f32", "dense_weights", "expert_pair", "deq64", "rel_l2", "max_abs_over_rms"}
+    fns = {n for n, f in inspect.getmembers(O, inspect.isfunction) if f.__module__ == O.__name__ and not n.startswith("_")}
+    missing = fns - helpers - set(O.PINS)
+    assert not missing, f"oracle functions without a pin: {sorted(missing)}"
+    assert set(O.PINS) <= fns, f"PINS names functions the oracle lacks: {sorted(set(O.PINS) - fns)}"
