@@ -15,6 +15,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 #define DSV41_EINVAL (-1)
+#define DSV41_ENOSPACE (-2)   // the no-allocation entry point's scratch array is too small for the call
 
 #define WAVE 64
 

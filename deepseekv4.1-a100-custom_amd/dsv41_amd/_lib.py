@@ -39,6 +39,8 @@ SIGNATURES = {
     "dsv41_gate_topk": [P, LL, P, I, I, F, I, F, I, I, P, P, I, LL, P],
     "dsv41_router_logits": [P, LL, P, LL, P, F, P, LL, I, I, I, P, P, LL, P, LL, P],
     "dsv41_moe_dispatch": [P, P, I, I, I, I, P, P, P, P, P, P, P],
+    "dsv41_moe_experts_noalloc": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, P, LL, P, LL, I, I, I, F, P, P, P, LL, P, LL,
+                                  P, LL, P],
     "dsv41_selftest_mfma_scale": [P, P, P, P, P, I, I, P],
     "dsv41_selftest_mfma_bf16": [P, P, P, P],
 }
@@ -63,6 +65,8 @@ def lib() -> ctypes.CDLL:
 
 def check(err: int, what: str) -> None:
     if err != 0:
+        if err == -2:
+            raise RuntimeError(f"{what}: the call needs more than the library's scratch array (status -2)")
         if err < 0:
             raise RuntimeError(f"{what}: invalid arguments (status {err})")
         raise RuntimeError(f"{what} failed with HIP error {err}")

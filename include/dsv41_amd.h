@@ -2,7 +2,8 @@
  *
  * Every entry point takes raw device pointers, sizes, and the HIP stream to launch on (hipStream_t passed as
  * void*), launches its kernels on that stream and returns immediately (stream-ordered, capturable in a
- * hipGraph). Return value: 0 ok, -1 invalid arguments (nothing launched), > 0 the hipError_t of the launch.
+ * hipGraph). Return value: 0 ok, -1 invalid arguments (nothing launched), -2 (dsv41_moe_experts_noalloc only) the
+ * call needs more than the library's scratch array (nothing launched), > 0 the hipError_t of the launch.
  * No entry point allocates device memory; callers own every buffer.
  *
  * Formats (reference dsv41/quant.py:6-110):
@@ -147,6 +148,21 @@ int dsv41_gate_topk(const float* scores, long long lds, const float* bias, int B
  * cukern.moe_dispatch (cukern.py:323-337, p2p.cu:90-132); E <= 512. */
 int dsv41_moe_dispatch(const int* eid, const float* wt, int n, int topk, int E, int gmax, int* tok_sorted, float* wt_sorted,
                        int* inv, int* grp_expert, int* grp_start, int* n_groups, void* stream);
+
+/* Decode routed experts without allocating (no counterpart in the reference): the same computation and the same
+ * results as dsv41_moe_decode_up followed by dsv41_moe_down_sum (arguments as there; the W13 / W2 expert strides are
+ * stride_w13 / stride_w2 and their scales' stride_s13 / stride_s2), for callers that cannot allocate device memory
+ * (code under graph capture that must not call hipMalloc, serving loops, harnesses that forbid allocation). The h
+ * rows and bucketing tables live in a 2 MiB device array of the library, one per GPU, held until the process
+ * ends; nothing is allocated or freed. Returns -2 when a call needs more than that array: (M topk + 1) (I + I / 32)
+ * bytes plus the tables, e.g. M = 16, topk = 8, I = 1664 needs 0.22 MiB. Calls on one GPU share the array: calls
+ * that overlap in time on that GPU (other streams, other host threads) race. I % 128 == 0. */
+int dsv41_moe_experts_noalloc(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                              float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E,
+                              const uint16_t* x, long long ldx, const uint8_t* W13, long long stride_w13, const uint8_t* S13,
+                              long long stride_s13, const uint8_t* W2, long long stride_w2, const uint8_t* S2, long long stride_s2,
+                              int tiled, int H, int I, float limit, int* eid_out, float* wt_out, float* y, long long ldy,
+                              const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb, void* stream);
 
 /* Diagnostics (no reference counterpart): one wave runs one matrix instruction on caller-given operands so a
  * test can check the lane layouts the kernels rely on. a, b: [64][8] dwords; sa, sb: [64]; c: [64][4] fp32. */

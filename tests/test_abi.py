@@ -98,3 +98,24 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert down(32768) == -1
     assert down(-1) == -1
 
+
+def test_noalloc_rejects_calls_beyond_its_scratch():
+    """dsv41_moe_experts_noalloc returns -2 (nothing launched, no GPU touched) for a call whose h rows exceed its 2 MiB
+    array, and -1 for invalid arguments."""
+    import ctypes
+    from dsv41_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    H = 7168
+
+    def call(M, topk, I, stride_w2=None):
+        sw2 = H * (I // 2) if stride_w2 is None else stride_w2
+        return L.dsv41_moe_experts_noalloc(None, 0, 1, 0, None, 1.0, 1.0, 0, 0, p, p, M, topk, 512, p, H, p, 2 * I * H // 2, p,
+                                           2 * I * H // 32, p, sw2, p, H * (I // 32), 1, H, I, ctypes.c_float(10.0), None, None, p, H,
+                                           None, H, None, H, None)
+    assert call(16, 16, 8192) == -2            # 257 rows of 8448 bytes > 2 MiB
+    assert call(16, 8, 1664, stride_w2=100) == -1
+    assert call(17, 8, 1664) == -1
+    assert call(16, 8, 1600) == -1             # I % 128
