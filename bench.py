@@ -105,7 +105,10 @@ def routing_stream(torch, dev, steps, M, seed):
     return torch.randn(steps, M, E, generator=g, device=dev)
 
 
-def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared=None, seed=7):
+def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode="fused", seed=7):
+    """One decode layer per step over the rotating layer copies; shared: list of (Ws13, Ws2) bf16 shared-expert copies,
+    rotated with the layers, computed inside the two decode launches ("fused") or as its own launches first
+    ("separate"). Returns (seconds per step, mean unique experts per step)."""
     from dsv41_amd import moe, quant
     logits = routing_stream(torch, dev, steps, M, seed)
     gx = torch.Generator(device=dev).manual_seed(seed + 1)
@@ -118,8 +121,15 @@ def bench_decode(torch, dev, layers, steps, warmup, M, with_shared=False, shared
 
     def step(i):
         ex = layers[i % len(layers)]
-        y_s = moe.shared_expert(xq, shared[0], shared[1], LIMIT, ys=ys) if with_shared else None
-        moe.moe_route_experts(xq, logits[i], None, 1.0, TOPK, 1.0, "softmax", True, ex, LIMIT, ys=y_s, out=out, eid_out=eid[i], wt_out=wt[i])
+        route = (xq, logits[i], None, 1.0, TOPK, 1.0, "softmax", True, ex, LIMIT)
+        if shared is None:
+            moe.moe_route_experts(*route, out=out, eid_out=eid[i], wt_out=wt[i])
+        elif shared_mode == "fused":
+            moe.moe_route_experts(*route, out=out, eid_out=eid[i], wt_out=wt[i], shared=shared[i % len(shared)], ys_out=ys)
+        else:
+            sw = shared[i % len(shared)]
+            y_s = moe.shared_expert(xq, sw.w13, sw.w2, LIMIT, ys=ys, tiled=sw.tiled)
+            moe.moe_route_experts(*route, ys=y_s, out=out, eid_out=eid[i], wt_out=wt[i])
 
     t, g = graph_time(torch, step, steps, warmup)
     # unique experts per step (selected-expert bytes: each unique expert is read once)
@@ -447,11 +457,24 @@ def main():
     extra["down_sum_us_est"] = round((t_routed - t_up) * 1e6, 2)
     progress(f"up kernel alone {t_up * 1e6:.2f} us")
     if not args.quick:
+        # the bf16 shared expert, one copy per layer copy (4 x 71.6 MB: with the routed bytes between two uses of a copy,
+        # more than the 256 MB Infinity Cache holds)
+        from dsv41_amd import moe
         g = torch.Generator(device=dev).manual_seed(5)
-        Ws13 = (torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16)
-        Ws2 = (torch.randn(H, I, generator=g, device=dev) / I ** 0.5).to(torch.bfloat16)
-        t_layer, _ = bench_decode(torch, dev, layers, K, W, 1, with_shared=True, shared=(Ws13, Ws2))
+        shared = [moe.SharedExpert.prepare((torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16),
+                                           (torch.randn(H, I, generator=g, device=dev) / I ** 0.5).to(torch.bfloat16), tiled=True)
+                  for _ in range(N_COPIES)]
+        t_layer, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared, shared_mode="fused")
+        t_sep, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared, shared_mode="separate")
+        sh_bytes = 2 * I * H * 2 + H * I * 2
         extra["layer_us_with_shared_expert"] = round(t_layer * 1e6, 2)
+        extra["shared_expert"] = {"bytes": sh_bytes, "us_added_fused": round((t_layer - t_routed) * 1e6, 2),
+                                  "layer_us_separate_launches": round(t_sep * 1e6, 2), "us_added_separate": round((t_sep - t_routed) * 1e6, 2),
+                                  "layer_TBps_fused": round((sel_bytes + sh_bytes) / t_layer / 1e12, 3),
+                                  "note": "fused: its gate/up row blocks are extra workgroups of the up launch and its down projection "
+                                          "rides in the down launch; separate: three launches (gate/up GEMV, SwiGLU, down GEMV) before "
+                                          "the routed experts; 4 rotating copies"}
+        del shared
         progress("layer with shared expert")
         for M in (4, 8, 16):
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)

@@ -15,6 +15,8 @@
 #include "common.h"
 #include "gate.h"
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
 #define UP_WAVES 8
 #define UP_MAXM 16
 #define UP_MAXK 16
@@ -35,9 +37,55 @@ struct DecodeUpArgs {
     uint8_t* hc; long long ldhc; uint8_t* hs; long long ldhs;   // h codes [P + 1][I], E8M0 [P + 1][I / 32]
     int* eid_out; float* wt_out;                                 // routing [M][topk]
     int* grp_expert; int* grp_start; int* tok_sorted; float* wt_sorted;   // tables, P = M * topk slots
+    // SH: the bf16 shared expert's gate/up GEMV rides in the same launch: grid rows 0 .. sh_y - 1 are its 16-row
+    // blocks of Ws13 (2 I rows, bf16 [2I][ldws]), each over the full K; gus = bf16(x . Ws13^T) [M][ldgus]
+    const uint16_t* Ws13; long long ldws; uint16_t* gus; long long ldgus; int sh_y;
+    int sh_tiled;   // Ws13 in 16 x 32 tiles of 1 KiB ([2I/16][H/32][16][32], ldws = H) instead of row-major
 };
 
-template <int TILED, int PF, int PER, int EARLY, int SCL>
+// One 16-row block of the shared expert's [w1; w3] (bf16) over the full K for M tokens: the 8 waves split K into
+// contiguous 32-k chunk ranges, stream 16 x 64-byte row pieces per bf16 MFMA (1 KiB per wave-load) with the token
+// rows as the B operand, and sum through LDS in wave order; gate/up are stored rounded to bf16 (the shared expert's
+// F.linear output is a bf16 tensor, decode.py:368, w8.py:102-103). These workgroups need no routing, so their
+// weight streams start at kernel entry, while the routed workgroups still run the gate.
+template <int PF>
+__device__ __forceinline__ void shared_up_unit(const DecodeUpArgs& a, v4f (*s_red)[64]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.y * gridDim.x + blockIdx.x;            // 16-row block of Ws13
+    const int nc = a.H >> 5;                                        // 32-k chunks
+    const int c0 = nc * wave / UP_WAVES, c1 = nc * (wave + 1) / UP_WAVES;
+    const int col = lane & 15, kb = lane >> 4;
+    // a lane's 16 bytes of chunk c: row col, k [32 c + 8 kb, +8); tiled: at 1024 c + 64 col + 16 kb of the row block
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.Ws13 + (long long)rb * 16 * a.ldws, (uint32_t)(16 * a.ldws * 2));
+    const uint32_t cs = a.sh_tiled ? 1024u : 64u;
+    const uint32_t wv = (uint32_t)(a.sh_tiled ? col * 64 + kb * 16 : (col * a.ldws + kb * 8) * 2) + (uint32_t)c0 * cs;
+    const bool ok = col < a.M;                                      // columns past the tokens read row 0, unused
+    const uint16_t* xr = a.x + (long long)(ok ? col : 0) * a.ldx + kb * 8 + (long long)c0 * 32;
+    v4i A[PF], B[PF];
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    pipelined<PF>(c1 - c0,
+        [&](int slot, int c) {
+            A[slot] = buffer_load_tile(wr, wv, (uint32_t)c * cs);
+            B[slot] = *(const v4i*)(xr + (long long)c * 32);
+        },
+        [&](int slot) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, A[slot]), __builtin_bit_cast(v8bf, B[slot]), acc, 0, 0, 0);
+        });
+    s_red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || !ok) return;
+    v4f sum = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < UP_WAVES; ++w) sum += s_red[w][lane];
+    uint16_t* o = a.gus + (long long)col * a.ldgus + rb * 16 + 4 * kb;
+    o[0] = (uint16_t)f32_to_bf16_bits(sum.x);
+    o[1] = (uint16_t)f32_to_bf16_bits(sum.y);
+    o[2] = (uint16_t)f32_to_bf16_bits(sum.z);
+    o[3] = (uint16_t)f32_to_bf16_bits(sum.w);
+}
+
+template <int TILED, int PF, int PER, int EARLY, int SCL, int SH>
 __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const DecodeUpArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];   // staged activation rows (codes) then their E8M0 bytes
     __shared__ int s_eid[UP_MAXM * UP_MAXK];
@@ -48,6 +96,10 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ int s_mg, s_pick, s_xready;
     __shared__ v4f s_acc[UP_WAVES][64];
     __shared__ __align__(16) uint8_t s_wsc[SCL ? UP_WAVES * UP_WSC : 16];
+    if (SH && (int)blockIdx.y < a.sh_y) {   // a shared-expert row block (uniform over the workgroup)
+        shared_up_unit<8>(a, s_acc);
+        return;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform values kept in scalar registers
@@ -98,6 +150,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // the wave that runs the gate rotates with the workgroup index (waves 0-3 sit on different SIMDs), so the two
     // workgroups a CU holds do not run their gates on the same SIMD
     const int gw = (int)((blockIdx.x + blockIdx.y * gridDim.x) & 3);
+    const int g = (int)blockIdx.y - (SH ? a.sh_y : 0);   // this workgroup's group slot (the g-th selected expert)
     const bool gwave = early && wave == gw;
     if (gwave && a.logits) gr.load_logits(a.logits, E, a.nparts, a.pstride);
     const int xq = (wave - (wave > gw ? 1 : 0)) * 64 + lane;   // early: the lane's 16 values of row 0 among the stagers
@@ -112,7 +165,6 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
 
     // ---- this wave's weight stream: row block rb of {gate c0, gate c0 + 16, up c0, up c0 + 16}, K-half kh; the
     // expert (the buffer descriptors) comes from the routing
-    const int g = blockIdx.y;
     const int c0 = blockIdx.x * 32;
     const int rbi = wave & 3, kh = wave >> 2;
     const int row_first = (rbi < 2 ? c0 : a.I + c0) + (rbi & 1) * 16;
@@ -452,12 +504,12 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     }
 }
 
-extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
-                                   float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
-                                   long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
-                                   int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
-                                   int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
-                                   void* stream) {
+static int decode_up_launch(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                            float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
+                            long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
+                            int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
+                            int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
+                            const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream) {
     if ((!logits && (!eid_in || !wt_in)) || !x || !W13 || !S13 || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || !wt_sorted)
         return DSV41_EINVAL;
     if (M < 1 || M > UP_MAXM || topk < 1 || topk > UP_MAXK || topk > E || E < 1 || E > UP_MAXE || score_func < 0 || score_func > 2)
@@ -466,6 +518,11 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
     if (H <= 0 || (H & 255) || I <= 0 || (I & 31) || ldx < H || (ldx & 7) || (((uintptr_t)x) & 15) || (logits && ldl < E)) return DSV41_EINVAL;
     // every h row holds I codes and I / 32 scale bytes (the epilogue writes columns 0 .. I - 1 of each)
     if (ldhc < I || ldhs < I / 32) return DSV41_EINVAL;
+    // the shared expert's [w1; w3] (bf16 [2I][ldws]) and its gate/up output (bf16 [M][ldgus]): 16-row blocks addressed
+    // with 32-bit offsets, 16-byte row pieces
+    if (Ws13 && (!gus || ldws < H || (ldws & 7) || (((uintptr_t)Ws13) & 15) || 16 * ldws * 2 > 0xFFFFFFFFll || ldgus < 2 * I ||
+                 (sh_tiled && ldws != H)))
+        return DSV41_EINVAL;
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
         stride_we < (long long)2 * I * (H / 2) || stride_se < (long long)2 * I * (H / 32)) return DSV41_EINVAL;
@@ -481,20 +538,40 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
     int rows = early ? 1 : (int)(((scl ? 44 : 60) * 1024) / row_bytes);
     rows = rows > 16 ? 16 : (rows > M ? M : rows);
     if (rows < 1) return DSV41_EINVAL;
+    // the shared expert's 2 I / 16 row blocks take sh_y = 4 extra grid rows of I / 32 workgroups, ahead of the routed
+    // ones (the hardware dispatches workgroups in linear order, so their streams start first)
+    const int sh_y = Ws13 ? (2 * I / 16) / (I / 32) : 0;
     DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
-                   stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted};
+                   stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted,
+                   Ws13, ldws, gus, ldgus, sh_y, sh_tiled};
     const size_t lds = rows * row_bytes;
-    const dim3 grid(I / 32, M * topk), block(UP_WAVES * 64);
+    const dim3 grid(I / 32, M * topk + sh_y), block(UP_WAVES * 64);
     hipStream_t st = (hipStream_t)stream;
+#define UP_LAUNCH_SH(T, PER, SHV)                                                                                 \
+    do {                                                                                                      \
+        if (early) moe_decode_up_kernel<T, 8, PER, 1, 1, SHV><<<grid, block, lds, st>>>(a);                   \
+        else if (scl) moe_decode_up_kernel<T, 4, PER, 0, 1, SHV><<<grid, block, lds, st>>>(a);                \
+        else moe_decode_up_kernel<T, 4, PER, 0, 0, SHV><<<grid, block, lds, st>>>(a);                         \
+    } while (0)
 #define UP_LAUNCH(T, PER)                                                                                         \
     do {                                                                                                      \
-        if (early) moe_decode_up_kernel<T, 8, PER, 1, 1><<<grid, block, lds, st>>>(a);                        \
-        else if (scl) moe_decode_up_kernel<T, 4, PER, 0, 1><<<grid, block, lds, st>>>(a);                     \
-        else moe_decode_up_kernel<T, 4, PER, 0, 0><<<grid, block, lds, st>>>(a);                              \
+        if (sh_y) UP_LAUNCH_SH(T, PER, 1); else UP_LAUNCH_SH(T, PER, 0);                                      \
     } while (0)
     if (E <= 256) { if (tiled) UP_LAUNCH(1, 4); else UP_LAUNCH(0, 4); }
     else if (E <= 384) { if (tiled) UP_LAUNCH(1, 6); else UP_LAUNCH(0, 6); }
     else { if (tiled) UP_LAUNCH(1, 8); else UP_LAUNCH(0, 8); }
 #undef UP_LAUNCH
+#undef UP_LAUNCH_SH
     return (int)hipGetLastError();
+}
+
+extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                                   float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
+                                   long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
+                                   int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
+                                   int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
+                                   const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream) {
+    return decode_up_launch(logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, x, ldx, W13,
+                            stride_we, S13, stride_se, tiled, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start,
+                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, stream);
 }

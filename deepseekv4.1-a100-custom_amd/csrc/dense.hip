@@ -17,7 +17,8 @@ struct DenseArgs {
     uint16_t* outb; long long ldob;     // optional bf16
 };
 
-template <int WPG, int PF>
+// TILED: W in 16 x 32 tiles of 1 KiB ([N/16][K/32][16][32], ldw = K): a wave-load is one contiguous block.
+template <int WPG, int PF, int TILED>
 __global__ void __launch_bounds__(WPG * 64) dense_gemv_bf16_kernel(const DenseArgs a) {
     __shared__ v4f s_red[WPG][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -25,7 +26,9 @@ __global__ void __launch_bounds__(WPG * 64) dense_gemv_bf16_kernel(const DenseAr
     const int col = lane & 15, kb = lane >> 4;
     const int nk = a.K >> 5;                               // 32-k chunks
     const int c0 = (int)((long long)nk * wave / WPG), c1 = (int)((long long)nk * (wave + 1) / WPG);
-    const uint16_t* wrow = a.W + ((long long)nb * 16 + col) * a.ldw + kb * 8 + (long long)c0 * 32;
+    const uint16_t* wrow = TILED ? a.W + (long long)nb * 16 * a.ldw + col * 32 + kb * 8 + (long long)c0 * 512
+                                 : a.W + ((long long)nb * 16 + col) * a.ldw + kb * 8 + (long long)c0 * 32;
+    constexpr int cstep = TILED ? 512 : 32;   // elements from one 32-k chunk to the next
     const bool ok = col < a.M;
     // columns without a token read row 0 (their outputs are not stored): no divergent loads
     const uint16_t* xrow = a.x + (long long)(ok ? col : 0) * a.ldx + kb * 8 + (long long)c0 * 32;
@@ -33,7 +36,7 @@ __global__ void __launch_bounds__(WPG * 64) dense_gemv_bf16_kernel(const DenseAr
     v4i A[PF], B[PF];
     pipelined<PF>(c1 - c0,
         [&](int slot, int c) {
-            A[slot] = __builtin_nontemporal_load((const v4i*)(wrow + (long long)c * 32));
+            A[slot] = __builtin_nontemporal_load((const v4i*)(wrow + (long long)c * cstep));
             B[slot] = *(const v4i*)(xrow + (long long)c * 32);
         },
         [&](int slot) {
@@ -55,13 +58,19 @@ __global__ void __launch_bounds__(WPG * 64) dense_gemv_bf16_kernel(const DenseAr
     }
 }
 
-extern "C" int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int N, int K, const uint16_t* x, long long ldx, int M,
+extern "C" int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int tiled, int N, int K, const uint16_t* x, long long ldx, int M,
                                      float* out, long long ldo, uint16_t* outb, long long ldob, void* stream) {
-    if (!W || !x || (!out && !outb) || N <= 0 || (N & 15) || K <= 0 || (K & 31) || M < 1 || M > 16 || ldw < K || ldx < K) return DSV41_EINVAL;
+    if (!W || !x || (!out && !outb) || N <= 0 || (N & 15) || K <= 0 || (K & 31) || M < 1 || M > 16 || ldw < K || ldx < K || (tiled && ldw != K))
+        return DSV41_EINVAL;
     if ((out && ldo < N) || (outb && ldob < N)) return DSV41_EINVAL;
     DenseArgs a{W, ldw, N, K, x, ldx, M, out, ldo, outb, ldob};
     hipStream_t st = (hipStream_t)stream;
-    if (K >= 4096) dense_gemv_bf16_kernel<8, 8><<<N / 16, 512, 0, st>>>(a);
-    else dense_gemv_bf16_kernel<4, 8><<<N / 16, 256, 0, st>>>(a);
+    if (tiled) {
+        if (K >= 4096) dense_gemv_bf16_kernel<8, 8, 1><<<N / 16, 512, 0, st>>>(a);
+        else dense_gemv_bf16_kernel<4, 8, 1><<<N / 16, 256, 0, st>>>(a);
+    } else {
+        if (K >= 4096) dense_gemv_bf16_kernel<8, 8, 0><<<N / 16, 512, 0, st>>>(a);
+        else dense_gemv_bf16_kernel<4, 8, 0><<<N / 16, 256, 0, st>>>(a);
+    }
     return (int)hipGetLastError();
 }

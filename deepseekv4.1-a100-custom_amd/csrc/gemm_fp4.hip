@@ -17,6 +17,8 @@
 //                      every selected expert's w2 is read once. Optional epilogue: bf16(y + shared-expert ys).
 #include "common.h"
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
 __device__ __forceinline__ v8i widen(v4i a) { return v8i{a.x, a.y, a.z, a.w, 0, 0, 0, 0}; }
 __device__ __forceinline__ v8i join(v4i a, v4i b) { return v8i{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}; }
 
@@ -177,15 +179,27 @@ struct DownSumArgs {
     const uint16_t* ys; long long ldys;       // optional bf16 shared-expert output
     uint16_t* yb; long long ldyb;             // optional bf16 [M][N] = bf16(y + ys)
     int shard_start, shard_n;
+    // SH: the bf16 shared expert's down projection in the same launch. gus: its bf16 gate/up [M][ldgus] (the up
+    // launch's output); each workgroup turns it into h_s = fq8(bf16(silu(min(g, L)) * clamp(u, +-L))) in LDS and adds
+    // bf16(h_s . Ws2[rows]^T) (Ws2 bf16 [N][ldws2]) to y before the bf16 rounding; ys_out (optional) receives it
+    const uint16_t* gus; long long ldgus; const uint16_t* Ws2; long long ldws2; float limit; uint16_t* ys_out; long long ldyso;
+    int sh_tiled;   // Ws2 in 16 x 32 tiles of 1 KiB ([N/16][K/32][16][32], ldws2 = K) instead of row-major
 };
 
 #define DS_MAX_SLOTS 256
 #define DS_WAVES 8
 #define DS_HV 8          // H_LDS: h code vectors (16 bytes) per thread: 60 KiB of rows / 512 threads, rounded up
 #define DS_HS 4          // H_LDS: h E8M0 bytes per thread (rows * K / 32 <= 2048 whenever the rows fit 60 KiB)
+#define DS_HV_SH 4       // SH: the same with the shared expert's registers beside them (at most 32 KiB of h rows)
+#define DS_SHC 7         // SH: the shared expert's 32-k chunks per wave (K / 32 <= 8 DS_SHC)
+#define DS_HS_SH 2
+#ifndef DS_PF_SH
+#define DS_PF_SH 12      // SH: weight tiles in flight per wave
+#endif
 #define DS_SCG 2         // SCL: groups per wave whose weight scales are staged in LDS
 #define DS_SCW 2048      // SCL: LDS bytes per wave for them (<= 32 k-chunks of 64 bytes)
                          // SCL == 2: the current group's weight scales (<= 1 KiB) + its 16 h scale rows (64 bytes each)
+#define DS_GUV 2         // SH: 16-byte vectors of the shared expert's gate/up rows per thread (M * 2K * 2 <= 16 * 512 * DS_GUV)
 
 // One workgroup per 16-row block of the output; its 8 waves split the selected experts (group slots g = wave,
 // wave + 8, ...), each accumulating sum over its experts and k of W2[e] . h in one MFMA accumulator whose
@@ -202,13 +216,22 @@ struct DownSumArgs {
 // with one wide load each when the producer enters the group, into registers of the tile slot that starts it; the
 // consumer copies them into the wave's LDS region when it reaches that tile and reads its bytes there per k-step.
 // Three loads per tile remain (weights, two h vectors) instead of five.
-template <int TILED, int PF, int NKC, int H_LDS, int SCL>
+// SH (with H_LDS): the bf16 shared expert's down projection for the same 16 rows. Its gate/up rows are loaded in the
+// prologue with the h rows (16-byte vectors, staged in LDS where the end-of-kernel reduction buffers live), and h_s is
+// built in LDS (bf16, [M][K + 8]) between the prologue's two barriers. Its 32-k chunks (16 rows x 64 bytes of Ws2 =
+// 1 KiB per wave-load) are split over the 8 waves; a wave's chunks go out right behind its first routed tiles, into
+// their own registers, and are consumed after the routed pipeline, in straight-line code, so the routed pipeline runs
+// exactly as without the shared expert (mixing the two kinds in one tile loop costs its exact wait counts).
+template <int TILED, int PF, int NKC, int H_LDS, int SCL, int SH = 0>
 __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_kernel(const DownSumArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ short s_pair[DS_MAX_SLOTS][16];        // pair row of token t in group slot g (zero row if absent)
     __shared__ int s_start[DS_MAX_SLOTS + 1];
     __shared__ short s_tok[DS_MAX_SLOTS];
-    __shared__ v4f s_red[DS_WAVES][64];
+    // the waves' accumulators for the final reduction (SH: then the shared expert's after them); SH also stages the
+    // shared expert's gate/up rows here during the prologue, long before the reduction
+    __shared__ v4f s_red_all[SH ? 2 * DS_WAVES : DS_WAVES][64];
+    v4f (*s_red)[64] = s_red_all;
     __shared__ __align__(16) uint8_t s_sc[SCL ? DS_WAVES * DS_SCW : 16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -235,22 +258,37 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     // H_LDS: h rows 0 .. zero_row into registers now (buffer loads: a vector past the rows reads 0 and is not
     // stored); waves past the last vector issue none
     const int vpr = K >> 4, n_hv = (a.zero_row + 1) * vpr, n_hs = (a.zero_row + 1) * Ks;
-    v4i HV[H_LDS ? DS_HV : 1];
-    int HS[H_LDS ? DS_HS : 1];
+    constexpr int NHV = SH ? DS_HV_SH : DS_HV, NHS = SH ? DS_HS_SH : DS_HS;
+    v4i HV[H_LDS ? NHV : 1];
+    int HS[H_LDS ? NHS : 1];
     if (H_LDS) {
         const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(a.hc, (uint32_t)((long long)a.zero_row * a.ldh + K));
         const __amdgpu_buffer_rsrc_t hsr = buffer_rsrc(a.hs, (uint32_t)((long long)a.zero_row * a.ldhs + Ks));
 #pragma unroll
-        for (int i = 0; i < DS_HV; ++i) {
+        for (int i = 0; i < NHV; ++i) {
             const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
             if (i * DS_WAVES * 64 + wave * 64 < n_hv)   // wave-uniform
                 HV[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(hr, idx < n_hv ? (uint32_t)(r * a.ldh + v * 16) : 0xFFFFFFF0u, 0, 0));
         }
 #pragma unroll
-        for (int i = 0; i < DS_HS; ++i) {
+        for (int i = 0; i < NHS; ++i) {
             const int idx = i * DS_WAVES * 64 + tid, r = idx / Ks, v = idx - r * Ks;
             if (i * DS_WAVES * 64 + wave * 64 < n_hs)
                 HS[i] = buffer_load_byte(hsr, idx < n_hs ? (uint32_t)(r * a.ldhs + v) : 0xFFFFFFF0u, 0);
+        }
+    }
+    // SH: the shared expert's gate/up rows (M rows of 2K bf16 = 4K bytes each), 16-byte vectors, loaded with the h rows
+    // (past the rows the offset is beyond the descriptor: zeros, no fetch)
+    const int gvr = SH ? (K >> 2) : 0;                  // vectors per row
+    const int n_gv = SH ? a.M * gvr : 0;
+    v4i GV[SH ? DS_GUV : 1];
+    if (SH) {
+        const __amdgpu_buffer_rsrc_t gr = buffer_rsrc(a.gus, (uint32_t)((long long)(a.M - 1) * a.ldgus * 2 + 4 * K));
+#pragma unroll
+        for (int i = 0; i < DS_GUV; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid, t = idx / (gvr > 0 ? gvr : 1), v = idx - t * gvr;
+            GV[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                gr, idx < n_gv ? (uint32_t)(t * a.ldgus * 2 + v * 16) : 0xFFFFFFF0u, 0, 0));
         }
     }
     int e = gvalid && ge >= 0 ? ge - a.shard_start : -1;
@@ -341,6 +379,10 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     const uint8_t* wscl = s_sc + (SCL ? wave * DS_SCW : 0) + col * 4 + kb;
     // SCL == 2: weight scale of (col, kb) at k-chunk kc: 64 kc + 4 col + kb; h scale: 1024 + 64 col + 4 kc + kb
     const uint8_t* gsw = s_sc + (GS ? wave * DS_SCW : 0);
+    // SH: h_s rows in LDS after the h rows and their scales (bf16, row stride K + 8); lane (col, kb) reads token col's
+    // k [32 c + 8 kb, +8) (columns past the tokens read token 0: unused)
+    const int hss = (K + 8) * 2;
+    uint8_t* const hsh = smem + (((size_t)(a.zero_row + 1) * LS + (size_t)(a.zero_row + 1) * Ks + 15) & ~(size_t)15);
     auto use = [&](int slot) {
         if (GS && ckc == 0) {
             // the consumer enters a group (the previous group's reads were issued before, and one wave's LDS
@@ -411,6 +453,21 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+    // SH: this wave's share of the shared expert's 32-k chunks (a contiguous range of at most DS_SHC), issued behind the
+    // routed first tiles into their own registers and consumed after the routed pipeline (slots past the range read
+    // zeros: offset beyond the descriptor)
+    const int shc = SH ? (K >> 5) : 0;
+    const int sc0 = SH ? shc * wave / DS_WAVES : 0, n_sh = SH ? shc * (wave + 1) / DS_WAVES - sc0 : 0;
+    v4i SW[SH ? DS_SHC : 1];
+    if (SH) {
+        const __amdgpu_buffer_rsrc_t s2r = buffer_rsrc(a.Ws2 + (long long)nb * 16 * a.ldws2, (uint32_t)(16 * a.ldws2 * 2));
+        // lane (col, kb)'s 16 bytes of chunk c: row col, k [32 c + 8 kb, +8); tiled: at 1024 c + 64 col + 16 kb
+        const uint32_t cs = a.sh_tiled ? 1024u : 64u;
+        const uint32_t wv2 = (uint32_t)(a.sh_tiled ? (lane & 15) * 64 + (lane >> 4) * 16 : ((lane & 15) * a.ldws2 + (lane >> 4) * 8) * 2) +
+                             (uint32_t)sc0 * cs;
+#pragma unroll
+        for (int j = 0; j < DS_SHC; ++j) SW[j] = buffer_load_tile(s2r, j < n_sh ? wv2 : 0xFFFFFFF0u, (uint32_t)j * cs);
+    }
 
     // ---- tables -> LDS (and h rows 0 .. zero_row when H_LDS: their loads are older than every tile), the wave's
     // weight scales (SCL), then the pair rows of every valid group
@@ -418,15 +475,23 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     if (tid < n_slots) s_tok[tid] = (short)tk;
     if (H_LDS) {
 #pragma unroll
-        for (int i = 0; i < DS_HV; ++i) {
+        for (int i = 0; i < NHV; ++i) {
             const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
             if (i * DS_WAVES * 64 + wave * 64 < n_hv && idx < n_hv) *(v4i*)(smem + r * LS + v * 16) = HV[i];
         }
         uint8_t* hsw = smem + (size_t)(a.zero_row + 1) * LS;
 #pragma unroll
-        for (int i = 0; i < DS_HS; ++i) {
+        for (int i = 0; i < NHS; ++i) {
             const int idx = i * DS_WAVES * 64 + tid;
             if (i * DS_WAVES * 64 + wave * 64 < n_hs && idx < n_hs) hsw[idx] = (uint8_t)HS[i];
+        }
+    }
+    if (SH) {
+        uint8_t* gsh = (uint8_t*)s_red_all;
+#pragma unroll
+        for (int i = 0; i < DS_GUV; ++i) {
+            const int idx = i * DS_WAVES * 64 + tid;
+            if (idx < n_gv) *(v4i*)(gsh + idx * 16) = GV[i];
         }
     }
     if (SCL == 1) {
@@ -451,6 +516,24 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
         if (e >= 0)
             for (int q = s_start[gslot]; q < s_start[gslot + 1]; ++q) s_pair[gslot][s_tok[q] & 15] = (short)q;
     }
+    if (SH) {
+        // h_s = fq8(bf16(silu(min(g, L)) * clamp(u, +-L))) per 32 columns (fused.py:284-306 without a routing weight:
+        // the shared expert's swiglu_quant(gu, None, ...), model.py:410), stored as bf16 values; half-wave j takes the
+        // 32-column groups j, j + 16, ... of every token
+        const uint16_t* gsh = (const uint16_t*)s_red_all;
+        const int shg = a.M * (K >> 5);
+        for (int idx = tid >> 5; idx < shg; idx += 2 * DS_WAVES) {
+            const int t = idx / (K >> 5), c = (idx - t * (K >> 5)) * 32 + (tid & 31);
+            float gg = bf16_to_f32(gsh[t * 2 * K + c]), uu = bf16_to_f32(gsh[t * 2 * K + K + c]);
+            if (a.limit > 0.f) {
+                uu = fminf(fmaxf(uu, -a.limit), a.limit);
+                gg = fminf(gg, a.limit);
+            }
+            const float h = bf16_round(gg * (1.0f / (1.0f + expf(-gg))) * uu);
+            const int ex = fq8_exponent(wave_max32(fabsf(h)));
+            *(uint16_t*)(hsh + (size_t)t * hss + c * 2) = (uint16_t)f32_to_bf16_bits(fq8_value(fq8_code(h, ex), ex));
+        }
+    }
     __syncthreads();
     if (H_LDS) {
         group_rows();
@@ -465,25 +548,52 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
         prod_rows();
         pipelined<PF>(total, load, use);
     }
+    v4f acc_s = v4f{0.f, 0.f, 0.f, 0.f};
+    if (SH) {
+        // the wave's shared-expert chunks: bf16 products of Ws2's 16 rows with h_s (lane (col, kb): token col's k
+        // [32 c + 8 kb, +8); columns past the tokens read token 0, unused). Slots past the wave's range hold zeros and
+        // read an in-range chunk of h_s (finite), so they add exactly 0.
+        const uint8_t* hl = hsh + (size_t)(col < a.M ? col : 0) * hss + kb * 16;
+#pragma unroll
+        for (int j = 0; j < DS_SHC; ++j) {
+            const int c = min(sc0 + j, shc - 1);
+            const v4i b = *(const v4i*)(hl + c * 64);
+            acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, SW[j]), __builtin_bit_cast(v8bf, b), acc_s, 0, 0, 0);
+        }
+    }
     s_red[wave][lane] = acc;
+    if (SH) s_red_all[DS_WAVES + wave][lane] = acc_s;
     __syncthreads();
     if (wave != 0) return;
     v4f sum = s_red[0][lane];
 #pragma unroll
     for (int w = 1; w < DS_WAVES; ++w) sum += s_red[w][lane];
+    v4f ssum = v4f{0.f, 0.f, 0.f, 0.f};
+    if (SH) {
+        ssum = s_red_all[DS_WAVES][lane];
+#pragma unroll
+        for (int w = 1; w < DS_WAVES; ++w) ssum += s_red_all[DS_WAVES + w][lane];
+    }
     if (col >= a.M) return;
     const int row0 = nb * 16 + 4 * kb;
     if (a.y) {
         float* o = a.y + (long long)col * a.ldy + row0;
         o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
     }
-    if (a.yb) {
+    if (a.yb || (SH && a.ys_out)) {
         const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+        const float sv[4] = {ssum.x, ssum.y, ssum.z, ssum.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float t = v[i];
-            if (a.ys) t += bf16_to_f32(a.ys[(long long)col * a.ldys + row0 + i]);
-            a.yb[(long long)col * a.ldyb + row0 + i] = (uint16_t)f32_to_bf16_bits(t);
+            if (SH) {   // the shared expert's output is a bf16 tensor (w8.py:102-103), added to the fp32 sum (model.py:590)
+                const uint32_t yb16 = f32_to_bf16_bits(sv[i]);
+                if (a.ys_out) a.ys_out[(long long)col * a.ldyso + row0 + i] = (uint16_t)yb16;
+                t += bf16_to_f32(yb16);
+            } else if (a.ys) {
+                t += bf16_to_f32(a.ys[(long long)col * a.ldys + row0 + i]);
+            }
+            if (a.yb) a.yb[(long long)col * a.ldyb + row0 + i] = (uint16_t)f32_to_bf16_bits(t);
         }
     }
 }
@@ -530,8 +640,17 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                                   int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                                   const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                                   float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
-                                  int shard_start, int shard_n, void* stream) {
-    if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb)) return DSV41_EINVAL;
+                                  int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
+                                  long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, void* stream) {
+    if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb && !ys_out)) return DSV41_EINVAL;
+    // the fused shared expert: its gate/up (bf16 [M][ldgus], 2 K columns) and Ws2 (bf16 [N][ldws2], 16-byte row pieces,
+    // 16-row blocks addressed with 32-bit offsets); it replaces a given ys
+    const bool sh = Ws2 != nullptr;
+    if (sh && (!gus || ys || ldgus < 2LL * K || ldws2 < K || (ldws2 & 7) || (((uintptr_t)Ws2) & 15) || 16 * ldws2 * 2 > 0xFFFFFFFFll ||
+               (ldgus & 7) || (((uintptr_t)gus) & 15) || (sh_tiled && ldws2 != K) || (long long)M * 4 * K > 16LL * DS_WAVES * 64 * DS_GUV ||
+               (long long)M * 4 * K > (long long)sizeof(v4f) * 2 * DS_WAVES * 64 || (ys_out && ldyso < N)))
+        return DSV41_EINVAL;
+    if (!sh && !y && !yb) return DSV41_EINVAL;
     // zero_row is kept in the kernel's 16-bit pair table
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0 || zero_row > 32767)
         return DSV41_EINVAL;
@@ -542,9 +661,11 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     if ((ldh & 15) || (((uintptr_t)hc) & 15) || ldh < K || ldhs < K / 32) return DSV41_EINVAL;
     if ((y && ldy < N) || (yb && ldyb < N) || (yb && ys && ldys < N)) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
-                  y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n};
+                  y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, gus, ldgus, Ws2, ldws2, limit, ys_out, ldyso, sh_tiled};
     hipStream_t st = (hipStream_t)stream;
-    const size_t lds = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
+    // dynamic LDS: the h rows (codes, then their E8M0 bytes) and, with the shared expert, its bf16 h_s rows
+    const size_t lds_h = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
+    const size_t lds = sh ? ((lds_h + 15) & ~(size_t)15) + (size_t)M * (K + 8) * 2 : lds_h;
     // the h buffer descriptors (staged h, per-group scale loads) take 32-bit sizes and offsets; otherwise h is read
     // through 64-bit pointers
     const bool h32 = (long long)zero_row * ldh + K <= 0xFFFFFFFFll && (long long)zero_row * ldhs + K / 32 <= 0xFFFFFFFFll;
@@ -560,7 +681,18 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     // h scale rows hold >= 16 bytes and every wide load is aligned (16 bytes for the weight scales, 4 for h's)
     const bool gs = !h_lds && h32 && K / 128 <= 16 && K >= 512 && (((uintptr_t)S) & 15) == 0 && (stride_se & 15) == 0 &&
                     (ldhs & 3) == 0 && (((uintptr_t)hs) & 3) == 0;
+    // the fused shared expert runs with the h rows staged in LDS only, through fewer staging registers
+    if (sh && !(h_lds && K / 32 <= DS_SHC * DS_WAVES && (long long)(zero_row + 1) * (K / 16) <= DS_HV_SH * DS_WAVES * 64 &&
+                (long long)(zero_row + 1) * (K / 32) <= DS_HS_SH * DS_WAVES * 64))
+        return DSV41_EINVAL;
 #define DS_LAUNCH(T, PF, NK, HL, SC) moe_down_sum_kernel<T, PF, NK, HL, SC><<<grid, block, HL ? lds : 0, st>>>(a)
+#define DS_LAUNCH_SH(T, SC) moe_down_sum_kernel<T, DS_PF_SH, 0, 1, SC, 1><<<grid, block, lds, st>>>(a)
+    if (sh) {
+        if (scl) { if (tiled) DS_LAUNCH_SH(1, 1); else DS_LAUNCH_SH(0, 1); }
+        else { if (tiled) DS_LAUNCH_SH(1, 0); else DS_LAUNCH_SH(0, 0); }
+        return (int)hipGetLastError();
+    }
+#undef DS_LAUNCH_SH
     if (scl) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 1); else DS_LAUNCH(0, 12, 0, 1, 1); }
     else if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 0); else DS_LAUNCH(0, 12, 0, 1, 0); }
     else if (gs) { if (tiled) DS_LAUNCH(1, 6, 0, 0, 2); else DS_LAUNCH(0, 6, 0, 0, 2); }

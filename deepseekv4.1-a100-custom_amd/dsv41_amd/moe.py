@@ -59,6 +59,42 @@ class ExpertWeights:
         return per(self.w13) + per(self.s13) + per(self.w2) + per(self.s2)
 
 
+@dataclass
+class SharedExpert:
+    """The bf16 shared expert of a layer (model.py:385-387, 409-412): w13 = [w1; w3] bf16 [2I, H] (gate rows, then up
+    rows) and w2 bf16 [H, I]; `tiled`: both in the tile_bf16 layout (16 x 32 tiles of 1 KiB, one contiguous block per
+    wave-load), which the decode kernels stream faster than row-major rows."""
+    w13: torch.Tensor
+    w2: torch.Tensor
+    tiled: bool = False
+
+    @property
+    def I(self) -> int:
+        return self.w2.shape[1]
+
+    @classmethod
+    def of(cls, shared) -> "SharedExpert | None":
+        """A SharedExpert from one, or from a (w13, w2) row-major pair; None stays None."""
+        if shared is None or isinstance(shared, SharedExpert):
+            return shared
+        w13, w2 = shared
+        return cls(w13, w2, False)
+
+    @classmethod
+    def prepare(cls, w13: torch.Tensor, w2: torch.Tensor, tiled: bool = True) -> "SharedExpert":
+        """From row-major [w1; w3] and w2 (bf16, on the GPU), repacked once into the tiled layout when `tiled`."""
+        from .quant import tile_bf16
+        w13, w2 = w13.to(torch.bfloat16).contiguous(), w2.to(torch.bfloat16).contiguous()
+        return cls(tile_bf16(w13), tile_bf16(w2), True) if tiled else cls(w13, w2, False)
+
+    def check(self, H: int, I: int):
+        assert self.w13.dtype == torch.bfloat16 and self.w2.dtype == torch.bfloat16
+        assert tuple(self.w13.shape) == (2 * I, H) and tuple(self.w2.shape) == (H, I)
+        assert self.w13.stride(1) == 1 and self.w2.stride(1) == 1
+        if self.tiled:
+            assert self.w13.is_contiguous() and self.w2.is_contiguous()
+
+
 class _Workspace:
     def __init__(self, dev, M, k, H, I):
         P = M * k
@@ -74,6 +110,16 @@ class _Workspace:
         self.grp_start = torch.empty(P + 1, dtype=i32, device=dev)
         self.eid = torch.empty(M, k, dtype=i32, device=dev)       # routing, when the caller keeps none
         self.wt = torch.empty(M, k, dtype=f32, device=dev)
+        self.gus = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)   # the fused shared expert's gate/up
+        self.shared = None                                          # the SharedExpert of the last decode_up, if fused
+
+
+def fused_shared_ok(M: int, k: int, I: int) -> bool:
+    """Whether the bf16 shared expert can ride in the two decode launches (dsv41_moe_down_sum's LDS rule: the h rows,
+    their scales and M bf16 h_s rows in 60 KiB, M I <= 4096); otherwise it runs as its own launches."""
+    P = M * k
+    lds = (((P + 1) * (I + 16) + (P + 1) * (I // 32) + 15) & ~15) + M * (I + 8) * 2
+    return lds <= 60 * 1024 and (P + 1) * (I // 16) <= 8 * 512 and (P + 1) * (I // 32) <= 4 * 512 and M * I <= 4096 and P <= 256
 
 
 _WS: dict = {}
@@ -94,9 +140,11 @@ def _as(t: torch.Tensor, dtype) -> torch.Tensor:
     return t.contiguous()
 
 
-def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=None, eid=None, wt=None, eid_out=None, wt_out=None):
+def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=None, eid=None, wt=None, eid_out=None, wt_out=None,
+              shared=None):
     """The first of the two decode launches (dsv41_moe_decode_up): routing (from `logits` with gate = (bias,
-    temp, route_scale, score_func, norm), or the given eid / wt), bucketing, up projection and SwiGLU.
+    temp, route_scale, score_func, norm), or the given eid / wt), bucketing, up projection and SwiGLU; with
+    shared (a SharedExpert or a row-major (w13, w2) pair) also the shared expert's gate/up (decode_down finishes it).
     Returns the workspace holding h (codes + E8M0, expert-sorted pair rows) and the tables for decode_down."""
     dev = _lib.require_cuda(xq, logits, eid, wt)
     M, H = xq.shape
@@ -117,42 +165,74 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
     else:
         eid32, wt32 = _as(eid, torch.int32), _as(wt, torch.float32)
         route = (None, ex.E, 1, 0, None, 1.0, 1.0, 0, 0, _lib.ptr(eid32), _lib.ptr(wt32))
+    sh = SharedExpert.of(shared)
+    Ws13 = None
+    if sh is not None:
+        sh.check(H, ex.I)
+        assert fused_shared_ok(M, k, ex.I)
+        Ws13 = sh.w13
+    ws.shared = sh
     _lib.call("dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, H, ex.I, float(limit), _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0),
               _lib.ptr(eid_out), _lib.ptr(wt_out), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.tok_sorted),
-              _lib.ptr(ws.wt_sorted), _lib.stream(dev))
+              _lib.ptr(ws.wt_sorted), _lib.ptr(Ws13), H if Ws13 is None else Ws13.stride(0), 1 if sh is not None and sh.tiled else 0,
+              _lib.ptr(ws.gus), ws.gus.stride(0), _lib.stream(dev))
     return ws
 
 
-def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None):
+def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, limit: float = 0.0, ys_out=None):
     """The second decode launch (dsv41_moe_down_sum): y[t] = sum over t's groups of h . deq(W2[e])^T (fp32, into
-    y32 or the workspace) and/or out = bf16(y + ys)."""
-    dev = _lib.require_cuda(ws.hc, ys, out, y32)
+    y32 or the workspace) and/or out = bf16(y + ys). When decode_up ran with the shared expert, this launch finishes it
+    (SwiGLU with `limit`, Ws2) and adds its bf16 output instead of `ys` (ys_out, bf16 [M, H], receives it)."""
+    dev = _lib.require_cuda(ws.hc, ys, out, y32, ys_out)
     M, H = ws.M, ex.H
     y = ws.y if y32 is None else y32
     want_y = out is None or y32 is not None
+    Ws2 = None
+    if ws.shared is not None:
+        Ws2 = ws.shared.w2
+        assert ys is None
     _lib.call("dsv41_moe_down_sum", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H, ex.I,
               _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), ws.P, _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start),
               _lib.ptr(ws.tok_sorted), ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
-              _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.stream(dev))
+              _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.ptr(ws.gus) if Ws2 is not None else None, ws.gus.stride(0),
+              _lib.ptr(Ws2), ex.I if Ws2 is None else Ws2.stride(0), 1 if Ws2 is not None and ws.shared.tiled else 0, float(limit),
+              _lib.ptr(ys_out), H if ys_out is None else ys_out.stride(0), _lib.stream(dev))
     return out if out is not None else y
 
 
+def _shared_plan(xq, shared, ys, k, ex, limit, ys_out):
+    """(shared expert for the fused launches or None, ys): the bf16 shared expert rides in the two decode launches when
+    it fits them; otherwise it runs first as its own launches and enters as ys."""
+    sh = SharedExpert.of(shared)
+    if sh is None:
+        return None, ys
+    assert ys is None, "give either the shared expert's weights or its output"
+    if fused_shared_ok(xq.shape[0], k, ex.I):
+        return sh, None
+    return None, shared_expert(xq, sh.w13, sh.w2, limit, ys=ys_out, tiled=sh.tiled)
+
+
 def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
-                ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None) -> torch.Tensor:
+                ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None,
+                shared: tuple | None = None, ys_out: torch.Tensor | None = None) -> torch.Tensor:
     """Routed experts of one layer for M <= 16 tokens with given routing.
     xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int [M, k] (distinct per token); wt fp32 [M, k].
     Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
     or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None);
-    y32 (fp32 [M, H]) additionally receives y."""
-    ws = decode_up(xq, ex, limit, eid.shape[-1], eid=eid, wt=wt)
-    return decode_down(ws, ex, ys, out, y32)
+    y32 (fp32 [M, H]) additionally receives y. shared (a SharedExpert, or a row-major (w13, w2) bf16 pair) computes
+    the shared expert too (model.py:409-412) instead of taking ys: in the same two launches when it fits them
+    (fused_shared_ok), else as its own launches first; ys_out (bf16 [M, H]) receives its output."""
+    k = eid.shape[-1]
+    fused, ys = _shared_plan(xq, shared, ys, k, ex, limit, ys_out)
+    ws = decode_up(xq, ex, limit, k, eid=eid, wt=wt, shared=fused)
+    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None)
 
 
 def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None, temp: float, topk: int, route_scale: float,
                       score_func: str, norm: bool, ex: ExpertWeights, limit: float, ys: torch.Tensor | None = None,
                       out: torch.Tensor | None = None, y32: torch.Tensor | None = None, eid_out: torch.Tensor | None = None,
-                      wt_out: torch.Tensor | None = None) -> torch.Tensor:
+                      wt_out: torch.Tensor | None = None, shared: tuple | None = None, ys_out: torch.Tensor | None = None) -> torch.Tensor:
     """gate_topk (fused2.py:418-452) with the routed experts: logits fp32 [M, E] -> routing (written to
     eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts.
     M = 1: the routing runs inside the up-projection launch (every workgroup routes the one token while its
@@ -160,22 +240,23 @@ def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor
     each of its workgroups would cost more than the extra launch)."""
     M = xq.shape[0]
     gate = (bias, temp, route_scale, score_func, norm)
+    fused, ys = _shared_plan(xq, shared, ys, topk, ex, limit, ys_out)
     if M == 1:
-        ws = decode_up(xq, ex, limit, topk, logits=logits, gate=gate, eid_out=eid_out, wt_out=wt_out)
+        ws = decode_up(xq, ex, limit, topk, logits=logits, gate=gate, eid_out=eid_out, wt_out=wt_out, shared=fused)
     else:
         from .fused2 import gate_topk
         ws0 = _workspace(_lib.require_cuda(xq), M, topk, ex.H, ex.I)
         eid = ws0.eid if eid_out is None else eid_out
         wt = ws0.wt if wt_out is None else wt_out
         gate_topk(logits, bias, temp, topk, route_scale, score_func, norm, eid=eid, wt=wt)
-        ws = decode_up(xq, ex, limit, topk, eid=eid, wt=wt)
-    return decode_down(ws, ex, ys, out, y32)
+        ws = decode_up(xq, ex, limit, topk, eid=eid, wt=wt, shared=fused)
+    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None)
 
 
 # --------------------------------------------------------------------------- dense bf16 (shared expert, router)
-def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, out_bf16: bool = False) -> torch.Tensor:
-    """out[t, n] = sum_k x[t, k] W[n, k] for M <= 16 rows of bf16 x and bf16 W [N, K] (fp32 accumulation);
-    fp32 output, or bf16 (round to nearest even) when out_bf16."""
+def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None, out_bf16: bool = False, tiled: bool = False) -> torch.Tensor:
+    """out[t, n] = sum_k x[t, k] W[n, k] for M <= 16 rows of bf16 x and bf16 W [N, K] (fp32 accumulation; `tiled`: W in
+    the tile_bf16 layout); fp32 output, or bf16 (round to nearest even) when out_bf16."""
     dev = _lib.require_cuda(W, x)
     M, K = x.shape
     N = W.shape[0]
@@ -183,7 +264,8 @@ def dense_gemv(W: torch.Tensor, x: torch.Tensor, out: torch.Tensor | None = None
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=dev)
     is_b = out.dtype == torch.bfloat16
-    _lib.call("dsv41_dense_gemv_bf16", _lib.ptr(W), W.stride(0), N, K, _lib.ptr(x), x.stride(0), M,
+    assert not tiled or W.is_contiguous()
+    _lib.call("dsv41_dense_gemv_bf16", _lib.ptr(W), W.stride(0), 1 if tiled else 0, N, K, _lib.ptr(x), x.stride(0), M,
               None if is_b else _lib.ptr(out), out.stride(0), _lib.ptr(out) if is_b else None, out.stride(0), _lib.stream(dev))
     return out
 
@@ -289,10 +371,11 @@ class _SharedWs:
 _SWS: dict = {}
 
 
-def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit: float, ys: torch.Tensor | None = None) -> torch.Tensor:
-    """Shared expert with bf16 weights (model.py:409-412, decode.py:368-370): gu = linear_w(xq, Ws13) is bf16 (one
-    rounding of the fp32-accumulated product), h = swiglu_quant(gu, no weight) (bf16 on the FP8 grid),
-    ys = bf16(h . Ws2^T). Ws13 = [w1; w3] bf16 [2I, H]."""
+def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit: float, ys: torch.Tensor | None = None,
+                  tiled: bool = False) -> torch.Tensor:
+    """Shared expert with bf16 weights as its own launches (model.py:409-412, decode.py:368-370): gu = linear_w(xq,
+    Ws13) is bf16 (one rounding of the fp32-accumulated product), h = swiglu_quant(gu, no weight) (bf16 on the FP8
+    grid), ys = bf16(h . Ws2^T). Ws13 = [w1; w3] bf16 [2I, H]; `tiled`: both in the tile_bf16 layout."""
     dev = _lib.require_cuda(xq, Ws13, Ws2)
     M, H = xq.shape
     I = Ws2.shape[1]
@@ -300,10 +383,10 @@ def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit
     sw = _SWS.get(key)
     if sw is None:
         sw = _SWS[key] = _SharedWs(dev, M, H, I)
-    dense_gemv(Ws13, xq, out=sw.gu)
+    dense_gemv(Ws13, xq, out=sw.gu, tiled=tiled)
     _lib.call("dsv41_swiglu_quant", _lib.ptr(sw.gu), 1, sw.gu.stride(0), None, M, I, float(limit), None, None, _lib.ptr(sw.h), 0, _lib.stream(dev))
     out = sw.ys if ys is None else ys
-    dense_gemv(Ws2, sw.h, out=out)
+    dense_gemv(Ws2, sw.h, out=out, tiled=tiled)
     return out
 
 
@@ -317,6 +400,8 @@ class MoEDecodeLayer:
                  router: torch.Tensor | None = None, bias: torch.Tensor | None = None, temp: float = 1.0):
         experts.check()
         self.ex, self.Ws13, self.Ws2, self.limit = experts, Ws13, Ws2, float(limit)
+        # the shared expert as the decode kernels stream it best (tile_bf16 layout, repacked once)
+        self.shared = SharedExpert.prepare(Ws13, Ws2, tiled=True) if Ws13 is not None else None
         self.topk, self.score_func, self.route_scale, self.norm = topk, score_func, route_scale, norm
         self.router, self.bias, self.temp = router, bias, temp
         self._bufs: dict = {}
@@ -345,12 +430,11 @@ class MoEDecodeLayer:
         if logits is None:
             assert self.router is not None, "router weights or logits are required"
             logits = dense_gemv(self.router, x, out=b["logits"])
-        ys = None
-        if self.Ws13 is not None:
-            ys = shared_expert(b["xq"], self.Ws13, self.Ws2, self.limit, ys=b["ys"])
         o = b["out"] if out is None else out
+        shared = self.shared
         moe_route_experts(b["xq"], logits, self.bias, self.temp, self.topk, self.route_scale, self.score_func, self.norm and self.topk > 1,
-                          self.ex, self.limit, ys=ys, out=o, eid_out=b["eid"], wt_out=b["wt"])
+                          self.ex, self.limit, out=o, eid_out=b["eid"], wt_out=b["wt"], shared=shared,
+                          ys_out=b["ys"] if shared is not None else None)
         return o
 
     @property

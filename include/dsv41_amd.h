@@ -68,25 +68,35 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
  * group), grp_start [P + 1], tok_sorted [P], wt_sorted [P]; routing eid_out / wt_out [M][topk] (optional).
  * Expert ids outside [0, E) are dropped. Replaces gate_topk + moe_dispatch + the w13 fp4_gemm_tc + swiglu_quant
  * of decode.DecodeRuntime.moe2 / experts_tc (decode.py:354-361, 316-335; fused2.py:418-452; cukern.py:238-276;
- * fused.py:283-345; p2p.cu:90-132). */
+ * fused.py:283-345; p2p.cu:90-132).
+ * Optional bf16 shared expert (Ws13 = [w1; w3] bf16 [2I][ldws], or NULL; sh_tiled = 1: in 16 x 32 tiles of 1 KiB,
+ * [2I/16][H/32][16][32] with ldws = H): the same launch also writes its gate/up gus = bf16(x . Ws13^T) as bf16
+ * [M][ldgus] (linear_w(xq, sh_w13), decode.py:368), for dsv41_moe_down_sum. */
 int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
                         float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
                         long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                         int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                         int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
-                        void* stream);
+                        const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream);
 
 /* Decode down projection and per-token combine: y[t][n] = sum over groups g and their pair p of token t of
  * h_p . deq(W2[e_g])[n]  (M <= 16 tokens, n_slots <= 256 group slots; slots with expert -1 are unused).
  * zero_row: index of an all-zero row of hc and hs (read for tokens a group does not contain).
  * Optional outputs: y fp32 [M][ldy]; yb bf16 = bf16(y + ys) with ys the bf16 shared-expert output or NULL.
  * Replaces the w2 call of decode.DecodeRuntime.experts_tc (decode.py:316-335) plus the sum of the k rows in
- * fused2.hc_post2_ (fused2.py:490-495) and model.MoE.__call__ (model.py:581, 590-591). */
+ * fused2.hc_post2_ (fused2.py:490-495) and model.MoE.__call__ (model.py:581, 590-591).
+ * Optional bf16 shared expert in the same launch (Ws2 bf16 [N][ldws2], or NULL; then ys must be NULL; sh_tiled = 1:
+ * Ws2 in 16 x 32 tiles of 1 KiB, [N/16][K/32][16][32] with ldws2 = K): from gus
+ * (dsv41_moe_decode_up's bf16 gate/up [M][ldgus]) each workgroup forms h_s = swiglu_quant(gus, no weight, limit)
+ * (model.py:410) and adds ys = bf16(h_s . Ws2^T) (linear_w(hs, sh_w2), decode.py:370) to y before the bf16 rounding
+ * of yb; ys_out (bf16 [M][ldyso], optional) receives ys. Needs the h rows and h_s in 60 KiB of LDS
+ * ((n_slots + 1)(K + 16 + K / 32) + 2 M (K + 8) bytes, e.g. M <= 2 at K = 1664) and M K <= 4096; else -1. */
 int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
                        int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                        const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                        float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
-                       int shard_start, int shard_n, void* stream);
+                       int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
+                       long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, void* stream);
 
 /* Prefill w13 + SwiGLU: for every group g of <= 128 expert-sorted pairs (moe_dispatch tables with gmax 128),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;
@@ -111,10 +121,11 @@ int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, lon
 int dsv41_combine_pairs(const float* y2, long long ldy2, const int* inv, int topk, int T, int N, const uint16_t* ys, long long ldys,
                         uint16_t* out, long long ldo, float* y32, long long ld32, void* stream);
 
-/* out[t][n] = sum_k x[t][k] * W[n][k], bf16 W [N][ldw], bf16 x [M][ldx], M <= 16, fp32 and/or bf16 output.
+/* out[t][n] = sum_k x[t][k] * W[n][k], bf16 W [N][ldw] (tiled = 1: 16 x 32 tiles of 1 KiB, [N/16][K/32][16][32] with
+ * ldw = K), bf16 x [M][ldx], M <= 16, fp32 and/or bf16 output.
  * The bf16 shared expert's two GEMVs (model.MoE.shared_expert, model.py:409-412; decode.py:369-371) and the
  * router logits (decode.py:357, model.py:391-392). */
-int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int N, int K, const uint16_t* x, long long ldx, int M,
+int dsv41_dense_gemv_bf16(const uint16_t* W, long long ldw, int tiled, int N, int K, const uint16_t* x, long long ldx, int M,
                           float* out, long long ldo, uint16_t* outb, long long ldob, void* stream);
 
 /* Layer-to-layer step of the decode stack, per token row (M rows, H <= 8192, H % 32 == 0): r = bf16(x + y),

@@ -49,11 +49,11 @@ def test_invalid_arguments_are_rejected_without_launch():
     assert L.dsv41_dequant_fp4(None, None, 16, 64, 0, None, None) == -1
     assert L.dsv41_quant_fp8(ctypes.c_void_p(16), 0, 4, 33, 33, 0, ctypes.c_void_p(16), None, None, None) == -1  # K % 32
     assert L.dsv41_moe_dispatch(ctypes.c_void_p(16), None, 8, 8, 1000, 64, *[ctypes.c_void_p(16)] * 5, None, None) == -1  # E > 512
-    assert L.dsv41_dense_gemv_bf16(ctypes.c_void_p(16), 64, 16, 64, ctypes.c_void_p(16), 64, 17, ctypes.c_void_p(16), 16, None, 0, None) == -1
+    assert L.dsv41_dense_gemv_bf16(ctypes.c_void_p(16), 64, 0, 16, 64, ctypes.c_void_p(16), 64, 17, ctypes.c_void_p(16), 16, None, 0, None) == -1
     # decode down projection: h rows shorter than K (codes or scales), an output row stride below N
     p = ctypes.c_void_p(16)
     down = lambda ldh, ldhs, ldy: L.dsv41_moe_down_sum(p, 7168 * 832, p, 7168 * 52, 1, 7168, 1664, p, ldh, p, ldhs, 8, p, p, p, 8, 1,
-                                                      p, ldy, None, 7168, None, 7168, 0, 384, None)
+                                                      p, ldy, None, 7168, None, 7168, 0, 384, None, 0, None, 0, 0, 0.0, None, 0, None)
     assert down(1600, 52, 7168) == -1
     assert down(1664, 51, 7168) == -1
     assert down(1664, 52, 7000) == -1
@@ -88,15 +88,18 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
 
     def up(ldhc, ldhs):
         return L.dsv41_moe_decode_up(None, 0, 1, 0, None, 1.0, 1.0, 2, 1, p, p, 1, 8, 384, p, H, p, 2 * I * H // 2, p, 2 * I * H // 32,
-                                     1, H, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p, None)
+                                     1, H, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p, None, 0, 0, None, 0, None)
     assert up(I - 32, I // 32) == -1
     assert up(I, I // 32 - 1) == -1
 
-    def down(zero_row):
-        return L.dsv41_moe_down_sum(p, H * (I // 2), p, H * (I // 32), 1, H, I, p, I, p, I // 32, zero_row, p, p, p, 8, 1,
-                                    p, H, None, H, None, H, 0, 384, None)
+    def down(zero_row, Ws2=None, M=1, ys=None):
+        return L.dsv41_moe_down_sum(p, H * (I // 2), p, H * (I // 32), 1, H, I, p, I, p, I // 32, zero_row, p, p, p, 8, M,
+                                    p, H, ys, H, None, H, 0, 384, p if Ws2 else None, 2 * I, Ws2, I, 0, ctypes.c_float(10.0), None, H, None)
     assert down(32768) == -1
     assert down(-1) == -1
+    # the fused shared expert: not together with a given ys, and only while its M h_s rows fit (M I / 32 <= 128)
+    assert down(8, Ws2=p, ys=p) == -1
+    assert down(8, Ws2=p, M=3) == -1
 
 
 def test_noalloc_rejects_calls_beyond_its_scratch():

@@ -692,3 +692,37 @@ def test_grouped_gemm_bounds():
     assert np.all(got[1] == 0.0)          # token 7 of 4 rows: zeros
     assert np.all(got[2] == 5.0)          # expert 9 of 6: skipped, untouched
     close(got[3:5], ref[3:5], "range clamped to n_pairs")
+
+
+@pytest.mark.parametrize("M,tiled", [(1, True), (2, True), (1, False)])
+def test_decode_fused_shared_expert(full_layer, M, tiled):
+    """The bf16 shared expert riding in the two decode launches (its gate/up row blocks in the up launch, its down
+    projection in each down-launch workgroup): ys against the oracle's shared expert (bf16 gate/up, model.py:409-412),
+    the routed part unchanged bit for bit, out = bf16(routed + ys) exactly, and ys close to the standalone launches'."""
+    from dsv41_amd import moe, quant
+    E, H, I, ws, ex = full_layer
+    assert moe.fused_shared_ok(M, 8, I)
+    g = torch.Generator(device=DEV).manual_seed(880 + M)
+    Ws13 = (torch.randn(2 * I, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16)
+    Ws2 = (torch.randn(H, I, generator=g, device=DEV) / I ** 0.5).to(torch.bfloat16)
+    eid, wt = rand_routing(M, E, 8, 881 + M)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 882 + M).to(DEV))
+    ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    y32 = torch.empty(M, H, device=DEV)
+    ys = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    sh = moe.SharedExpert.prepare(Ws13, Ws2, tiled=tiled)
+    moe.moe_experts(xq, ed, wd, ex, 10.0, out=out, y32=y32, shared=sh, ys_out=ys)
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    ys_ref = O.shared_expert(bf16_vals(xq), u16(Ws13), u16(Ws2), I, 10.0)
+    close(bf16_vals(ys), ys_ref, f"fused shared expert M={M}")
+    y_plain = moe.moe_experts(xq, ed, wd, ex, 10.0).clone()
+    assert torch.equal(y32, y_plain), "the routed sum changed with the shared expert fused in"
+    comp = O.f32_to_bf16_bits((y32.cpu().numpy() + bf16_vals(ys)).astype(np.float32))
+    assert np.array_equal(u16(out), comp)
+    ys_alone = moe.shared_expert(xq, sh.w13, sh.w2, 10.0, tiled=tiled).clone()
+    close(bf16_vals(ys), bf16_vals(ys_alone), f"fused vs standalone shared expert M={M}")
+    close(bf16_vals(ys_alone), ys_ref, f"standalone shared expert (tiled={tiled}) M={M}")
+    W13, S13, W2, S2 = host_subset(ws, set(eid.reshape(-1).tolist()))
+    ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, W13, S13, W2, S2, I, 10.0)
+    close(y32.cpu().numpy(), ref, f"routed part with the shared expert fused M={M}")

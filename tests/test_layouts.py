@@ -1,0 +1,20 @@
+"""Host-side weight layouts (CPU, torch): the bf16 tile layout of the shared expert is a permutation with the
+documented index formula, and untile inverts it."""
+import torch
+
+from dsv41_amd import quant
+
+
+def test_tile_bf16_index_formula_and_round_trip():
+    N, K = 48, 96
+    w = torch.arange(N * K, dtype=torch.float32).reshape(N, K).to(torch.bfloat16)   # exact up to 256: use the bits below
+    bits = torch.arange(N * K, dtype=torch.int32).reshape(N, K).to(torch.int16).view(torch.bfloat16)
+    t = quant.tile_bf16(bits)
+    flat = t.view(torch.int16).reshape(-1)
+    src = bits.view(torch.int16)
+    # element (n, k) sits in tile (n / 16, k / 32) at row n % 16, column k % 32
+    for n, k in [(0, 0), (5, 31), (16, 32), (47, 95), (20, 70)]:
+        off = ((n // 16) * (K // 32) + k // 32) * 512 + (n % 16) * 32 + k % 32
+        assert flat[off] == src[n, k]
+    assert torch.equal(quant.untile_bf16(t).view(torch.int16), src)
+    assert torch.equal(quant.untile_bf16(quant.tile_bf16(w)), w)
