@@ -173,3 +173,64 @@ extern "C" int dsv41_router_logits(const uint16_t* x, long long ldx, const uint1
     router_norm_kernel<<<dim3(E / 16, H / RT_KC), RT_THREADS, 0, (hipStream_t)stream>>>(a);
     return (int)hipGetLastError();
 }
+
+// ------------------------------------------------------------------------------------------ fp32 router weights
+// Router logits with fp32 router weights (model.MoE.gate: F.linear(x.float(), gate_w) with gate_w fp32, model.py:368,
+// 392), for M <= 16 bf16 rows, split along K like the kernel above: part[ks][t][e] = sum over k in [1024 ks, +1024)
+// of x[t][k] * G[e][k]. fp32 MFMA 16x16x4: in one product lane l holds row e0 + l % 16 and token l % 16 at k-group
+// g = l / 16. Each lane loads 16 bytes (4 consecutive k) of its row per 16-k block and uses them in 4 products
+// (product i takes k = 16 j + 4 g + i), with the matching activations from LDS, so every weight load is a full
+// 16-byte vector and each wave-load covers 16 rows x 64 contiguous bytes.
+#define RF_THREADS 256
+__global__ void __launch_bounds__(RF_THREADS) router_f32w_kernel(const uint16_t* __restrict__ x, long long ldx, const float* __restrict__ G,
+                                                                 long long ldg, int E, int M, float* __restrict__ part) {
+    __shared__ __align__(16) uint16_t s_x[RT_MAXM][RT_KC + 8];   // this workgroup's k range of the M rows, bf16
+    __shared__ v4f s_acc[RF_THREADS / 64][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.x, ks = blockIdx.y;
+    const int k0 = ks * RT_KC;
+    const int col = lane & 15, kg = lane >> 4;
+    // the wave's 16 blocks of 16 k: all 16 weight loads in flight at once
+    const int kw = k0 + wave * (RT_KC / (RF_THREADS / 64));
+    const float* wr = G + ((long long)rb * 16 + col) * ldg + kw + 4 * kg;
+    v4f A[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) A[j] = __builtin_nontemporal_load((const v4f*)(wr + 16 * j));
+    // stage the activations (16 bytes per thread per step; rows past M are not read)
+    for (int i = tid; i < M * (RT_KC / 8); i += RF_THREADS) {
+        const int t = i / (RT_KC / 8), v = i - t * (RT_KC / 8);
+        *(v4i*)&s_x[t][v * 8] = *(const v4i*)(x + (long long)t * ldx + k0 + v * 8);
+    }
+    __syncthreads();
+    const uint16_t* xr = &s_x[col < M ? col : 0][wave * (RT_KC / (RF_THREADS / 64)) + 4 * kg];
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint2 xb = *(const uint2*)(xr + 16 * j);
+        const float b[4] = {bf16_to_f32(xb.x & 0xFFFFu), bf16_to_f32(xb.x >> 16), bf16_to_f32(xb.y & 0xFFFFu), bf16_to_f32(xb.y >> 16)};
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[j].x, b[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[j].y, b[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[j].z, b[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[j].w, b[3], acc, 0, 0, 0);
+    }
+    s_acc[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && col < M) {
+        v4f sum = s_acc[0][lane];
+#pragma unroll
+        for (int w = 1; w < RF_THREADS / 64; ++w) sum += s_acc[w][lane];
+        // lane l holds D[4 (l / 16) + i][l % 16]: rows = experts, column = token
+        float* o = part + ((long long)ks * M + col) * E + rb * 16 + 4 * kg;
+        o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
+    }
+}
+
+extern "C" int dsv41_router_logits_f32w(const uint16_t* x, long long ldx, const float* G, long long ldg, int E, int H, int M, float* part,
+                                        void* stream) {
+    if (!x || !G || !part || M < 1 || M > RT_MAXM || E <= 0 || (E & 15) || H <= 0 || (H % RT_KC) || ldx < H || ldg < H || (ldx & 7) ||
+        (ldg & 3) || (((uintptr_t)x) & 15) || (((uintptr_t)G) & 15))
+        return DSV41_EINVAL;
+    router_f32w_kernel<<<dim3(E / 16, H / RT_KC), RF_THREADS, 0, (hipStream_t)stream>>>(x, ldx, G, ldg, E, M, part);
+    return (int)hipGetLastError();
+}

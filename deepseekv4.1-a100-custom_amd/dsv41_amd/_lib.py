@@ -38,6 +38,7 @@ SIGNATURES = {
     "dsv41_dense_gemv_bf16": [P, LL, I, I, I, P, LL, I, P, LL, P, LL, P],
     "dsv41_residual_rmsnorm_quant": [P, LL, P, LL, P, F, I, I, P, LL, P, LL, P],
     "dsv41_gate_topk": [P, LL, P, I, I, F, I, F, I, I, P, P, I, LL, P],
+    "dsv41_router_logits_f32w": [P, LL, P, LL, I, I, I, P, P],
     "dsv41_router_logits": [P, LL, P, LL, P, F, P, LL, I, I, I, P, P, LL, P, LL, P],
     "dsv41_moe_dispatch": [P, P, I, I, I, I, P, P, P, P, P, P, P],
     "dsv41_moe_experts_noalloc": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, P, LL, P, LL, I, I, I, F, P, P, P, LL, P, LL,

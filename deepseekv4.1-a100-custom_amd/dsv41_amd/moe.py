@@ -440,3 +440,115 @@ class MoEDecodeLayer:
     @property
     def last_routing(self):
         return {M: (v["eid"], v["wt"]) for M, v in self._bufs.items()}
+
+
+# --------------------------------------------------------------------------- the whole MoE layer (eager / prefill)
+def router_logits_f32w(x: torch.Tensor, G: torch.Tensor, part: torch.Tensor | None = None) -> torch.Tensor:
+    """Router logits with fp32 router weights G [E, H] for M <= 16 bf16 rows x (F.linear(x.float(), gate_w),
+    model.py:392): fp32 [H / 1024, M, E] partial sums over k ranges of 1024, which gate_topk / moe_route_experts add
+    in part order."""
+    dev = _lib.require_cuda(x, G, part)
+    M, H = x.shape
+    E = G.shape[0]
+    assert x.dtype == torch.bfloat16 and G.dtype == torch.float32 and G.shape[1] == H and G.stride(1) == 1 and x.stride(1) == 1
+    part = torch.empty(H // 1024, M, E, dtype=torch.float32, device=dev) if part is None else part
+    assert part.shape == (H // 1024, M, E) and part.is_contiguous()
+    _lib.call("dsv41_router_logits_f32w", _lib.ptr(x), x.stride(0), _lib.ptr(G), G.stride(0), E, H, M, _lib.ptr(part), _lib.stream(dev))
+    return part
+
+
+class MoE:
+    """The expert compute of the reference's model.MoE (model.py:354-413, 554-591) for one layer on the GPU path:
+    gate (fp32 router weights, softmax / sigmoid / sqrt(softplus), + bias for the selection, top-k, renormalised and
+    scaled), x fake-quantised to FP8 (model.py:565), the routed FP4 experts, the bf16 shared expert, and
+    y = bf16(sum_j w_j y2_j + shared) (model.py:589-591).
+      * <= 16 tokens (decode): the router GEMV on fp32 weights as split-K partial sums, then the two fused decode
+        launches (routing inside the up launch for one token; the shared expert rides in both launches when it fits
+        them, else runs as its own launches first);
+      * > 16 tokens (prefill): router logits and the shared expert's two products as plain library GEMMs (F.linear on
+        the GPU, as the reference runs them, model.py:392, 410-412; w8.py:102-103), gate_topk, then the prefill grouped
+        GEMMs with the slot-ordered combine.
+    Attribute names follow the reference (n_experts, topk, score_func, gate_temp, norm_topk_prob, route_scale,
+    swiglu_limit, gate_w, gate_bias, inter, sh_w13, sh_w2). Routing of the last call: last_routing."""
+
+    def __init__(self, experts: ExpertWeights, gate_w: torch.Tensor, gate_bias: torch.Tensor | None = None, topk: int = 8,
+                 score_func: str = "softmax", route_scale: float = 1.0, norm_topk_prob: bool = True, gate_temp: float = 1.0,
+                 swiglu_limit: float = 0.0, sh_w13: torch.Tensor | None = None, sh_w2: torch.Tensor | None = None,
+                 shared_tiled: bool = True):
+        experts.check()
+        self.ex = experts
+        self.n_experts, self.dim, self.inter = experts.E, experts.H, experts.I
+        self.topk, self.score_func, self.gate_temp = topk, score_func, float(gate_temp)
+        self.norm_topk_prob, self.route_scale, self.swiglu_limit = norm_topk_prob, float(route_scale), float(swiglu_limit)
+        self.gate_w = gate_w.to(torch.float32).contiguous()                       # fp32 [E, dim] (model.py:368)
+        assert self.gate_w.shape == (self.n_experts, self.dim)
+        self.gate_bias = None if gate_bias is None else gate_bias.to(torch.float32).contiguous()
+        self.sh_w13 = None if sh_w13 is None else sh_w13.to(torch.bfloat16).contiguous()   # [w1; w3] row-major (prefill GEMMs)
+        self.sh_w2 = None if sh_w2 is None else sh_w2.to(torch.bfloat16).contiguous()
+        # the decode kernels stream the shared expert in the tile_bf16 layout (repacked once)
+        self.shared = SharedExpert.prepare(self.sh_w13, self.sh_w2, tiled=shared_tiled) if self.sh_w13 is not None else None
+        self._bufs: dict = {}
+        self.last_routing = None
+
+    def _norm(self) -> bool:
+        return self.norm_topk_prob and self.topk > 1
+
+    def gate(self, x: torch.Tensor):
+        """(weights fp32 [T, topk], indices int32 [T, topk]) as model.MoE.gate (model.py:391-404)."""
+        from .fused2 import gate_topk
+        T = x.shape[0]
+        if T <= 16:
+            scores = router_logits_f32w(x.to(torch.bfloat16).contiguous(), self.gate_w)
+        else:
+            scores = torch.nn.functional.linear(x.float(), self.gate_w)
+        eid, wt = gate_topk(scores, self.gate_bias, self.gate_temp, self.topk, self.route_scale, self.score_func, self._norm(),
+                            eid=torch.empty(T, self.topk, dtype=torch.int32, device=x.device),
+                            wt=torch.empty(T, self.topk, dtype=torch.float32, device=x.device))
+        return wt, eid
+
+    def shared_expert(self, x: torch.Tensor) -> torch.Tensor:
+        """fp32 [T, dim] = linear_w(swiglu_quant(linear_fp8(x, sh_w13)), sh_w2) (model.py:409-412)."""
+        from .fused import swiglu_quant
+        from .quant import fake_quant_fp8
+        xq = fake_quant_fp8(x.to(torch.bfloat16))
+        if x.shape[0] <= 16:
+            return shared_expert(xq.contiguous(), self.shared.w13, self.shared.w2, self.swiglu_limit, tiled=self.shared.tiled).float()
+        gu = torch.nn.functional.linear(xq, self.sh_w13)
+        return torch.nn.functional.linear(swiglu_quant(gu, None, self.inter, self.swiglu_limit), self.sh_w2).float()
+
+    def _buf(self, dev, T):
+        b = self._bufs.get(T)
+        if b is None:
+            H, E, k = self.dim, self.n_experts, self.topk
+            b = self._bufs[T] = {"xq": torch.empty(T, H, dtype=torch.bfloat16, device=dev), "out": torch.empty(T, H, dtype=torch.bfloat16, device=dev),
+                                 "part": torch.empty(H // 1024, T, E, dtype=torch.float32, device=dev),
+                                 "eid": torch.empty(T, k, dtype=torch.int32, device=dev), "wt": torch.empty(T, k, dtype=torch.float32, device=dev)}
+        return b
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.size()
+        x2 = x.reshape(-1, self.dim)
+        if x2.dtype != torch.bfloat16 or not x2.is_contiguous():
+            x2 = x2.to(torch.bfloat16).contiguous()
+        dev = _lib.require_cuda(x2)
+        T, H = x2.shape
+        if T <= 16:
+            b = self._buf(dev, T)
+            _lib.call("dsv41_quant_fp8", _lib.ptr(x2), 0, T, H, x2.stride(0), 0, None, None, _lib.ptr(b["xq"]), _lib.stream(dev))
+            router_logits_f32w(x2, self.gate_w, part=b["part"])
+            moe_route_experts(b["xq"], b["part"], self.gate_bias, self.gate_temp, self.topk, self.route_scale, self.score_func, self._norm(),
+                              self.ex, self.swiglu_limit, out=b["out"], eid_out=b["eid"], wt_out=b["wt"], shared=self.shared)
+            self.last_routing = (b["eid"], b["wt"])
+            return b["out"].view(shape)
+        from .fused import swiglu_quant
+        from .quant import fake_quant_fp8
+        wt, eid = self.gate(x2)
+        xq = fake_quant_fp8(x2)
+        ys = None
+        if self.sh_w13 is not None:
+            ys = torch.nn.functional.linear(swiglu_quant(torch.nn.functional.linear(xq, self.sh_w13), None, self.inter, self.swiglu_limit),
+                                            self.sh_w2)
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        prefill_experts(xq, eid, wt, self.ex, self.swiglu_limit, ys=ys, out=out)
+        self.last_routing = (eid, wt)
+        return out.view(shape)

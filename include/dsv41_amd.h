@@ -145,6 +145,13 @@ int dsv41_router_logits(const uint16_t* x, long long ldx, const uint16_t* y, lon
                         const uint16_t* G, long long ldg, int E, int H, int M, float* part, uint16_t* xn, long long ldn,
                         uint16_t* xq, long long ldq, void* stream);
 
+/* Router logits with fp32 router weights (model.MoE.gate: F.linear(x.float(), gate_w), gate_w fp32 [E][ldg],
+ * model.py:368, 392) for M <= 16 bf16 rows x [M][ldx]: KS = H / 1024 partial sums part [KS][M][E] (k ranges of 1024,
+ * ascending), which dsv41_gate_topk / dsv41_moe_decode_up add in part order (nparts = KS, part_stride = M * E).
+ * H % 1024 == 0, E % 16 == 0. */
+int dsv41_router_logits_f32w(const uint16_t* x, long long ldx, const float* G, long long ldg, int E, int H, int M, float* part,
+                             void* stream);
+
 /* MoE gate on logits: score_func 0 sqrt(softplus), 1 sigmoid, 2 softmax; top-k of scores + bias (lowest index
  * wins ties); weights renormalised when norm, times route_scale. fused2.gate_topk (fused2.py:418-471),
  * model.MoE.gate (model.py:391-404). nparts > 1: scores are that many partial sums part_stride floats apart

@@ -726,3 +726,43 @@ def test_decode_fused_shared_expert(full_layer, M, tiled):
     W13, S13, W2, S2 = host_subset(ws, set(eid.reshape(-1).tolist()))
     ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, W13, S13, W2, S2, I, 10.0)
     close(y32.cpu().numpy(), ref, f"routed part with the shared expert fused M={M}")
+
+
+@pytest.mark.parametrize("T", [1, 3, 40])
+def test_moe_layer_class(T):
+    """model.MoE.__call__'s surface (moe.MoE): fp32 router weights, sigmoid gate with bias and route scale, FP8 x, routed
+    experts, bf16 shared expert, bf16 output, for one token (shared expert fused into the decode launches), three tokens
+    (decode, shared expert as its own launches) and 40 tokens (prefill path). Routing against the oracle gate on fp64
+    logits; the output against the oracle layer on the same routing (bf16 output: the spec tolerance plus one bf16
+    rounding step)."""
+    from dsv41_amd import moe
+    E, H, I, k = 32, 1024, 384, 4
+    ws = make_experts(E, H, I, 1200 + T)
+    ex = to_ex(*ws, True)
+    g = torch.Generator(device=DEV).manual_seed(1300 + T)
+    gate_w = torch.randn(E, H, generator=g, device=DEV) / H ** 0.5
+    bias = torch.randn(E, generator=g, device=DEV) * 0.05
+    Ws13 = (torch.randn(2 * I, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16)
+    Ws2 = (torch.randn(H, I, generator=g, device=DEV) / I ** 0.5).to(torch.bfloat16)
+    layer = moe.MoE(ex, gate_w, bias, topk=k, score_func="sigmoid", route_scale=2.5, swiglu_limit=10.0, sh_w13=Ws13, sh_w2=Ws2)
+    x = (rand_x(T, H, 1400 + T) * 2).to(DEV)
+    y = layer(x).clone()
+    eid, wt = [t.cpu().numpy() for t in layer.last_routing]
+    logits = (bf16_vals(x).astype(np.float64) @ gate_w.cpu().double().numpy().T).astype(np.float32)
+    ref_i, ref_w = O.gate_topk(logits, bias.cpu().numpy(), 1.0, k, 2.5, "sigmoid", True)
+    assert np.array_equal(eid, ref_i)
+    assert np.allclose(wt, ref_w, rtol=1e-4, atol=1e-6)
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    ids = set(eid.reshape(-1).tolist())
+    W13, S13, W2, S2 = host_subset(ws, ids)
+    ref = O.moe_layer(bf16_vals(x), eid, wt, W13, S13, W2, S2, u16(Ws13), u16(Ws2), I, 10.0)
+    got = bf16_vals(y)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    print(f"MoE T={T}: rel L2 {O.rel_l2(got, ref):.2e}")
+    assert O.rel_l2(got, ref) <= RTOL_L2
+    assert np.all(np.abs(got - ref) <= MAXABS_RMS * rms + np.abs(ref) * 2.0 ** -7)
+    xs = O.fake_quant_fp8(bf16_vals(x))
+    close(layer.shared_expert(x).cpu().numpy(), O.shared_expert(xs, u16(Ws13), u16(Ws2), I, 10.0), f"MoE.shared_expert T={T}")
+    # the gate entry point on its own
+    w2_, i2_ = layer.gate(x)
+    assert np.array_equal(i2_.cpu().numpy(), ref_i)
