@@ -193,7 +193,8 @@ __global__ void __launch_bounds__(RF_THREADS) router_f32w_kernel(const uint16_t*
     const int col = lane & 15, kg = lane >> 4;
     // the wave's 16 blocks of 16 k: all 16 weight loads in flight at once
     const int kw = k0 + wave * (RT_KC / (RF_THREADS / 64));
-    const float* wr = G + ((long long)rb * 16 + col) * ldg + kw + 4 * kg;
+    // rows past E (the last block when E % 16 != 0) read row E - 1; their outputs are not stored
+    const float* wr = G + (long long)min(rb * 16 + col, E - 1) * ldg + kw + 4 * kg;
     v4f A[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) A[j] = __builtin_nontemporal_load((const v4f*)(wr + 16 * j));
@@ -222,15 +223,18 @@ __global__ void __launch_bounds__(RF_THREADS) router_f32w_kernel(const uint16_t*
         for (int w = 1; w < RF_THREADS / 64; ++w) sum += s_acc[w][lane];
         // lane l holds D[4 (l / 16) + i][l % 16]: rows = experts, column = token
         float* o = part + ((long long)ks * M + col) * E + rb * 16 + 4 * kg;
-        o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (rb * 16 + 4 * kg + i < E) o[i] = v[i];
     }
 }
 
 extern "C" int dsv41_router_logits_f32w(const uint16_t* x, long long ldx, const float* G, long long ldg, int E, int H, int M, float* part,
                                         void* stream) {
-    if (!x || !G || !part || M < 1 || M > RT_MAXM || E <= 0 || (E & 15) || H <= 0 || (H % RT_KC) || ldx < H || ldg < H || (ldx & 7) ||
+    if (!x || !G || !part || M < 1 || M > RT_MAXM || E <= 0 || H <= 0 || (H % RT_KC) || ldx < H || ldg < H || (ldx & 7) ||
         (ldg & 3) || (((uintptr_t)x) & 15) || (((uintptr_t)G) & 15))
         return DSV41_EINVAL;
-    router_f32w_kernel<<<dim3(E / 16, H / RT_KC), RF_THREADS, 0, (hipStream_t)stream>>>(x, ldx, G, ldg, E, M, part);
+    router_f32w_kernel<<<dim3((E + 15) / 16, H / RT_KC), RF_THREADS, 0, (hipStream_t)stream>>>(x, ldx, G, ldg, E, M, part);
     return (int)hipGetLastError();
 }

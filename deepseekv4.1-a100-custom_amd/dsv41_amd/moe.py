@@ -115,11 +115,13 @@ class _Workspace:
 
 
 def fused_shared_ok(M: int, k: int, I: int) -> bool:
-    """Whether the bf16 shared expert can ride in the two decode launches (dsv41_moe_down_sum's LDS rule: the h rows,
-    their scales and M bf16 h_s rows in 60 KiB, M I <= 4096); otherwise it runs as its own launches."""
+    """Whether the bf16 shared expert can ride in the two decode launches (dsv41_moe_down_sum's limits: the h rows,
+    their scales and M bf16 h_s rows in 60 KiB with at most 4 h vectors per thread, M I <= 4096, I / 32 <= 56 chunks);
+    otherwise it runs as its own launches."""
     P = M * k
     lds = (((P + 1) * (I + 16) + (P + 1) * (I // 32) + 15) & ~15) + M * (I + 8) * 2
-    return lds <= 60 * 1024 and (P + 1) * (I // 16) <= 8 * 512 and (P + 1) * (I // 32) <= 4 * 512 and M * I <= 4096 and P <= 256
+    return (lds <= 60 * 1024 and (P + 1) * (I // 16) <= 4 * 512 and (P + 1) * (I // 32) <= 2 * 512 and M * I <= 4096 and P <= 256
+            and I // 32 <= 7 * 8)
 
 
 _WS: dict = {}

@@ -148,7 +148,7 @@ int dsv41_router_logits(const uint16_t* x, long long ldx, const uint16_t* y, lon
 /* Router logits with fp32 router weights (model.MoE.gate: F.linear(x.float(), gate_w), gate_w fp32 [E][ldg],
  * model.py:368, 392) for M <= 16 bf16 rows x [M][ldx]: KS = H / 1024 partial sums part [KS][M][E] (k ranges of 1024,
  * ascending), which dsv41_gate_topk / dsv41_moe_decode_up add in part order (nparts = KS, part_stride = M * E).
- * H % 1024 == 0, E % 16 == 0. */
+ * H % 1024 == 0. */
 int dsv41_router_logits_f32w(const uint16_t* x, long long ldx, const float* G, long long ldg, int E, int H, int M, float* part,
                              void* stream);
 
