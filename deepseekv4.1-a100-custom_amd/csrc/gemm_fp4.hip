@@ -184,6 +184,10 @@ struct DownSumArgs {
     // bf16(h_s . Ws2[rows]^T) (Ws2 bf16 [N][ldws2]) to y before the bf16 rounding; ys_out (optional) receives it
     const uint16_t* gus; long long ldgus; const uint16_t* Ws2; long long ldws2; float limit; uint16_t* ys_out; long long ldyso;
     int sh_tiled;   // Ws2 in 16 x 32 tiles of 1 KiB ([N/16][K/32][16][32], ldws2 = K) instead of row-major
+    // optional hyper-connection post mix in the epilogue (fused2.hc_post2_, fused2.py:476-508): with x = bf16(y + ys),
+    // each of the 4 residual streams r_i (bf16, token t's streams at hres + 4 N t + N i) <- bf16(post[t][i] x +
+    // sum_j comb[t][j][i] r_j), in place (post fp32 [M][4], comb fp32 [M][4][4])
+    uint16_t* hres; const float* hpost; const float* hcomb;
 };
 
 #define DS_MAX_SLOTS 256
@@ -580,9 +584,10 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
         float* o = a.y + (long long)col * a.ldy + row0;
         o[0] = sum.x; o[1] = sum.y; o[2] = sum.z; o[3] = sum.w;
     }
-    if (a.yb || (SH && a.ys_out)) {
+    if (a.yb || a.hres || (SH && a.ys_out)) {
         const float v[4] = {sum.x, sum.y, sum.z, sum.w};
         const float sv[4] = {ssum.x, ssum.y, ssum.z, ssum.w};
+        float xo[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float t = v[i];
@@ -593,7 +598,34 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
             } else if (a.ys) {
                 t += bf16_to_f32(a.ys[(long long)col * a.ldys + row0 + i]);
             }
-            if (a.yb) a.yb[(long long)col * a.ldyb + row0 + i] = (uint16_t)f32_to_bf16_bits(t);
+            const uint32_t tb = f32_to_bf16_bits(t);
+            xo[i] = bf16_to_f32(tb);
+            if (a.yb) a.yb[(long long)col * a.ldyb + row0 + i] = (uint16_t)tb;
+        }
+        if (a.hres) {
+            // the post mix for this lane's 4 columns of token col: all 4 streams read before any is written
+            uint16_t* r = a.hres + (long long)col * 4 * a.N + row0;
+            const float* pb = a.hpost + col * 4;
+            const float* cb = a.hcomb + col * 16;
+            float rv[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 u = *(const uint2*)(r + (long long)j * a.N);
+                rv[j][0] = bf16_to_f32(u.x & 0xFFFFu); rv[j][1] = bf16_to_f32(u.x >> 16);
+                rv[j][2] = bf16_to_f32(u.y & 0xFFFFu); rv[j][3] = bf16_to_f32(u.y >> 16);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                uint32_t o[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float acc = pb[s] * xo[c];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc = fmaf(cb[j * 4 + s], rv[j][c], acc);
+                    o[c] = f32_to_bf16_bits(acc);
+                }
+                *(uint2*)(r + (long long)s * a.N) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+            }
         }
     }
 }
@@ -641,8 +673,10 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                                   const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                                   float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                                   int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
-                                  long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, void* stream) {
-    if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb && !ys_out)) return DSV41_EINVAL;
+                                  long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, uint16_t* hres,
+                                  const float* hpost, const float* hcomb, void* stream) {
+    if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb && !ys_out && !hres)) return DSV41_EINVAL;
+    if (hres && (!hpost || !hcomb || (((uintptr_t)hres) & 7))) return DSV41_EINVAL;
     // the fused shared expert: its gate/up (bf16 [M][ldgus], 2 K columns) and Ws2 (bf16 [N][ldws2], 16-byte row pieces,
     // 16-row blocks addressed with 32-bit offsets); it replaces a given ys
     const bool sh = Ws2 != nullptr;
@@ -650,7 +684,7 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                (ldgus & 7) || (((uintptr_t)gus) & 15) || (sh_tiled && ldws2 != K) || (long long)M * 4 * K > 16LL * DS_WAVES * 64 * DS_GUV ||
                (long long)M * 4 * K > (long long)sizeof(v4f) * 2 * DS_WAVES * 64 || (ys_out && ldyso < N)))
         return DSV41_EINVAL;
-    if (!sh && !y && !yb) return DSV41_EINVAL;
+    if (!sh && !y && !yb && !hres) return DSV41_EINVAL;
     // zero_row is kept in the kernel's 16-bit pair table
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0 || zero_row > 32767)
         return DSV41_EINVAL;
@@ -661,7 +695,8 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     if ((ldh & 15) || (((uintptr_t)hc) & 15) || ldh < K || ldhs < K / 32) return DSV41_EINVAL;
     if ((y && ldy < N) || (yb && ldyb < N) || (yb && ys && ldys < N)) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
-                  y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, gus, ldgus, Ws2, ldws2, limit, ys_out, ldyso, sh_tiled};
+                  y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, gus, ldgus, Ws2, ldws2, limit, ys_out, ldyso, sh_tiled,
+                  hres, hpost, hcomb};
     hipStream_t st = (hipStream_t)stream;
     // dynamic LDS: the h rows (codes, then their E8M0 bytes) and, with the shared expert, its bf16 h_s rows
     const size_t lds_h = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);

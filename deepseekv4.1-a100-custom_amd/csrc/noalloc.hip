@@ -86,5 +86,5 @@ extern "C" int dsv41_moe_experts_noalloc(const float* logits, long long ldl, int
     r = (int)hipGetLastError();
     if (r) return r;
     return dsv41_moe_down_sum(W2, stride_w2, S2, stride_s2, tiled, H, I, hc, I, hs, I / 32, P, grp_expert, grp_start, tok_sorted, P, M, y, ldy,
-                              ys, ldys, yb, ldyb, 0, E, nullptr, 0, nullptr, 0, 0, 0.f, nullptr, 0, stream);
+                              ys, ldys, yb, ldyb, 0, E, nullptr, 0, nullptr, 0, 0, 0.f, nullptr, 0, nullptr, nullptr, nullptr, stream);
 }

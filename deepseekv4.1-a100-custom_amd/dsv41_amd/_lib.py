@@ -31,7 +31,8 @@ SIGNATURES = {
     "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
     "dsv41_moe_decode_up": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P,
                             P, LL, I, P, LL, P],
-    "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, LL, P, LL, I, F, P, LL, P],
+    "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, LL, P, LL, I, F, P, LL,
+                           P, P, P, P],
     "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],
     "dsv41_prefill_down": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, LL, P],
     "dsv41_combine_pairs": [P, LL, P, I, I, I, P, LL, P, LL, P, LL, P],
@@ -39,6 +40,8 @@ SIGNATURES = {
     "dsv41_residual_rmsnorm_quant": [P, LL, P, LL, P, F, I, I, P, LL, P, LL, P],
     "dsv41_gate_topk": [P, LL, P, I, I, F, I, F, I, I, P, P, I, LL, P],
     "dsv41_router_logits_f32w": [P, LL, P, LL, I, I, I, P, P],
+    "dsv41_hc_pre_norm_quant": [P, LL, I, P, LL, P, F, I, I, P, LL, P, LL, P, LL, P, LL, P],
+    "dsv41_hc_post": [P, LL, P, LL, LL, I, P, LL, P, LL, P, LL, P, LL, I, I, P],
     "dsv41_router_logits": [P, LL, P, LL, P, F, P, LL, I, I, I, P, P, LL, P, LL, P],
     "dsv41_moe_dispatch": [P, P, I, I, I, I, P, P, P, P, P, P, P],
     "dsv41_moe_experts_noalloc": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, P, LL, P, LL, I, I, I, F, P, P, P, LL, P, LL,

@@ -182,14 +182,22 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
     return ws
 
 
-def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, limit: float = 0.0, ys_out=None):
+def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, limit: float = 0.0, ys_out=None, hc=None):
     """The second decode launch (dsv41_moe_down_sum): y[t] = sum over t's groups of h . deq(W2[e])^T (fp32, into
     y32 or the workspace) and/or out = bf16(y + ys). When decode_up ran with the shared expert, this launch finishes it
-    (SwiGLU with `limit`, Ws2) and adds its bf16 output instead of `ys` (ys_out, bf16 [M, H], receives it)."""
+    (SwiGLU with `limit`, Ws2) and adds its bf16 output instead of `ys` (ys_out, bf16 [M, H], receives it).
+    hc = (residual bf16 [M, 1, 4, H], post fp32 [M, 4], comb fp32 [M, 4, 4]): the hyper-connection post mix
+    (fused2.hc_post2_) applied to bf16(y + ys) in the same launch, in place on residual."""
     dev = _lib.require_cuda(ws.hc, ys, out, y32, ys_out)
+    hres = hpost = hcomb = None
+    if hc is not None:
+        hres, hpost, hcomb = hc
+        assert hres.dtype == torch.bfloat16 and hres.is_contiguous() and hres.numel() == ws.M * 4 * ex.H
+        hpost = hpost.reshape(ws.M, 4).to(torch.float32).contiguous()
+        hcomb = hcomb.reshape(ws.M, 16).to(torch.float32).contiguous()
     M, H = ws.M, ex.H
     y = ws.y if y32 is None else y32
-    want_y = out is None or y32 is not None
+    want_y = (out is None and hc is None) or y32 is not None
     Ws2 = None
     if ws.shared is not None:
         Ws2 = ws.shared.w2
@@ -199,7 +207,10 @@ def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, 
               _lib.ptr(ws.tok_sorted), ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
               _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.ptr(ws.gus) if Ws2 is not None else None, ws.gus.stride(0),
               _lib.ptr(Ws2), ex.I if Ws2 is None else Ws2.stride(0), 1 if Ws2 is not None and ws.shared.tiled else 0, float(limit),
-              _lib.ptr(ys_out), H if ys_out is None else ys_out.stride(0), _lib.stream(dev))
+              _lib.ptr(ys_out), H if ys_out is None else ys_out.stride(0), _lib.ptr(hres), _lib.ptr(hpost), _lib.ptr(hcomb),
+              _lib.stream(dev))
+    if hc is not None and out is None:
+        return hres
     return out if out is not None else y
 
 
@@ -217,24 +228,26 @@ def _shared_plan(xq, shared, ys, k, ex, limit, ys_out):
 
 def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float,
                 ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None,
-                shared: tuple | None = None, ys_out: torch.Tensor | None = None) -> torch.Tensor:
+                shared: tuple | None = None, ys_out: torch.Tensor | None = None, hc: tuple | None = None) -> torch.Tensor:
     """Routed experts of one layer for M <= 16 tokens with given routing.
     xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int [M, k] (distinct per token); wt fp32 [M, k].
     Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
     or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None);
     y32 (fp32 [M, H]) additionally receives y. shared (a SharedExpert, or a row-major (w13, w2) bf16 pair) computes
     the shared expert too (model.py:409-412) instead of taking ys: in the same two launches when it fits them
-    (fused_shared_ok), else as its own launches first; ys_out (bf16 [M, H]) receives its output."""
+    (fused_shared_ok), else as its own launches first; ys_out (bf16 [M, H]) receives its output. hc = (residual, post,
+    comb) applies the hyper-connection post mix to bf16(y + ys) in the same launch (decode_down)."""
     k = eid.shape[-1]
     fused, ys = _shared_plan(xq, shared, ys, k, ex, limit, ys_out)
     ws = decode_up(xq, ex, limit, k, eid=eid, wt=wt, shared=fused)
-    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None)
+    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None, hc=hc)
 
 
 def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None, temp: float, topk: int, route_scale: float,
                       score_func: str, norm: bool, ex: ExpertWeights, limit: float, ys: torch.Tensor | None = None,
                       out: torch.Tensor | None = None, y32: torch.Tensor | None = None, eid_out: torch.Tensor | None = None,
-                      wt_out: torch.Tensor | None = None, shared: tuple | None = None, ys_out: torch.Tensor | None = None) -> torch.Tensor:
+                      wt_out: torch.Tensor | None = None, shared: tuple | None = None, ys_out: torch.Tensor | None = None,
+                      hc: tuple | None = None) -> torch.Tensor:
     """gate_topk (fused2.py:418-452) with the routed experts: logits fp32 [M, E] -> routing (written to
     eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts.
     M = 1: the routing runs inside the up-projection launch (every workgroup routes the one token while its
@@ -252,7 +265,7 @@ def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor
         wt = ws0.wt if wt_out is None else wt_out
         gate_topk(logits, bias, temp, topk, route_scale, score_func, norm, eid=eid, wt=wt)
         ws = decode_up(xq, ex, limit, topk, eid=eid, wt=wt, shared=fused)
-    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None)
+    return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None, hc=hc)
 
 
 # --------------------------------------------------------------------------- dense bf16 (shared expert, router)

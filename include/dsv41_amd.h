@@ -90,13 +90,17 @@ int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long lon
  * (dsv41_moe_decode_up's bf16 gate/up [M][ldgus]) each workgroup forms h_s = swiglu_quant(gus, no weight, limit)
  * (model.py:410) and adds ys = bf16(h_s . Ws2^T) (linear_w(hs, sh_w2), decode.py:370) to y before the bf16 rounding
  * of yb; ys_out (bf16 [M][ldyso], optional) receives ys. Needs the h rows and h_s in 60 KiB of LDS
- * ((n_slots + 1)(K + 16 + K / 32) + 2 M (K + 8) bytes, e.g. M <= 2 at K = 1664) and M K <= 4096; else -1. */
+ * ((n_slots + 1)(K + 16 + K / 32) + 2 M (K + 8) bytes, e.g. M <= 2 at K = 1664) and M K <= 4096; else -1.
+ * Optional hyper-connection post mix in the same epilogue (hres bf16 residual, token t's 4 streams at hres + 4 N t + N i;
+ * hpost fp32 [M][4]; hcomb fp32 [M][4][4]; or NULL): r_i <- bf16(post[t][i] x + sum_j comb[t][j][i] r_j) with
+ * x = bf16(y + ys), in place (fused2.hc_post2_, fused2.py:476-508), replacing its separate launch. */
 int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
                        int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                        const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                        float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                        int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
-                       long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, void* stream);
+                       long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, uint16_t* hres,
+                       const float* hpost, const float* hcomb, void* stream);
 
 /* Prefill w13 + SwiGLU: for every group g of <= 128 expert-sorted pairs (moe_dispatch tables with gmax 128),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;
@@ -151,6 +155,22 @@ int dsv41_router_logits(const uint16_t* x, long long ldx, const uint16_t* y, lon
  * H % 1024 == 0. */
 int dsv41_router_logits_f32w(const uint16_t* x, long long ldx, const float* G, long long ldg, int E, int H, int M, float* part,
                              void* stream);
+
+/* The decode block's hyper-connection steps either side of the experts (hc <= 4 residual streams):
+ * pre (fused2.hc_pre_norm_quant2, fused2.py:189-236): per row b, a = bf16(sum_h pre[b][h] * x[b][h]) (x bf16 [B][ldx], the
+ * hc streams D apart; pre fp32 [B][ldp]), y = bf16(a * (1 / sqrt(mean(a^2) + eps)) * w) (w bf16 [D]), yq =
+ * fake_quant_fp8(y); optional yf = y as fp32 and yqp = yq in the 8-k permuted order (fused2.py:113-117). D % 32 == 0. */
+int dsv41_hc_pre_norm_quant(const uint16_t* x, long long ldx, int hc, const float* pre, long long ldp, const uint16_t* w, float eps,
+                            int B, int D, uint16_t* y, long long ldy, uint16_t* yq, long long ldq, float* yf, long long ldf,
+                            uint16_t* yqp, long long ldqp, void* stream);
+
+/* post (fused2.hc_post2_, fused2.py:474-538), in place on the residual res bf16 [B][ldr] (4 streams D apart): per row b
+ * and column n, x = bf16(sum_{k < nsum} y2[b][k][n] + ys[b][n]) (y2 fp32 at y2 + b y2_row + k y2_sum; ys bf16 or NULL),
+ * or the given bf16 x when nsum = 0; then r[i] <- bf16(post[b][i] x + sum_j comb[b][j][i] r[j]) (post fp32 [B][ldpost],
+ * comb fp32 [B][ldcomb] as 4 x 4 row-major). D % 4 == 0. */
+int dsv41_hc_post(const uint16_t* x, long long ldx, const float* y2, long long y2_row, long long y2_sum, int nsum, const uint16_t* ys,
+                  long long ldys, uint16_t* res, long long ldr, const float* post, long long ldpost, const float* comb, long long ldcomb,
+                  int B, int D, void* stream);
 
 /* MoE gate on logits: score_func 0 sqrt(softplus), 1 sigmoid, 2 softmax; top-k of scores + bias (lowest index
  * wins ties); weights renormalised when norm, times route_scale. fused2.gate_topk (fused2.py:418-471),

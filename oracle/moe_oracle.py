@@ -43,6 +43,11 @@ PINS = {
                      "halves, no routing weight, limit) against moe_layer_routed with the expert's dequantised weights "
                      "and a one-hot x (gu exact in bf16)",
     "gemv_pairs": "wt x grouped_gemm on singleton groups + scalar brute force on a tiny case",
+    "hc_pre_norm_quant": "one-hot pre weights reduce it to rmsnorm: torch.nn.functional.rms_norm (fp32, CPU) + golden-pinned "
+                         "fake_quant_fp8; an equal split of one stream over two weights gives the same",
+    "hc_post": "special cases (post 0, comb identity: unchanged; comb 0, post one-hot: the stream takes x) + torch.einsum "
+               "of the 4 x 4 mix in float64",
+    "hc_post_input": "closed form on exactly representable sums (small integers times powers of two)",
     "residual_rmsnorm_quant": "torch.nn.functional.rms_norm (fp32, CPU) + golden-pinned fake_quant_fp8",
     "int8_quant_blocks": "closed form (|v - q s| <= s / 2, q range, zero block) + compiled reference CPU library (int8 mode) layer output",
     "w4a8_gemv": "brute force on tiny inputs (integer dot by hand) + compiled reference CPU library (int8 mode) layer output",
@@ -443,6 +448,38 @@ def moe_layer(x_bf16_vals, eid, wt, W13, S13, W2, S2, Ws13, Ws2, inter: int, lim
     if Ws13 is not None:
         y = (y + shared_expert(xq, Ws13, Ws2, inter, limit)).astype(F32)
     return bf16_round(y)
+
+
+# --------------------------------------------------------------------------- hyper-connection steps around the experts
+def hc_pre_norm_quant(x, pre, w, eps: float):
+    """The decode block's hyper-connection pre-mix + rmsnorm + FP8 fake quant (fused2.py:121-151; the two-pass twin
+    fused2.py:180-236): a = bf16(sum_h pre[h] x_h) (fp32), y = bf16(a * (1 / sqrt(mean(a^2) + eps)) * w),
+    yq = fake_quant_fp8(y). x [B, hc, d] (values of bf16), pre [B, hc], w [d]. Returns (y, yq) as fp32 values of bf16.
+    The sums are evaluated in float64 and rounded once to fp32 (the kernels' fp32 order differs by at most an ulp)."""
+    x = np.asarray(x, np.float64)
+    pre = np.asarray(pre, np.float64)
+    a = bf16_round((pre[:, :, None] * x).sum(1).astype(F32))
+    var = ((a.astype(np.float64) ** 2).sum(-1, keepdims=True) / a.shape[-1]).astype(F32)
+    inv = (F32(1.0) / np.sqrt(var + F32(eps))).astype(F32)
+    y = bf16_round((a * inv * np.asarray(w, F32)).astype(F32))
+    return y, fake_quant_fp8(y).astype(F32)
+
+
+def hc_post(x, res, post, comb):
+    """In-place hyper-connection post mix (fused2.py:476-508): r_i <- bf16(post[i] x + sum_j comb[j][i] r_j) per row, the 4
+    streams of res [B, 4, d] (values of bf16); x [B, d]; post [B, 4]; comb [B, 4, 4]. Evaluated in float64, rounded once."""
+    x = np.asarray(x, np.float64)
+    res = np.asarray(res, np.float64)
+    post = np.asarray(post, np.float64)
+    comb = np.asarray(comb, np.float64)
+    out = post[:, :, None] * x[:, None, :] + (comb[:, :, :, None] * res[:, :, None, :]).sum(1)
+    return bf16_round(out.astype(F32))
+
+
+def hc_post_input(y2, ys):
+    """x of the post mix from the MoE pieces (fused2.py:490-495): bf16(sum_k y2_k + ys), y2 [B, nsum, d] fp32, ys [B, d]."""
+    s = np.asarray(y2, np.float64).sum(1) + (0.0 if ys is None else np.asarray(ys, np.float64))
+    return bf16_round(s.astype(F32))
 
 
 # --------------------------------------------------------------------------- host (CPU) int8 path

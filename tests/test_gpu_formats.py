@@ -143,3 +143,53 @@ def test_residual_rmsnorm_quant(M, H, weighted):
     assert np.all(np.abs(got_n - ref_n) <= np.abs(ref_n) * 2.0 ** -7 + 1e-30)
     assert (got_n == ref_n).mean() > 0.99
     assert np.array_equal(f(xq), O.fake_quant_fp8(got_n))
+
+
+@pytest.mark.parametrize("B,want_perm", [(1, True), (4, False)])
+def test_hc_pre_norm_quant(B, want_perm):
+    """The hyper-connection pre-mix + rmsnorm + FP8 quant against the oracle (y within one bf16 ulp, fp32 order of the
+    statistics; yq exactly fq8 of the kernel's own y; yf = y; yqp = yq in the 8-k permuted order)."""
+    from dsv41_amd import fused2
+    g = torch.Generator().manual_seed(60 + B)
+    hc, d = 4, 7168
+    x = (torch.randn(B, 1, hc, d, generator=g) * 2).to(torch.bfloat16)
+    pre = torch.rand(B, hc, generator=g) * 0.8 + 0.1
+    w = (torch.rand(d, generator=g) + 0.5).to(torch.bfloat16)
+    r = fused2.hc_pre_norm_quant2(x.to(DEV), pre.to(DEV), w.to(DEV), 1e-6, want_f32=True, want_perm=want_perm)
+    y, yq, yf = r[0], r[1], r[2]
+    f = lambda t: O.bf16_bits_to_f32(u16(t.contiguous()))
+    ref_y, _ = O.hc_pre_norm_quant(f(x.reshape(B, hc, d)), pre.numpy(), f(w), 1e-6)
+    got = f(y)
+    assert np.all(np.abs(got - ref_y) <= np.abs(ref_y) * 2.0 ** -7 + 1e-30) and (got == ref_y).mean() > 0.99
+    assert np.array_equal(f(yq), O.fake_quant_fp8(got))
+    assert np.array_equal(yf.cpu().numpy(), got)
+    if want_perm:
+        assert np.array_equal(f(r[3]), O.permute_x(f(yq)))
+
+
+@pytest.mark.parametrize("mode", ["x", "y2", "y2_sum_first"])
+def test_hc_post(mode):
+    """The in-place hyper-connection post mix against the oracle (one rounding; fp32 FMA order within one bf16 ulp), with
+    x given, or from the MoE pieces y2 [B, nsum, d] (or [nsum, B, d]) + ys."""
+    from dsv41_amd import fused2
+    rng = np.random.default_rng(70)
+    B, d, nsum = 3, 7168, 8
+    res0 = O.bf16_round(rng.standard_normal((B, 1, 4, d)).astype(np.float32))
+    post = rng.standard_normal((B, 4)).astype(np.float32)
+    comb = rng.standard_normal((B, 4, 4)).astype(np.float32)
+    to_bf16 = lambda a: torch.from_numpy(O.f32_to_bf16_bits(a).view(np.int16)).view(torch.bfloat16).to(DEV)
+    res = to_bf16(res0)
+    if mode == "x":
+        xv = O.bf16_round(rng.standard_normal((B, d)).astype(np.float32))
+        fused2.hc_post2_(to_bf16(xv), res, torch.from_numpy(post).to(DEV), torch.from_numpy(comb).to(DEV))
+    else:
+        y2 = rng.standard_normal((B, nsum, d)).astype(np.float32)
+        ys = O.bf16_round(rng.standard_normal((B, d)).astype(np.float32))
+        xv = O.hc_post_input(y2, ys)
+        y2d = torch.from_numpy(y2 if mode == "y2" else np.ascontiguousarray(y2.transpose(1, 0, 2))).to(DEV)
+        fused2.hc_post2_(None, res, torch.from_numpy(post).to(DEV), torch.from_numpy(comb).to(DEV), y2=y2d, ys=to_bf16(ys),
+                         y2_sum_first=(mode == "y2_sum_first"))
+    ref = O.hc_post(xv, res0.reshape(B, 4, d), post, comb)
+    got = O.bf16_bits_to_f32(u16(res.contiguous())).reshape(B, 4, d)
+    tol = np.maximum(np.abs(ref), np.abs(got)) * 2.0 ** -7 + 1e-5
+    assert np.all(np.abs(got - ref) <= tol) and (got == ref).mean() > 0.99

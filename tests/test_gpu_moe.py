@@ -766,3 +766,31 @@ def test_moe_layer_class(T):
     # the gate entry point on its own
     w2_, i2_ = layer.gate(x)
     assert np.array_equal(i2_.cpu().numpy(), ref_i)
+
+
+@pytest.mark.parametrize("M,with_shared", [(1, True), (3, False)])
+def test_decode_hc_post_fused(full_layer, M, with_shared):
+    """The hyper-connection post mix in the down launch's epilogue equals the standalone hc_post2_ on the layer's bf16
+    output, bit for bit (same x = bf16(y + ys), same multiply-add order), in place on the 4 residual streams."""
+    from dsv41_amd import fused2, moe, quant
+    E, H, I, ws, ex = full_layer
+    rng = np.random.default_rng(990 + M)
+    eid, wt = rand_routing(M, E, 8, 991 + M)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 992 + M).to(DEV))
+    ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
+    shared = None
+    if with_shared:
+        g = torch.Generator(device=DEV).manual_seed(993)
+        shared = moe.SharedExpert.prepare((torch.randn(2 * I, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16),
+                                          (torch.randn(H, I, generator=g, device=DEV) / I ** 0.5).to(torch.bfloat16))
+    res0 = torch.from_numpy(O.f32_to_bf16_bits(rng.standard_normal((M, 1, 4, H)).astype(np.float32)).view(np.int16)).view(torch.bfloat16).to(DEV)
+    post = torch.from_numpy(rng.standard_normal((M, 4)).astype(np.float32)).to(DEV)
+    comb = torch.from_numpy(rng.standard_normal((M, 4, 4)).astype(np.float32)).to(DEV)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    moe.moe_experts(xq, ed, wd, ex, 10.0, out=out, shared=shared)
+    res_ref = res0.clone()
+    fused2.hc_post2_(out, res_ref, post, comb)
+    res = res0.clone()
+    moe.moe_experts(xq, ed, wd, ex, 10.0, shared=shared, hc=(res, post, comb))
+    torch.cuda.synchronize()
+    assert torch.equal(res, res_ref)

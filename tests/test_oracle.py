@@ -329,3 +329,49 @@ def test_every_oracle_function_has_a_pin():
     missing = fns - helpers - set(O.PINS)
     assert not missing, f"oracle functions without a pin: {sorted(missing)}"
     assert set(O.PINS) <= fns, f"PINS names functions the oracle lacks: {sorted(set(O.PINS) - fns)}"
+
+
+def test_hc_pre_norm_quant_pins():
+    """One-hot pre weights reduce the pre-mix to a copy of one stream: rmsnorm of it (torch rms_norm, fp32 CPU) and the
+    golden-pinned fq8; splitting that stream's weight over two equal streams gives the same result."""
+    import torch
+    g = torch.Generator().manual_seed(7)
+    B, hc, d = 3, 4, 512
+    x = (torch.randn(B, hc, d, generator=g) * 2).to(torch.bfloat16)
+    w = (torch.rand(d, generator=g) + 0.5).to(torch.bfloat16)
+    pre = np.zeros((B, hc), np.float32)
+    pre[:, 2] = 1.0
+    y, yq = O.hc_pre_norm_quant(x.float().numpy(), pre, w.float().numpy(), 1e-6)
+    ref = torch.nn.functional.rms_norm(x[:, 2].float(), (d,), w.float(), eps=1e-6).to(torch.bfloat16).float().numpy()
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30) and (y == ref).mean() > 0.99
+    assert np.array_equal(yq, O.fake_quant_fp8(y))
+    x2 = x.clone()
+    x2[:, 1] = x2[:, 2]
+    pre2 = np.zeros((B, hc), np.float32)
+    pre2[:, 1] = pre2[:, 2] = 0.5
+    y2, _ = O.hc_pre_norm_quant(x2.float().numpy(), pre2, w.float().numpy(), 1e-6)
+    assert np.array_equal(y2, y)
+
+
+def test_hc_post_pins():
+    import torch
+    rng = np.random.default_rng(8)
+    B, d = 2, 256
+    res = O.bf16_round(rng.standard_normal((B, 4, d)).astype(np.float32))
+    x = O.bf16_round(rng.standard_normal((B, d)).astype(np.float32))
+    # post 0 and comb = identity: the streams are unchanged; comb 0 and post one-hot: stream i takes x, the rest 0
+    assert np.array_equal(O.hc_post(x, res, np.zeros((B, 4)), np.tile(np.eye(4), (B, 1, 1))), res)
+    oh = np.zeros((B, 4))
+    oh[:, 3] = 1.0
+    out = O.hc_post(x, res, oh, np.zeros((B, 4, 4)))
+    assert np.array_equal(out[:, 3], x) and np.all(out[:, :3] == 0)
+    # general mix against torch's einsum in float64
+    post = rng.standard_normal((B, 4))
+    comb = rng.standard_normal((B, 4, 4))
+    t = torch.einsum("bji,bjn->bin", torch.from_numpy(comb), torch.from_numpy(res.astype(np.float64))) + \
+        torch.from_numpy(post)[:, :, None] * torch.from_numpy(x.astype(np.float64))[:, None, :]
+    assert np.array_equal(O.hc_post(x, res, post, comb), O.bf16_round(t.numpy().astype(np.float32)))
+    # the MoE pieces: small integers times powers of two sum exactly
+    y2 = rng.integers(-64, 64, (B, 6, d)).astype(np.float32) * 0.25
+    ys = rng.integers(-8, 8, (B, d)).astype(np.float32)
+    assert np.array_equal(O.hc_post_input(y2, ys), O.bf16_round((y2.sum(1) + ys).astype(np.float32)))
