@@ -106,9 +106,10 @@ def routing_stream(torch, dev, steps, M, seed):
 
 
 def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode="fused", seed=7):
-    """One decode layer per step over the rotating layer copies; shared: list of (Ws13, Ws2) bf16 shared-expert copies,
-    rotated with the layers, computed inside the two decode launches ("fused") or as its own launches first
-    ("separate"). Returns (seconds per step, mean unique experts per step)."""
+    """One decode layer per step over the rotating layer copies; shared: list of bf16 SharedExpert copies, rotated with
+    the layers, computed inside the two decode launches ("fused") or as its own launches first ("separate"), or of
+    (w8.W8 w13, w8.W8 w2) FP8 copies run as two FP8 GEMMs and a SwiGLU first ("fp8"). Returns (seconds per step, mean
+    unique experts per step)."""
     from dsv41_amd import moe, quant
     logits = routing_stream(torch, dev, steps, M, seed)
     gx = torch.Generator(device=dev).manual_seed(seed + 1)
@@ -126,6 +127,10 @@ def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode=
             moe.moe_route_experts(*route, out=out, eid_out=eid[i], wt_out=wt[i])
         elif shared_mode == "fused":
             moe.moe_route_experts(*route, out=out, eid_out=eid[i], wt_out=wt[i], shared=shared[i % len(shared)], ys_out=ys)
+        elif shared_mode == "fp8":
+            w13, w2 = shared[i % len(shared)]
+            y_s = moe.shared_expert_rows(xq, w13, w2, I, LIMIT)
+            moe.moe_route_experts(*route, ys=y_s, out=out, eid_out=eid[i], wt_out=wt[i])
         else:
             sw = shared[i % len(shared)]
             y_s = moe.shared_expert(xq, sw.w13, sw.w2, LIMIT, ys=ys, tiled=sw.tiled)
@@ -407,6 +412,33 @@ def bench_gemv_gpu(torch, dev, steps, warmup):
             "note": "x quantisation + GEMV launches per step, in one graph"}
 
 
+FP8_SHAPES = [(5120, 8192), (4608, 5120), (32768, 1280), (1280, 5120), (5120, 2304)]   # test_fp8_tc.py:19 (V4.1 dims)
+
+
+def bench_fp8_dense(torch, dev, steps, warmup):
+    """The FP8 dense-weight GEMV (w8.linear_w on a W8 weight, one token) at the reference's own test shapes, each over
+    enough resident copies to exceed the 256 MB Infinity Cache, against torch's bf16 F.linear (hipBLASLt) on bf16
+    copies of the same shape. Bytes: the FP8 weights plus their E8M0 scales."""
+    from dsv41_amd import w8
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(17)
+    for (N, Kd) in FP8_SHAPES:
+        copies = max(2, int(600e6 // (N * Kd)) + 1)
+        Ws = [w8.W8(torch.randint(0, 256, (N, Kd), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
+                    torch.randint(115, 130, (N // 32, Kd // 32), generator=g, dtype=torch.uint8, device=dev)) for _ in range(copies)]
+        x = torch.randn(1, Kd, generator=g, device=dev).to(torch.bfloat16)
+        t8, _ = graph_time(torch, lambda i: w8.linear_w(x, Ws[i % copies]), max(steps, copies), warmup)
+        del Ws
+        Wb = [torch.randn(N, Kd, generator=g, device=dev).to(torch.bfloat16) for _ in range(max(2, copies // 2))]
+        tb, _ = graph_time(torch, lambda i: torch.nn.functional.linear(x, Wb[i % len(Wb)]), max(steps, len(Wb)), warmup)
+        del Wb
+        nbytes = N * Kd + (N // 32) * (Kd // 32)
+        out[f"{N}x{Kd}"] = {"us": round(t8 * 1e6, 2), "GBps": round(nbytes / t8 / 1e9, 1),
+                            "bf16_linear_us": round(tb * 1e6, 2), "speedup_vs_bf16": round(tb / t8, 2)}
+        torch.cuda.empty_cache()
+    return out
+
+
 def progress(msg):
     """One line per finished phase on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -475,7 +507,21 @@ def main():
                                           "rides in the down launch; separate: three launches (gate/up GEMV, SwiGLU, down GEMV) before "
                                           "the routed experts; 4 rotating copies"}
         del shared
+        # the same shared expert as the checkpoint stores it (FP8 E4M3, 32 x 32 E8M0 block scales, kept as w8.W8)
+        from dsv41_amd import w8
+        shared8 = [(w8.W8(torch.randint(0, 256, (2 * I, H), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
+                          torch.randint(118, 122, (2 * I // 32, H // 32), generator=g, dtype=torch.uint8, device=dev)),
+                    w8.W8(torch.randint(0, 256, (H, I), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
+                          torch.randint(118, 122, (H // 32, I // 32), generator=g, dtype=torch.uint8, device=dev)))
+                   for _ in range(N_COPIES)]
+        t_fp8, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared8, shared_mode="fp8")
+        extra["shared_expert"]["layer_us_fp8_weights"] = round(t_fp8 * 1e6, 2)
+        extra["shared_expert"]["us_added_fp8_weights"] = round((t_fp8 - t_routed) * 1e6, 2)
+        extra["shared_expert"]["fp8_bytes"] = 3 * I * H + 3 * (I // 32) * (H // 32)
+        del shared8
         progress("layer with shared expert")
+        extra["fp8_dense_gemv"] = bench_fp8_dense(torch, dev, K, W)
+        progress("FP8 dense GEMV")
         for M in (4, 8, 16):
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),

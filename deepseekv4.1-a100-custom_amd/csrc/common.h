@@ -271,11 +271,13 @@ __device__ __forceinline__ void pipeline_start(int n, LoadF&& load) {
 
 template <int PF, typename LoadF, typename UseF>
 __device__ __forceinline__ void pipeline_finish(int n, LoadF&& load, UseF&& use) {
-    if (n < PF) {  // short: no pipeline
-        for (int i = 0; i < n; ++i) {
-            load(0, i);
-            use(0);
-        }
+    if (n < PF) {  // short: issue every load, then consume in order (one memory latency, not n)
+#pragma unroll
+        for (int i = 0; i < PF; ++i)
+            if (i < n) load(i, i);
+#pragma unroll
+        for (int i = 0; i < PF; ++i)
+            if (i < n) use(i);
         return;
     }
     int it = 0;

@@ -40,6 +40,8 @@ SIGNATURES = {
     "dsv41_residual_rmsnorm_quant": [P, LL, P, LL, P, F, I, I, P, LL, P, LL, P],
     "dsv41_gate_topk": [P, LL, P, I, I, F, I, F, I, I, P, P, I, LL, P],
     "dsv41_router_logits_f32w": [P, LL, P, LL, I, I, I, P, P],
+    "dsv41_fp8_gemm": [P, LL, I, P, LL, I, I, P, LL, I, I, P, LL, P, LL, P],
+    "dsv41_dequant_fp8": [P, LL, I, P, LL, I, I, P, LL, P],
     "dsv41_hc_pre_norm_quant": [P, LL, I, P, LL, P, F, I, I, P, LL, P, LL, P, LL, P, LL, P],
     "dsv41_hc_post": [P, LL, P, LL, LL, I, P, LL, P, LL, P, LL, P, LL, I, I, P],
     "dsv41_router_logits": [P, LL, P, LL, P, F, P, LL, I, I, I, P, P, LL, P, LL, P],

@@ -121,3 +121,62 @@ def moe_dispatch(eid: torch.Tensor, wt: torch.Tensor, topk: int, n_experts: int,
     _lib.call("dsv41_moe_dispatch", _lib.ptr(eid), _lib.ptr(wt), n, topk, n_experts, gmax, _lib.ptr(tok_sorted), _lib.ptr(wt_sorted),
               _lib.ptr(inv), _lib.ptr(grp_expert), _lib.ptr(grp_start), _lib.ptr(n_groups), _lib.stream(device))
     return tok_sorted, wt_sorted, inv, grp_expert, grp_start
+
+
+# --------------------------------------------------------------------------- FP8-weight GEMM (M <= 64 rows per pass)
+FP8_ROWS = 64  # output rows one launch handles; the weights are read once for all of them
+
+def _fp8_launch(x: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, Mo: int, N: int, K: int, group_cols: int, tiled: bool,
+                out: torch.Tensor | None, outb: torch.Tensor | None) -> None:
+    _lib.call("dsv41_fp8_gemm", _lib.ptr(w8), w8.stride(0), 1 if tiled else 0, _lib.ptr(s8), s8.stride(0), N, K,
+              _lib.ptr(x), x.stride(0), Mo, group_cols, _lib.ptr(out), out.stride(0) if out is not None else 0,
+              _lib.ptr(outb), outb.stride(0) if outb is not None else 0, _lib.stream(x.device))
+
+
+def fp8_gemm_tc(x: torch.Tensor, w8: torch.Tensor, s8: torch.Tensor, group_cols: int = 0, out_dtype=torch.bfloat16,
+                tiled: bool = False) -> torch.Tensor:
+    """x: bf16 [M, K] (contiguous); w8: uint8 E4M3 bytes [N, K] in the order w8.permute_k gives (tiled=True: also
+    w8.tile); s8: uint8 E8M0 [ceil(N/32), K/32]. Returns x @ dequant(w8, s8)^T as [M, N] (fp32 accumulation,
+    rounded to out_dtype), cukern.py:114-173. group_cols > 0: block-diagonal use (x [B * N/group_cols, K]; output
+    row b, column n uses x row b * (N/group_cols) + n // group_cols) -> [B, N]. More than 64 output rows run in
+    passes of 64 (the reference also chunks, cukern.py:129-132)."""
+    dev = _lib.require_cuda(x, w8, s8)
+    M, K = x.shape
+    N = w8.shape[0]
+    assert x.dtype == torch.bfloat16 and x.is_contiguous() and w8.is_contiguous() and s8.is_contiguous()
+    assert w8.dtype == torch.uint8 and s8.dtype == torch.uint8
+    assert K % 64 == 0 and N % 8 == 0 and (group_cols == 0 or group_cols % 16 == 0 and N % group_cols == 0)
+    G = N // group_cols if group_cols else 1
+    Mo = M // G
+    assert Mo * G == M
+    if Mo > FP8_ROWS:
+        return torch.cat([fp8_gemm_tc(x[i * G:(i + FP8_ROWS) * G], w8, s8, group_cols, out_dtype, tiled)
+                          for i in range(0, Mo, FP8_ROWS)], dim=0)
+    if out_dtype == torch.bfloat16:
+        y = torch.empty(Mo, N, device=dev, dtype=torch.bfloat16)
+        _fp8_launch(x, w8, s8, Mo, N, K, group_cols, tiled, None, y)
+        return y
+    y = torch.empty(Mo, N, device=dev, dtype=torch.float32)
+    _fp8_launch(x, w8, s8, Mo, N, K, group_cols, tiled, y, None)
+    return y if out_dtype == torch.float32 else y.to(out_dtype)
+
+
+def fp8_gemv(x: torch.Tensor, w_fp8: torch.Tensor, s_u8: torch.Tensor) -> torch.Tensor:
+    """x: bf16 [M, K]; w_fp8: float8_e4m3fn / uint8 [N, K] row-major (any N); s_u8: uint8 [ceil(N/32), K/32] (E8M0).
+    fp32 [M, N] (cukern.py:78-93; the reference takes M == 1, this takes M <= 64). K % 32 == 0: a K that is not a
+    multiple of 64 is padded with 32 zero columns (weights and activations) for the 64-k chunks of the kernel."""
+    dev = _lib.require_cuda(x, w_fp8, s_u8)
+    M, K = x.shape
+    N = w_fp8.shape[0]
+    assert x.stride(1) == 1 and K % 32 == 0 and 1 <= M <= FP8_ROWS
+    w = w_fp8.view(torch.uint8)
+    s = s_u8.view(torch.uint8)
+    assert w.stride(1) == 1 and s.stride(1) == 1 and s.shape[0] * 32 >= N and s.shape[1] * 32 >= K
+    if K % 64:
+        w = torch.nn.functional.pad(w, (0, 32))
+        x = torch.nn.functional.pad(x, (0, 32))
+        s = torch.nn.functional.pad(s, (0, 1), value=127)
+        K += 32
+    out = torch.empty(M, N, device=dev, dtype=torch.float32)
+    _fp8_launch(x.to(torch.bfloat16), w, s, M, N, K, 0, False, out, None)
+    return out

@@ -2,8 +2,8 @@
 the routed experts' w1 / w3 / w2 packed E2M1 weights (I8) and E8M0 scales (F8_E8M0) under
 layers.{i}.ffn.experts.{e}.w{1,2,3}.{weight,scale} are stacked as w13 = [w1; w3] along N (load.py:128-148) and
 repacked into the tile_fp4 layout on the GPU (load.py:145-147); the router (ffn.gate.weight / .bias) and the shared
-expert (ffn.shared_experts.w{1,2,3}.weight, bf16, or FP8 E4M3 with per-32x32 E8M0 block scales dequantised to bf16 as
-quant.dequant_fp8_block does, quant.py:90-95) complete a MoE layer.
+expert (ffn.shared_experts.w{1,2,3}.weight: bf16, or FP8 E4M3 with per-32x32 E8M0 block scales, kept as FP8 w8.W8 on
+the GPU or dequantised to bf16 as quant.dequant_fp8_block does, quant.py:90-95) complete a MoE layer.
 """
 from __future__ import annotations
 
@@ -49,12 +49,16 @@ def load_experts(ckpt: Checkpoint, layer: int, device, tiled: bool = True, prefi
 
 
 def dequant_fp8_block(w: torch.Tensor, scale: torch.Tensor, block: int = 32) -> torch.Tensor:
-    """float8_e4m3fn [N, K] with E8M0 block scales [ceil(N/32), ceil(K/32)] -> bf16 [N, K] (quant.py:90-95)."""
-    from .quant import e8m0_to_float
+    """float8_e4m3fn [N, K] with E8M0 block scales [ceil(N/32), ceil(K/32)] -> bf16 [N, K] (quant.py:90-95): the HIP
+    kernel on the GPU; on the host each weight gathers its block's scale value and the fp32 product is cast."""
+    from . import quant
+    if w.is_cuda:
+        return quant.dequant_fp8_block(w, scale, block)
     n, k = w.shape
-    s = e8m0_to_float(scale.view(torch.uint8))[: (n + block - 1) // block, : (k + block - 1) // block]
-    s = s.repeat_interleave(block, 0)[:n].repeat_interleave(block, 1)[:, :k]
-    return (w.float() * s).to(torch.bfloat16)
+    blk_r = torch.arange(n, device=w.device) // block
+    blk_c = torch.arange(k, device=w.device) // block
+    sv = quant.e8m0_to_float(scale)[blk_r[:, None], blk_c[None, :]]
+    return (w.view(torch.float8_e4m3fn).float() * sv).to(torch.bfloat16)
 
 
 def _dense_bf16(ckpt: Checkpoint, name: str, device) -> torch.Tensor:
@@ -65,14 +69,25 @@ def _dense_bf16(ckpt: Checkpoint, name: str, device) -> torch.Tensor:
     return w.to(torch.bfloat16)
 
 
-def load_shared_expert(ckpt: Checkpoint, layer: int, device, tiled: bool = True, prefix: str | None = None) -> tuple:
-    """(w13 = [w1; w3] bf16 [2I, H], w2 bf16 [H, I]) of the layer's shared expert, row-major (model.py:385-387)."""
+def load_shared_expert(ckpt: Checkpoint, layer: int, device, tiled: bool = True, prefix: str | None = None,
+                       fp8: bool | None = None) -> tuple:
+    """(w13 = [w1; w3] [2I, H], w2 [H, I]) of the layer's shared expert (model.py:385-387). FP8 E4M3 checkpoint
+    weights stay FP8 on the GPU as w8.W8 (load.py:55-58 of the reference keeps W8 when enabled) unless fp8 is False;
+    bf16 weights, or FP8 ones on the host, come back as bf16 row-major tensors."""
+    from . import w8
     p = _prefix(layer, prefix) + "ffn.shared_experts."
-    w1, w3, w2 = (_dense_bf16(ckpt, p + f"{k}.weight", device) for k in ("w1", "w3", "w2"))
+    names = [p + f"{k}.weight" for k in ("w1", "w3", "w2")]
+    keep = (w8.ENABLED if fp8 is None else fp8) and torch.device(device).type == "cuda"
+    if keep and all(ckpt.meta(n)[0] == "F8_E4M3" for n in names):
+        W = [w8.W8(ckpt.get(n, device).view(torch.uint8), ckpt.get(n.replace(".weight", ".scale"), device).view(torch.uint8))
+             for n in names]
+        return w8.W8.cat(W[:2]), W[2]
+    w1, w3, w2 = (_dense_bf16(ckpt, n, device) for n in names)
     return torch.cat([w1, w3], dim=0).contiguous(), w2.contiguous()
 
 
-def load_moe(ckpt: Checkpoint, layer: int, device, cfg: dict | None = None, tiled: bool = True, prefix: str | None = None) -> MoE:
+def load_moe(ckpt: Checkpoint, layer: int, device, cfg: dict | None = None, tiled: bool = True, prefix: str | None = None,
+             shared_fp8: bool | None = None) -> MoE:
     """One MoE layer (router, routed experts, shared expert) as moe.MoE, with the gate settings from the model config
     (config.json beside the weights, or `cfg`): n_activated_experts, score_func, route_scale, swiglu_limit,
     gate_temp (default 1), norm_topk_prob (default true) (model.py:361-367)."""
@@ -83,7 +98,7 @@ def load_moe(ckpt: Checkpoint, layer: int, device, cfg: dict | None = None, tile
     ex = load_experts(ckpt, layer, device, tiled=tiled, prefix=prefix)
     sh_w13 = sh_w2 = None
     if (p + "ffn.shared_experts.w1.weight") in ckpt:
-        sh_w13, sh_w2 = load_shared_expert(ckpt, layer, device, prefix=prefix)
+        sh_w13, sh_w2 = load_shared_expert(ckpt, layer, device, prefix=prefix, fp8=shared_fp8)
     return MoE(ex, gate_w, gate_b, topk=int(cfg["n_activated_experts"]), score_func=cfg.get("score_func", "softmax"),
                route_scale=float(cfg.get("route_scale", 1.0)), norm_topk_prob=bool(cfg.get("norm_topk_prob", True)),
                gate_temp=float(cfg.get("gate_temp", 1.0)), swiglu_limit=float(cfg.get("swiglu_limit", 0.0)), sh_w13=sh_w13, sh_w2=sh_w2)

@@ -405,6 +405,16 @@ def shared_expert(xq: torch.Tensor, Ws13: torch.Tensor, Ws2: torch.Tensor, limit
     return out
 
 
+def shared_expert_rows(xq: torch.Tensor, sh_w13, sh_w2, inter: int, limit: float) -> torch.Tensor:
+    """bf16 ys = linear_w(swiglu_quant(linear_w(xq, sh_w13)), sh_w2) (decode.py:368-371, model.py:409-412) for
+    bf16 tensors or w8.W8 weights: the FP8 GEMM streams W8 weights (up to 64 rows per launch), the library GEMM takes
+    bf16 weights or more rows."""
+    from .fused import swiglu_quant
+    from .w8 import linear_w
+    gu = linear_w(xq, sh_w13)
+    return linear_w(swiglu_quant(gu, None, inter, limit), sh_w2)
+
+
 class MoEDecodeLayer:
     """One MoE layer at decode (M <= 16 tokens): router logits (given, or x . G^T with bf16 router weights G),
     gate_topk, the shared expert and the routed FP4 experts, combined as y = bf16(sum_j y2_j + ys)
@@ -475,11 +485,12 @@ def router_logits_f32w(x: torch.Tensor, G: torch.Tensor, part: torch.Tensor | No
 class MoE:
     """The expert compute of the reference's model.MoE (model.py:354-413, 554-591) for one layer on the GPU path:
     gate (fp32 router weights, softmax / sigmoid / sqrt(softplus), + bias for the selection, top-k, renormalised and
-    scaled), x fake-quantised to FP8 (model.py:565), the routed FP4 experts, the bf16 shared expert, and
+    scaled), x fake-quantised to FP8 (model.py:565), the routed FP4 experts, the shared expert (bf16, or FP8 w8.W8 as
+    the checkpoint stores it), and
     y = bf16(sum_j w_j y2_j + shared) (model.py:589-591).
       * <= 16 tokens (decode): the router GEMV on fp32 weights as split-K partial sums, then the two fused decode
-        launches (routing inside the up launch for one token; the shared expert rides in both launches when it fits
-        them, else runs as its own launches first);
+        launches (routing inside the up launch for one token; a bf16 shared expert rides in both launches when it fits
+        them, else runs as its own launches first; an FP8 one runs first as two FP8 GEMM launches and a SwiGLU);
       * > 16 tokens (prefill): router logits and the shared expert's two products as plain library GEMMs (F.linear on
         the GPU, as the reference runs them, model.py:392, 410-412; w8.py:102-103), gate_topk, then the prefill grouped
         GEMMs with the slot-ordered combine.
@@ -498,10 +509,18 @@ class MoE:
         self.gate_w = gate_w.to(torch.float32).contiguous()                       # fp32 [E, dim] (model.py:368)
         assert self.gate_w.shape == (self.n_experts, self.dim)
         self.gate_bias = None if gate_bias is None else gate_bias.to(torch.float32).contiguous()
-        self.sh_w13 = None if sh_w13 is None else sh_w13.to(torch.bfloat16).contiguous()   # [w1; w3] row-major (prefill GEMMs)
-        self.sh_w2 = None if sh_w2 is None else sh_w2.to(torch.bfloat16).contiguous()
-        # the decode kernels stream the shared expert in the tile_bf16 layout (repacked once)
-        self.shared = SharedExpert.prepare(self.sh_w13, self.sh_w2, tiled=shared_tiled) if self.sh_w13 is not None else None
+        from .w8 import W8
+        self.shared = None
+        if isinstance(sh_w13, W8):
+            # FP8 shared expert (the checkpoint's format, kept as FP8): its own FP8 GEMM launches at every row count
+            assert isinstance(sh_w2, W8)
+            self.sh_w13, self.sh_w2 = sh_w13, sh_w2
+        else:
+            self.sh_w13 = None if sh_w13 is None else sh_w13.to(torch.bfloat16).contiguous()   # [w1; w3] row-major
+            self.sh_w2 = None if sh_w2 is None else sh_w2.to(torch.bfloat16).contiguous()
+            # the decode kernels stream a bf16 shared expert in the tile_bf16 layout (repacked once)
+            if self.sh_w13 is not None:
+                self.shared = SharedExpert.prepare(self.sh_w13, self.sh_w2, tiled=shared_tiled)
         self._bufs: dict = {}
         self.last_routing = None
 
@@ -523,13 +542,14 @@ class MoE:
 
     def shared_expert(self, x: torch.Tensor) -> torch.Tensor:
         """fp32 [T, dim] = linear_w(swiglu_quant(linear_fp8(x, sh_w13)), sh_w2) (model.py:409-412)."""
-        from .fused import swiglu_quant
         from .quant import fake_quant_fp8
         xq = fake_quant_fp8(x.to(torch.bfloat16))
-        if x.shape[0] <= 16:
+        if x.shape[0] <= 16 and self.shared is not None:
             return shared_expert(xq.contiguous(), self.shared.w13, self.shared.w2, self.swiglu_limit, tiled=self.shared.tiled).float()
-        gu = torch.nn.functional.linear(xq, self.sh_w13)
-        return torch.nn.functional.linear(swiglu_quant(gu, None, self.inter, self.swiglu_limit), self.sh_w2).float()
+        return self._shared_rows(xq).float()
+
+    def _shared_rows(self, xq: torch.Tensor) -> torch.Tensor:
+        return shared_expert_rows(xq, self.sh_w13, self.sh_w2, self.inter, self.swiglu_limit)
 
     def _buf(self, dev, T):
         b = self._bufs.get(T)
@@ -551,18 +571,15 @@ class MoE:
             b = self._buf(dev, T)
             _lib.call("dsv41_quant_fp8", _lib.ptr(x2), 0, T, H, x2.stride(0), 0, None, None, _lib.ptr(b["xq"]), _lib.stream(dev))
             router_logits_f32w(x2, self.gate_w, part=b["part"])
+            ys = self._shared_rows(b["xq"]) if self.shared is None and self.sh_w13 is not None else None
             moe_route_experts(b["xq"], b["part"], self.gate_bias, self.gate_temp, self.topk, self.route_scale, self.score_func, self._norm(),
-                              self.ex, self.swiglu_limit, out=b["out"], eid_out=b["eid"], wt_out=b["wt"], shared=self.shared)
+                              self.ex, self.swiglu_limit, ys=ys, out=b["out"], eid_out=b["eid"], wt_out=b["wt"], shared=self.shared)
             self.last_routing = (b["eid"], b["wt"])
             return b["out"].view(shape)
-        from .fused import swiglu_quant
         from .quant import fake_quant_fp8
         wt, eid = self.gate(x2)
         xq = fake_quant_fp8(x2)
-        ys = None
-        if self.sh_w13 is not None:
-            ys = torch.nn.functional.linear(swiglu_quant(torch.nn.functional.linear(xq, self.sh_w13), None, self.inter, self.swiglu_limit),
-                                            self.sh_w2)
+        ys = self._shared_rows(xq) if self.sh_w13 is not None else None
         out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
         prefill_experts(xq, eid, wt, self.ex, self.swiglu_limit, ys=ys, out=out)
         self.last_routing = (eid, wt)

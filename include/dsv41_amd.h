@@ -172,6 +172,22 @@ int dsv41_hc_post(const uint16_t* x, long long ldx, const float* y2, long long y
                   long long ldys, uint16_t* res, long long ldr, const float* post, long long ldpost, const float* comb, long long ldcomb,
                   int B, int D, void* stream);
 
+/* Dense FP8 weights x bf16 activations, M <= 64 output rows (cukern.fp8_gemm_tc, cukern.py:98-173, and
+ * cukern.fp8_gemv, cukern.py:78-93, behind w8.linear_w / w8.oproj_a, w8.py:102-124):
+ * out[t][n] = sum_k x[t'][k] * e4m3(W[n][k]) * 2^(S[n / 32][k / 32] - 127), fp32 accumulation, fp32 and/or bf16 output.
+ * W: E4M3 bytes, natural row-major [N][ldw] or (tiled = 1) [N/16][K/64][4][16][16 B] with ldw = K (N % 16 == 0);
+ * S: E8M0 bytes [ceil(N/32)][lds]. x bf16 rows ldx apart; t' = t, or with group_cols > 0 (block-diagonal use,
+ * w8.oproj_a) t' = t * (N / group_cols) + n / group_cols (group_cols % 16 == 0). K % 64 == 0. Deterministic; no workspace. */
+int dsv41_fp8_gemm(const uint8_t* W, long long ldw, int tiled, const uint8_t* S, long long lds, int N, int K,
+                   const uint16_t* x, long long ldx, int M, int group_cols, float* out, long long ldo,
+                   uint16_t* outb, long long ldob, void* stream);
+
+/* W8.bf16 / quant.dequant_fp8_block (w8.py:78-82, quant.py:90-95): out bf16 [N][ldo] = bf16(e4m3(W) * 2^(S - 127)),
+ * the fp32 product rounded to bf16 (bit-exact). W in either layout of dsv41_fp8_gemm (tiled needs K % 64 == 0);
+ * K % 16 == 0. */
+int dsv41_dequant_fp8(const uint8_t* W, long long ldw, int tiled, const uint8_t* S, long long lds, int N, int K,
+                      uint16_t* out, long long ldo, void* stream);
+
 /* MoE gate on logits: score_func 0 sqrt(softplus), 1 sigmoid, 2 softmax; top-k of scores + bias (lowest index
  * wins ties); weights renormalised when norm, times route_scale. fused2.gate_topk (fused2.py:418-471),
  * model.MoE.gate (model.py:391-404). nparts > 1: scores are that many partial sums part_stride floats apart

@@ -53,6 +53,11 @@ PINS = {
     "w4a8_gemv": "brute force on tiny inputs (integer dot by hand) + compiled reference CPU library (int8 mode) layer output",
     "swiglu_quant_host": "compiled reference CPU library stage-2 output h (inter a multiple of 256) + golden-pinned fake_quant_fp8",
     "host_layer": "compiled reference CPU library (oracle/_ref) gu, h and out, int8 and bf16 modes, inter a multiple of 256",
+    "dequant_fp8_block_f32": "torch float8_e4m3fn -> float32 cast of all 256 codes (the reference's w.float()) times torch.ldexp "
+                             "over 256 scale bytes; one scale byte changed moves exactly its 32 x 32 block",
+    "dequant_fp8_block": "bf16 of dequant_fp8_block_f32 = torch .to(torch.bfloat16) of the torch-built product",
+    "linear_fp8w": "one-hot x rows give dequantised weight columns exactly; torch F.linear in float64 on the torch-built "
+                   "dequant; block-diagonal form against a scalar loop over (b, n) on a tiny case",
 }
 
 
@@ -397,6 +402,42 @@ def linear_bf16(x, W_bits) -> np.ndarray:
     one rounding (what linear_w does for a bf16 weight, w8.py:102-103). Returns fp32 values of the bf16 result."""
     W = bf16_bits_to_f32(W_bits)
     return bf16_round((np.asarray(x, F32) @ W.T).astype(F32))
+
+
+# --------------------------------------------------------------------------- FP8 dense weights (W8)
+def dequant_fp8_block_f32(w, scale, block: int = 32) -> np.ndarray:
+    """fp32 product e4m3(w) x 2^(S-127), one E8M0 byte per 32 x 32 block, before the bf16 cast (quant.py:90-95).
+    w: uint8 E4M3 bytes [N, K]; scale: uint8 [ceil(N/32), ceil(K/32)]."""
+    w = np.asarray(w, dtype=np.uint8)
+    N, K = w.shape
+    s = e8m0_to_f32(np.asarray(scale, dtype=np.uint8))[: -(-N // block), : -(-K // block)]
+    s = np.repeat(np.repeat(s, block, axis=0)[:N], block, axis=1)[:, :K]
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (e4m3_decode(w) * s).astype(F32)
+
+
+def dequant_fp8_block(w, scale, block: int = 32) -> np.ndarray:
+    """-> bf16 bit patterns [N, K] (quant.py:90-95: (w.float() * s).to(torch.bfloat16))."""
+    return f32_to_bf16_bits(dequant_fp8_block_f32(w, scale, block))
+
+
+def linear_fp8w(x, w, scale, group_cols: int = 0) -> np.ndarray:
+    """x @ dequant_fp8_block(w, scale)^T with fp32 accumulation of exact products (w8.linear_w, w8.py:102-113;
+    cukern.fp8_gemm_tc, cukern.py:114-173), summed in float64 here and rounded to fp32. group_cols > 0: block-diagonal
+    use (cukern.py:119-121): x has B * (N / group_cols) rows and output [b, n] uses x row b * (N / group_cols) +
+    n // group_cols. Returns fp32 [rows, N] before the bf16 output rounding."""
+    W = bf16_bits_to_f32(dequant_fp8_block(w, scale)).astype(np.float64)
+    x = np.asarray(x, dtype=np.float64)
+    if not group_cols:
+        return (x @ W.T).astype(F32)
+    N, K = W.shape
+    G = N // group_cols
+    xg = x.reshape(-1, G, K)
+    out = np.empty((xg.shape[0], N), dtype=np.float64)
+    for g in range(G):
+        cols = slice(g * group_cols, (g + 1) * group_cols)
+        out[:, cols] = xg[:, g, :] @ W[cols].T
+    return out.astype(F32)
 
 
 def shared_expert(xq, Ws13, Ws2, inter: int, limit: float) -> np.ndarray:

@@ -59,7 +59,10 @@ def test_v41_checkpoint_moe_layer(tmp_path):
     deq = lambda c, s, n, kk: O.e4m3_decode(c) * np.repeat(np.repeat(O.e8m0_to_f32(s), 32, 0)[:n], 32, 1)[:, :kk]
     Ws13 = O.f32_to_bf16_bits(np.concatenate([deq(*sh["w1"], I, H), deq(*sh["w3"], I, H)]).astype(np.float32))
     Ws2 = O.f32_to_bf16_bits(deq(*sh["w2"], H, I).astype(np.float32))
-    assert np.array_equal(layer.sh_w13.view(torch.int16).cpu().numpy().view(np.uint16), Ws13)
+    from dsv41_amd import w8
+    assert isinstance(layer.sh_w13, w8.W8) and isinstance(layer.sh_w2, w8.W8), "FP8 shared expert is kept as FP8"
+    assert np.array_equal(layer.sh_w13.bf16().view(torch.int16).cpu().numpy().view(np.uint16), Ws13)
+    assert np.array_equal(layer.sh_w2.bf16().view(torch.int16).cpu().numpy().view(np.uint16), Ws2)
     for T in (1, 3, 40):
         x = torch.from_numpy((rng.standard_normal((T, H)) * 2).astype(np.float32)).to(torch.bfloat16).to(DEV)
         y = layer(x).clone()

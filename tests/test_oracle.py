@@ -375,3 +375,79 @@ def test_hc_post_pins():
     y2 = rng.integers(-64, 64, (B, 6, d)).astype(np.float32) * 0.25
     ys = rng.integers(-8, 8, (B, d)).astype(np.float32)
     assert np.array_equal(O.hc_post_input(y2, ys), O.bf16_round((y2.sum(1) + ys).astype(np.float32)))
+
+
+def _torch_dequant_fp8(w, s):
+    """quant.dequant_fp8_block built from torch's own float8_e4m3fn cast and ldexp (not the oracle's decode)."""
+    import torch
+    wt = torch.from_numpy(np.ascontiguousarray(w)).view(torch.float8_e4m3fn).float()
+    e = torch.from_numpy(np.ascontiguousarray(s).astype(np.int32)) - 127
+    N, K = w.shape
+    e = e.repeat_interleave(32, 0)[:N].repeat_interleave(32, 1)[:, :K]
+    return torch.ldexp(wt, e.float())
+
+
+def test_dequant_fp8_every_code_and_scale():
+    """Every E4M3 code times every scale byte 1..254 against torch's float8_e4m3fn cast times ldexp (the reference's
+    w.float() * s), fp32 bit-exact and after the bf16 cast (NaN codes compared as NaN)."""
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    w = np.tile(codes, (32, 1))                                          # every row holds all 256 codes
+    for b0 in range(1, 255, 8):
+        sc = np.arange(b0, b0 + 8).clip(1, 254).astype(np.uint8).reshape(1, 8)
+        got = O.dequant_fp8_block_f32(w, sc)
+        ref = _torch_dequant_fp8(w, sc).numpy()
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(O.f32_bits(got)[~nan], O.f32_bits(ref)[~nan]), f"scale bytes {b0}.."
+        gb = O.dequant_fp8_block(w, sc)
+        rb = torch.from_numpy(ref).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(gb[~nan], rb[~nan])
+
+
+def test_dequant_fp8_block_structure():
+    """A scale byte changed in one block moves exactly that 32 x 32 block, by a factor of 2 (ragged N and K)."""
+    rng = np.random.default_rng(5)
+    w = rng.integers(0, 256, (70, 100), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0
+    s = rng.integers(110, 130, (3, 4), dtype=np.uint8)
+    a = O.dequant_fp8_block_f32(w, s)
+    s2 = s.copy()
+    s2[1, 2] += 1
+    b = O.dequant_fp8_block_f32(w, s2)
+    mask = np.zeros_like(a, dtype=bool)
+    mask[32:64, 64:96] = True
+    assert np.array_equal(a[~mask], b[~mask])
+    assert np.array_equal(b[mask], a[mask] * 2)
+
+
+def test_linear_fp8w_pins():
+    """One-hot rows pick dequantised columns exactly; random x against torch F.linear in float64 on the torch-built
+    dequant; the block-diagonal form against a scalar loop."""
+    import torch
+    rng = np.random.default_rng(6)
+    N, K = 96, 128
+    w = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    w[(w & 0x7F) == 0x7F] = 0
+    s = rng.integers(115, 135, (3, 4), dtype=np.uint8)
+    deq = torch.from_numpy(_torch_dequant_fp8(w, s).numpy()).to(torch.bfloat16).float()
+    x = np.zeros((3, K), np.float32)
+    x[0, 5] = 1.0
+    x[1, 77] = -2.0
+    x[2, 127] = 0.5
+    got = O.linear_fp8w(x, w, s)
+    assert np.array_equal(got[0], deq[:, 5].numpy())
+    assert np.array_equal(got[1], -2 * deq[:, 77].numpy())
+    assert np.array_equal(got[2], 0.5 * deq[:, 127].numpy())
+    xr = torch.randn(4, K, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).float().numpy()
+    ref = torch.nn.functional.linear(torch.from_numpy(xr).double(), deq.double()).float().numpy()
+    assert np.array_equal(O.linear_fp8w(xr, w, s), ref)
+    gc = 32
+    G = N // gc
+    xg = torch.randn(2 * G, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).float().numpy()
+    got = O.linear_fp8w(xg, w, s, group_cols=gc)
+    d = deq.double().numpy()
+    for b in range(2):
+        for n in range(N):
+            v = float(np.dot(xg[b * G + n // gc].astype(np.float64), d[n]))
+            assert got[b, n] == np.float32(v)
