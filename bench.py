@@ -439,6 +439,60 @@ def bench_fp8_dense(torch, dev, steps, warmup):
     return out
 
 
+def bench_offload(torch, dev, n_experts=64, tokens=20, seed=23):
+    """The single-GPU offload paths on a configs[1]-shaped layer cut to `n_experts` experts held in pinned host memory
+    (offload.OffloadMoE): one-token decode by gathering the 8 selected experts over PCIe; one-token decode with half the
+    experts resident in a GPU slot table and the rest on the host library, run at the same time; and a 2048-token
+    prefill that streams every expert through GPU staging. Wall-clock per call (host syncs included: these paths sync
+    once per layer by design). PCIe-inclusive; no HBM roofline applies."""
+    import time
+    from dsv41_amd import cpumoe, moe, offload, quant
+    g = torch.Generator(device=dev).manual_seed(seed)
+    u8 = lambda *shape, lo=0, hi=256: torch.randint(lo, hi, shape, generator=g, dtype=torch.uint8, device=dev)
+    w13, s13, w2, s2 = u8(n_experts, 2 * I, H // 2), u8(n_experts, 2 * I, H // 32, lo=119, hi=124), u8(n_experts, H, I // 2), \
+        u8(n_experts, H, I // 32, lo=119, hi=124)
+    hx = offload.HostExpertWeights.of(moe.ExpertWeights(quant.tile_fp4(w13), quant.tile_fp4_scales(s13), quant.tile_fp4(w2),
+                                                        quant.tile_fp4_scales(s2), True))
+    gate_w = torch.randn(n_experts, H, generator=g, device=dev) / H ** 0.5
+    x1 = torch.randn(1, H, generator=g, device=dev).to(torch.bfloat16)
+    out = {"n_experts": n_experts, "expert_bytes": hx.expert_bytes()}
+
+    def wall(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n
+
+    layer = offload.OffloadMoE(hx, gate_w, topk=TOPK, swiglu_limit=LIMIT, device=dev)
+    t_g = wall(lambda: layer(x1), tokens)
+    out["decode_gather_us"] = round(t_g * 1e6, 1)
+    out["decode_gather_h2d_GBps"] = round(TOPK * hx.expert_bytes() / t_g / 1e9, 1)
+    if cpumoe.isa_ok():
+        cw = [t.cpu() for t in (w13, s13, w2, s2)]
+        he = cpumoe.HostExperts(n_experts, I, H)
+        he.load_layer([cw[0][e, :I] for e in range(n_experts)], [cw[0][e, I:] for e in range(n_experts)],
+                      [cw[1][e, :I] for e in range(n_experts)], [cw[1][e, I:] for e in range(n_experts)],
+                      [cw[2][e] for e in range(n_experts)], [cw[3][e] for e in range(n_experts)])
+        del cw
+        layer_c = offload.OffloadMoE(hx, gate_w, topk=TOPK, swiglu_limit=LIMIT, device=dev, host=he,
+                                     hot_ids=list(range(n_experts // 2)))
+        t_c = wall(lambda: layer_c(x1), tokens)
+        out["decode_hot_cold_us"] = round(t_c * 1e6, 1)
+        out["hot_slots"] = n_experts // 2
+        del layer_c
+        he.close()
+    xp = torch.randn(2048, H, generator=g, device=dev).to(torch.bfloat16)
+    t_p = wall(lambda: layer(xp), 2)
+    out["prefill_2048_us"] = round(t_p * 1e6, 1)
+    out["prefill_h2d_GBps"] = round(n_experts * hx.expert_bytes() / t_p / 1e9, 1)
+    del layer, hx
+    torch.cuda.empty_cache()
+    return out
+
+
 def progress(msg):
     """One line per finished phase on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -547,6 +601,8 @@ def main():
     if not args.quick:
         extra["gemv_configs0_gpu"] = bench_gemv_gpu(torch, dev, K, W)
         progress("configs[4] stack and configs[0] GEMV")
+        extra["offload"] = bench_offload(torch, dev)
+        progress("offload paths")
     if args.no_cpu:
         cpu = {"value": None, "note": "skipped"}
     else:
