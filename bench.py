@@ -493,6 +493,75 @@ def bench_offload(torch, dev, n_experts=64, tokens=20, seed=23):
     return out
 
 
+def bench_surfaces(torch, dev, layers, steps, warmup):
+    """The reference-shaped kernel surfaces called the way the reference calls them:
+      * configs[1] decode through cukern.fp4_gemm_tc (decode.py:324-327: w13 GEMM, swiglu_quant(permute), w2 GEMM, sum)
+        and through cukern.fp4_gemv_pairs (model.py:578-581), one layer per step over the rotating layer copies;
+      * configs[3] prefill through GroupedPairs + moe_kernels.grouped_fp4_gemm (model.py:583-589, block_m 64: the
+        128-pair tile kernel), stage times from HIP events."""
+    from dsv41_amd import fused, hipkern, moe_kernels, quant
+    logits = routing_stream(torch, dev, steps, 1, 7)
+    top = [torch.topk(logits[i, 0], TOPK) for i in range(steps)]
+    eids = [t.indices.to(torch.int32).contiguous() for t in top]
+    wts = [torch.softmax(t.values, 0).contiguous() for t in top]
+    xq = quant.fake_quant_fp8(torch.randn(1, H, device=dev).to(torch.bfloat16))
+    xqp = hipkern.permute_x(xq)
+    starts = torch.arange(TOPK + 1, device=dev, dtype=torch.int32)
+    tok = torch.zeros(TOPK, device=dev, dtype=torch.int32)
+    rows = torch.arange(TOPK, device=dev, dtype=torch.int32)
+    ones = torch.ones(TOPK, device=dev)
+
+    def tc_step(i):
+        ex = layers[i % len(layers)]
+        gu = hipkern.fp4_gemm_tc(xqp, ex.w13, ex.s13, eids[i], starts, tok, TOPK, 1)
+        hqp = fused.swiglu_quant(gu, wts[i], I, LIMIT, permute=True)
+        return hipkern.fp4_gemm_tc(hqp, ex.w2, ex.s2, eids[i], starts, rows, TOPK, 1, zero_out=True).sum(0)
+
+    def gp_step(i):
+        ex = layers[i % len(layers)]
+        gu = hipkern.fp4_gemv_pairs(xq, ex.w13, ex.s13, tok, eids[i], ones, TOPK, tiled=True)
+        hq = fused.swiglu_quant(gu, wts[i], I, LIMIT)
+        return hipkern.fp4_gemv_pairs(hq, ex.w2, ex.s2, rows, eids[i], ones, TOPK, tiled=True).sum(0)
+
+    out = {}
+    t, _ = graph_time(torch, tc_step, steps, warmup)
+    out["configs1_decode_fp4_gemm_tc_us"] = round(t * 1e6, 2)
+    t, _ = graph_time(torch, gp_step, steps, warmup)
+    out["configs1_decode_fp4_gemv_pairs_us"] = round(t * 1e6, 2)
+    T = 2048
+    eid_np, wt_np = zipf_routing(T, 31)
+    eid = torch.from_numpy(eid_np).to(dev).reshape(-1)
+    wt = torch.from_numpy(wt_np).to(dev).reshape(-1)
+    xp = quant.fake_quant_fp8(torch.randn(T, H, device=dev).to(torch.bfloat16))
+    P = T * TOPK
+    tokp = torch.arange(T, device=dev, dtype=torch.int32).repeat_interleave(TOPK)
+    pr = torch.arange(P, device=dev, dtype=torch.int32)
+    onesp = torch.ones(P, device=dev)
+    ex = layers[0]
+    rec = []
+    for it in range(4):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        gu = moe_kernels.grouped_fp4_gemm(xp, ex.w13, ex.s13, moe_kernels.GroupedPairs(eid, tokp, pr, onesp, 64, n_experts=E), P, tiled=True)
+        ev[1].record()
+        hq = fused.swiglu_quant(gu, wt, I, LIMIT)
+        ev[2].record()
+        y = moe_kernels.grouped_fp4_gemm(hq, ex.w2, ex.s2, moe_kernels.GroupedPairs(eid, pr, pr, onesp, 64, n_experts=E), P,
+                                         tiled=True).view(T, TOPK, H).sum(1)
+        ev[3].record()
+        torch.cuda.synchronize()
+        if it:
+            rec.append([ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3]), ev[0].elapsed_time(ev[3])])
+        del gu, hq, y
+    m = [statistics.median(c) * 1e3 for c in zip(*rec)]
+    out["configs3_prefill_grouped_fp4_gemm_us"] = {"w13_with_pairs_and_quant": round(m[0], 1), "swiglu": round(m[1], 1),
+                                                   "w2_with_pairs_quant_and_sum": round(m[2], 1), "total": round(m[3], 1)}
+    out["note"] = ("drop-in surfaces with the reference's own call sequences; the fused paths (us_per_layer, prefill_2048) "
+                   "are this build's own orchestration of the same math")
+    return out
+
+
 def progress(msg):
     """One line per finished phase on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -603,6 +672,8 @@ def main():
         progress("configs[4] stack and configs[0] GEMV")
         extra["offload"] = bench_offload(torch, dev)
         progress("offload paths")
+        extra["drop_in_surfaces"] = bench_surfaces(torch, dev, layers, min(K, 40), W)
+        progress("drop-in surfaces")
     if args.no_cpu:
         cpu = {"value": None, "note": "skipped"}
     else:

@@ -28,13 +28,15 @@ struct PrefillArgs {
     const uint8_t* S; long long stride_se;
     int N, K, E;                              // N = weight rows (MODE 0: 2 I), K = reduction length
     const int* grp_expert; const int* grp_start; int G;
-    const int* row_of_pair;                  // MODE 0: token row of sorted pair p; MODE 1: NULL (row p)
+    const int* row_of_pair;                  // input row of sorted pair p (MODE 1: NULL = row p); rows outside the
+                                             // buffer read zeros (buffer descriptors bound every activation load)
     const float* wt_sorted;                  // MODE 0: routing weight of sorted pair p
     float limit;
     uint8_t* hc; long long ldhc; uint8_t* hs; long long ldhs;   // MODE 0 outputs
     float* y; long long ldy;                                     // MODE 1 output fp32 [pairs][ldy]
     int n_cb;                                 // column blocks (MODE 0: I / 64, MODE 1: N / 128)
     int g_pad;                                // G rounded up to a multiple of 8 (XCD remap)
+    int n_pairs;                              // group ranges are clamped to [0, n_pairs)
 };
 
 // ------------------------------------------------------------------------------------------ direct-to-LDS variant
@@ -94,7 +96,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     if (g >= a.G || cb >= a.n_cb) return;
     const int e = a.grp_expert[g];
     if (e < 0 || e >= a.E) return;
-    const int p0 = a.grp_start[g], m = min(a.grp_start[g + 1] - p0, PG_T);
+    const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), m = min(min(a.grp_start[g + 1], a.n_pairs) - p0, PG_T);
     if (m <= 0) return;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -116,7 +118,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
 
     if (tid < PG_T) {
         const int p = p0 + (tid < m ? tid : 0);
-        s_row[tid] = MODE == 0 ? a.row_of_pair[p] : p;
+        // MODE 1 without a table: input row = pair slot. A row outside the buffer becomes row x_rows, whose offsets
+        // (xc_bytes, xs_bytes) are past both buffer descriptors, so its loads read zeros
+        const int r = a.row_of_pair ? a.row_of_pair[p] : p;
+        const int x_rows = (int)(a.xc_bytes / (uint32_t)a.ldx);
+        s_row[tid] = (r >= 0 && r < x_rows) ? r : x_rows;
     }
     // the routing weights of this lane's pairs (MODE 0 epilogue), fetched now so the epilogue does not wait on them
     float wgt[4];
@@ -394,7 +400,7 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
         return DSV41_EINVAL;
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W13, stride_we, S13, stride_se, 2 * I, H, E,
-                  grp_expert, grp_start, G, tok_sorted, wt_sorted, limit, hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0};
+                  grp_expert, grp_start, G, tok_sorted, wt_sorted, limit, hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0, 0x7FFFFFFF};
     return launch_prefill(a, 0, tiled, (hipStream_t)stream);
 }
 
@@ -411,7 +417,26 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
         return DSV41_EINVAL;
     if (G == 0) return 0;
     PrefillArgs a{hc, ldhc, hs, ldhs, (uint32_t)(h_rows * ldhc), (uint32_t)(h_rows * ldhs), W2, stride_we, S2, stride_se, H, I, E,
-                  grp_expert, grp_start, G, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0};
+                  grp_expert, grp_start, G, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0, h_rows};
+    return launch_prefill(a, 1, tiled, (hipStream_t)stream);
+}
+
+extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const int* row_of_pair,
+                                           const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled, int E, int N,
+                                           int K, const int* grp_expert, const int* grp_start, int G, int n_pairs, float* y, long long ldy,
+                                           void* stream) {
+    if (!xc || !xs || !W || !S || !grp_expert || !grp_start || !y || n_pairs < 0) return DSV41_EINVAL;
+    if (!row_of_pair && n_pairs > x_rows) return DSV41_EINVAL;   // without a table, pair p reads input row p
+    if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
+    if (E < 1 || N <= 0 || (N & 255) || K < 128 * PG_PF || (K & 127) || G < 0 || ldx < K || (ldx & 15) || (((uintptr_t)xc) & 15) ||
+        ldxs < K / 32 || (ldxs & 3) || (((uintptr_t)xs) & 3) || ldy < N || (ldy & 3) || (((uintptr_t)y) & 15))
+        return DSV41_EINVAL;
+    if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
+        stride_se < (long long)N * (K / 32))
+        return DSV41_EINVAL;
+    if (G == 0) return 0;
+    PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W, stride_we, S, stride_se, N, K, E,
+                  grp_expert, grp_start, G, row_of_pair, nullptr, 0.f, nullptr, 0, nullptr, 0, y, ldy, N / 256, 0, n_pairs};
     return launch_prefill(a, 1, tiled, (hipStream_t)stream);
 }
 

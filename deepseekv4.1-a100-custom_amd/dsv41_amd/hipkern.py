@@ -63,6 +63,32 @@ def grouped_gemm_codes(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: t
     return out
 
 
+T128_MAX = 128   # pairs per group the 128-pair tile kernel computes
+
+
+def t128_ok(N: int, K: int, max_tokens: int) -> bool:
+    """Shapes for which groups of more than 16 pairs go to the 256-row x 128-pair tile kernel (the prefill w2 kernel as a
+    general grouped GEMM: the weights of a group are read once for all its pairs) instead of the 16-pair passes."""
+    return 16 < max_tokens <= T128_MAX and N % 256 == 0 and K % 128 == 0 and K >= 384
+
+
+def grouped_gemm_t128(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: torch.Tensor,
+                      grp_start: torch.Tensor, row_of_pair: torch.Tensor | None, y: torch.Tensor, n_pairs: int, tiled: bool,
+                      n_cols: int | None = None) -> torch.Tensor:
+    """y[p, :N] = codes(x)[row_of_pair[p]] . deq(W[e_g])^T for the pairs p of every group (<= 128 pairs each);
+    dsv41_fp4_grouped_gemm_t128."""
+    dev = _lib.require_cuda(xc, xs, w, s, grp_expert, grp_start, row_of_pair, y)
+    E, N, Kh = w.shape
+    N = n_cols if n_cols is not None else N
+    K = Kh * 2
+    assert w.stride(2) == 1 and w.stride(1) == Kh and s.stride(2) == 1 and s.stride(1) == K // 32
+    assert y.dtype == torch.float32 and y.stride(-1) == 1 and y.shape[0] >= n_pairs
+    _lib.call("dsv41_fp4_grouped_gemm_t128", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), xc.shape[0], _lib.ptr(row_of_pair),
+              _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 1 if tiled else 0, E, N, K, _lib.ptr(grp_expert), _lib.ptr(grp_start),
+              grp_expert.numel(), n_pairs, _lib.ptr(y), y.stride(0), _lib.stream(dev))
+    return y
+
+
 def fp4_gemv_pairs(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, row_in: torch.Tensor, expert: torch.Tensor,
                    wt: torch.Tensor, n_pairs: int, tiled: bool = False) -> torch.Tensor:
     """x: bf16 [rows_in, K]; w: uint8 [E, N, K/2]; s: uint8 [E, N, K/32]; row_in/expert: int32 [pairs];
@@ -97,8 +123,12 @@ def fp4_gemm_tc(xp: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: 
     assert out.shape[1] >= out_col + N
     xc, xs = _quant_x(xp, True)
     target = out[:, out_col:] if out_col else out
-    grouped_gemm_codes(xc, xs, w, s, grp_expert.to(torch.int32).contiguous(), grp_start.to(torch.int32).contiguous(),
-                       pair_tok.to(torch.int32).contiguous(), target, max_tokens, FP4_TILED, shard_start=shard_start,
+    ge, gs, pt = grp_expert.to(torch.int32).contiguous(), grp_start.to(torch.int32).contiguous(), pair_tok.to(torch.int32).contiguous()
+    if t128_ok(N, K, max_tokens) and shard_start == 0 and shard_n >= E:
+        # groups of up to 64 pairs (cukern.FP4_W_MAX): one weight read per group on the 128-pair tile kernel
+        grouped_gemm_t128(xc, xs, w, s, ge, gs, pt, target, n_pairs, FP4_TILED, n_cols=N)
+        return out
+    grouped_gemm_codes(xc, xs, w, s, ge, gs, pt, target, max_tokens, FP4_TILED, shard_start=shard_start,
                        shard_n=shard_n, zero_out=zero_out, n_cols=N, n_pairs=n_pairs)
     return out
 

@@ -119,6 +119,18 @@ int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, lon
                        const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                        const int* grp_start, int G, float* y2, long long ldy, void* stream);
 
+/* The w2 kernel of the prefill path as a general grouped GEMM for groups of up to 128 pairs (the 256-row x 128-pair tile
+ * kernel): for each group g (expert grp_expert[g] in [0, E), pairs grp_start[g] .. grp_start[g+1]-1, clamped to
+ * [0, n_pairs), at most the first 128 of a group are computed) and pair p: y[p][0:N] = x[row][:] . deq(W[e])^T with
+ * row = row_of_pair ? row_of_pair[p] : p (rows outside [0, x_rows) read zeros). x: E4M3 codes [x_rows][ldx] + E8M0
+ * [x_rows][ldxs]. Rows of y for pairs outside every computed group are not written. N % 256 == 0, K % 128 == 0,
+ * K >= 384. Serves moe_kernels.grouped_fp4_gemm (moe_kernels.py:127-200) and cukern.fp4_gemm_tc (cukern.py:238-276)
+ * when their groups exceed 16 pairs: the weights of a group are read once for up to 128 pairs. */
+int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const int* row_of_pair,
+                                const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled, int E, int N,
+                                int K, const int* grp_expert, const int* grp_start, int G, int n_pairs, float* y, long long ldy,
+                                void* stream);
+
 /* Combine: y[t] = sum_j y2[inv[t * topk + j]] for j ascending (model.py:589, view(n, k, dim).sum(1)), fp32 into
  * y32 and/or bf16(y + ys) into out (model.py:590-591; ys NULL: no shared expert). inv: moe_dispatch's inverse
  * permutation; an entry of -1 (a dropped pair) contributes nothing. N % 4 == 0. */

@@ -144,6 +144,76 @@ def test_grouped_fp4_gemm_atomic_rows():
     close(out.cpu().numpy(), ref, "grouped_fp4_gemm atomic")
 
 
+def test_big_groups_on_the_128_pair_tile_kernel():
+    """Groups of more than 16 pairs: cukern.fp4_gemm_tc (max_tokens 64, cukern.FP4_W_MAX) and moe_kernels.grouped_fp4_gemm
+    (block_m 64, the reference's prefill call, model.py:584-589) run on the 128-pair tile kernel; results equal the
+    textbook oracle, with repeated output rows (atomic sums), a group over the 64-pair cap split by the dispatch, and
+    dropped (out-of-range) expert ids."""
+    from dsv41_amd import hipkern, moe_kernels, quant
+    E, N, K = 6, 512, 768
+    w, s, _, _ = make_experts(E, K, N // 2, 21)
+    wtl, stl = quant.tile_fp4(w), quant.tile_fp4_scales(s)
+    X = 90
+    x = quant.fake_quant_fp8(rand_x(X, K, 22, 2.0).to(DEV))
+    rng = np.random.default_rng(23)
+    # fp4_gemm_tc: groups of 64, 40, 17 and 3 pairs over arbitrary token rows
+    sizes = [64, 40, 17, 3]
+    ge = torch.tensor([4, 0, 5, 2], dtype=torch.int32, device=DEV)
+    gs = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32), device=DEV)
+    P = int(sum(sizes))
+    tok = torch.from_numpy(rng.integers(0, X, P).astype(np.int32)).to(DEV)
+    assert hipkern.t128_ok(N, K, 64)
+    got = hipkern.fp4_gemm_tc(hipkern.permute_x(x), wtl, stl, ge, gs, tok, P, 64)
+    ref = O.grouped_gemm(bf16_vals(x), w.cpu().numpy(), s.cpu().numpy(), ge.cpu().numpy(), gs.cpu().numpy(), tok.cpu().numpy(), 4)
+    close(got.cpu().numpy(), ref, "fp4_gemm_tc 64-pair groups")
+    # grouped_fp4_gemm: 300 pairs, a popular expert (> 64 pairs: split into tiles), repeated output rows, ids out of range
+    P2 = 300
+    eid = rng.choice(E, P2, p=[0.5, 0.1, 0.1, 0.1, 0.1, 0.1]).astype(np.int32)
+    eid[[7, 100]] = [-1, E]                                                 # dropped by the dispatch
+    rin = rng.integers(0, X, P2).astype(np.int32)
+    rout = rng.integers(0, 50, P2).astype(np.int32)
+    wgt = rng.random(P2).astype(np.float32)
+    pairs = moe_kernels.GroupedPairs(torch.from_numpy(eid).to(DEV), torch.from_numpy(rin).to(DEV), torch.from_numpy(rout).to(DEV),
+                                     torch.from_numpy(wgt).to(DEV), 64, n_experts=E)
+    out = moe_kernels.grouped_fp4_gemm(x, wtl, stl, pairs, 50, tiled=True)
+    ref = np.zeros((50, N), np.float64)
+    xv, wn, sn = bf16_vals(x), w.cpu().numpy(), s.cpu().numpy()
+    for p in range(P2):
+        if 0 <= eid[p] < E:
+            ref[rout[p]] += O.gemv_pairs(xv, wn, sn, [rin[p]], [eid[p]], [wgt[p]])[0]
+    close(out.cpu().numpy(), ref, "grouped_fp4_gemm block_m 64")
+
+
+def test_t128_entry_bounds():
+    """dsv41_fp4_grouped_gemm_t128: group ranges are clamped to n_pairs, input rows outside [0, x_rows) read zeros (rows of
+    y for them are 0), rows of pairs outside every group are left untouched; shape errors return -1 before any launch."""
+    from dsv41_amd import _lib, quant
+    E, N, K = 3, 256, 384
+    w, s, _, _ = make_experts(E, K, N // 2, 31)
+    x = quant.fake_quant_fp8(rand_x(8, K, 32).to(DEV))
+    xc, xs = quant.quant_fp8_e8m0(x)
+    ge = torch.tensor([1, 2], dtype=torch.int32, device=DEV)
+    gs = torch.tensor([0, 5, 400], dtype=torch.int32, device=DEV)            # the second range runs past n_pairs
+    rows = torch.tensor([0, 3, -4, 8, 7, 1, 2, 100000], dtype=torch.int32, device=DEV)
+    y = torch.full((9, N), 5.0, device=DEV)
+    _lib.call("dsv41_fp4_grouped_gemm_t128", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), 8, _lib.ptr(rows), _lib.ptr(w),
+              w.stride(0), _lib.ptr(s), s.stride(0), 0, E, N, K, _lib.ptr(ge), _lib.ptr(gs), 2, 8, _lib.ptr(y), N, _lib.stream(DEV))
+    got = y.cpu().numpy()
+    xv, wn, sn = bf16_vals(x), w.cpu().numpy(), s.cpu().numpy()
+    for p in range(8):
+        e = 1 if p < 5 else 2
+        r = int(rows[p])
+        if 0 <= r < 8:
+            close(got[p], O.gemv_pairs(xv, wn, sn, [r], [e], [1.0])[0], f"t128 pair {p}")
+        else:
+            assert np.all(got[p] == 0.0), f"pair {p}: row {r} outside the input must read zeros"
+    assert np.all(got[8] == 5.0), "a row past n_pairs is not written"
+    bad = lambda **kw: _lib.lib().dsv41_fp4_grouped_gemm_t128(_lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), 8, _lib.ptr(rows),
+                                                              _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 0, E, kw.get("N", N),
+                                                              kw.get("K", K), _lib.ptr(ge), _lib.ptr(gs), 2, 8, _lib.ptr(y), N, _lib.stream(DEV))
+    assert bad(N=128) == -1 and bad(K=256) == -1
+
+
 # ------------------------------------------------------------------------------------------ routing
 @pytest.mark.parametrize("M,k,E,gmax", [(1, 8, 384, 64), (4, 8, 384, 64), (16, 8, 384, 64), (16, 8, 16, 4), (129, 8, 384, 64),
                                        (2048, 8, 384, 64), (4096, 8, 384, 64), (300, 6, 48, 16)])
