@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
     ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
+    ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
+                    "mixes): the attainable matrix rate the prefill kernels are measured against")
     ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
                                                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
@@ -562,6 +564,30 @@ def bench_surfaces(torch, dev, layers, steps, warmup):
     return out
 
 
+def mfma_rate(torch, dev, iters=2000):
+    """PFLOP/s of back-to-back independent block-scaled 16x16x128 MFMAs (dsv41_selftest_mfma_rate), median of 5 launches,
+    per operand mix and grid size."""
+    import ctypes
+    from dsv41_amd import _lib
+    out = torch.zeros(4, device=dev)
+    res = {"iters": iters, "peaks_PFLOPs": {"fp8": FP8_PEAK / 1e15, "mxfp4": MXFP4_PEAK / 1e15}}
+    for mode, name in ((0, "fp4xfp8"), (1, "fp8xfp8"), (2, "fp4xfp4")):
+        for blocks in (1024, 4096):
+            _lib.call("dsv41_selftest_mfma_rate", mode, blocks, 10, _lib.ptr(out), _lib.stream(dev))
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(5):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _lib.call("dsv41_selftest_mfma_rate", mode, blocks, iters, _lib.ptr(out), _lib.stream(dev))
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1) / 1e3)
+            flop = blocks * 4 * iters * 8 * 2 * 16 * 16 * 128
+            res[f"{name}_blocks{blocks}_PFLOPs"] = round(flop / statistics.median(ts) / 1e15, 3)
+    return res
+
+
 def progress(msg):
     """One line per finished phase on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -581,6 +607,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     K, W = args.steps, args.warmup
+    if args.mfma_rate:
+        print(json.dumps(mfma_rate(torch, dev)))
+        return
     if args.prefill_only:
         layers = make_layers(torch, dev, 1, 1000)
         print(json.dumps(dict(bench_prefill(torch, dev, layers[0], 2048, iters=K),

@@ -33,3 +33,38 @@ extern "C" int dsv41_selftest_mfma_bf16(const uint16_t* a, const uint16_t* b, fl
     selftest_mfma_bf16_kernel<<<1, 64, 0, (hipStream_t)stream>>>((const v8bf*)a, (const v8bf*)b, (v4f*)c);
     return (int)hipGetLastError();
 }
+
+// MFMA issue-rate probe: every lane runs `iters` rounds of 8 independent block-scaled 16x16x128 MFMAs on registers
+// (no memory traffic), so the launch time measures the matrix pipes' sustained rate for one operand-format mix.
+// mode 0: FP4 weights x FP8 activations (the expert kernels' mix), 1: FP8 x FP8, 2: FP4 x FP4.
+template <int AF, int BF>
+__global__ void __launch_bounds__(256) selftest_mfma_rate_kernel(int iters, float* out, int seed) {
+    v8i a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (seed * ((int)threadIdx.x + i)) | 0x11111111;
+        b[i] = seed ^ ((int)threadIdx.x * 7 + i);
+    }
+    if (AF == 4) { a[4] = a[5] = a[6] = a[7] = 0; }   // FP4 operands use the low 4 dwords
+    if (BF == 4) { b[4] = b[5] = b[6] = b[7] = 0; }
+    v4f c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c[j], AF, BF, 0, 127, 0, 127);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += c[j][0] + c[j][1] + c[j][2] + c[j][3];
+    if (sum == 1234.5f) out[0] = sum;   // keeps the MFMAs live; never true for these operands' finite sums in practice
+}
+
+extern "C" int dsv41_selftest_mfma_rate(int mode, int blocks, int iters, float* out, void* stream) {
+    if (!out || blocks < 1 || iters < 1 || mode < 0 || mode > 2) return DSV41_EINVAL;
+    hipStream_t st = (hipStream_t)stream;
+    if (mode == 0) selftest_mfma_rate_kernel<4, 0><<<blocks, 256, 0, st>>>(iters, out, 3);
+    else if (mode == 1) selftest_mfma_rate_kernel<0, 0><<<blocks, 256, 0, st>>>(iters, out, 3);
+    else selftest_mfma_rate_kernel<4, 4><<<blocks, 256, 0, st>>>(iters, out, 3);
+    return (int)hipGetLastError();
+}

@@ -50,6 +50,7 @@ SIGNATURES = {
     "dsv41_moe_experts_noalloc": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, P, LL, P, LL, I, I, I, F, P, P, P, LL, P, LL,
                                   P, LL, P],
     "dsv41_selftest_mfma_scale": [P, P, P, P, P, I, I, P],
+    "dsv41_selftest_mfma_rate": [I, I, I, P, P],
     "dsv41_selftest_mfma_bf16": [P, P, P, P],
 }
 

@@ -235,6 +235,12 @@ int dsv41_moe_experts_noalloc(const float* logits, long long ldl, int nparts, lo
 int dsv41_selftest_mfma_scale(const int* a, const int* b, const int* sa, const int* sb, float* c, int fmt_a, int fmt_b, void* stream);
 int dsv41_selftest_mfma_bf16(const uint16_t* a, const uint16_t* b, float* c, void* stream);
 
+/* Diagnostic: the matrix pipes' sustained rate for one operand mix (no counterpart in the reference): blocks x 256 threads
+ * each run iters rounds of 8 independent v_mfma_scale_f32_16x16x128_f8f6f4 on registers. mode 0 FP4 x FP8, 1 FP8 x FP8,
+ * 2 FP4 x FP4. FLOP per launch = blocks x 4 waves x iters x 8 x 2 x 16 x 16 x 128. out: one float, written only in a
+ * case that does not occur (keeps the work live). */
+int dsv41_selftest_mfma_rate(int mode, int blocks, int iters, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
