@@ -108,10 +108,10 @@ def routing_stream(torch, dev, steps, M, seed):
 
 
 def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode="fused", seed=7):
-    """One decode layer per step over the rotating layer copies; shared: list of bf16 SharedExpert copies, rotated with
-    the layers, computed inside the two decode launches ("fused") or as its own launches first ("separate"), or of
-    (w8.W8 w13, w8.W8 w2) FP8 copies run as two FP8 GEMMs and a SwiGLU first ("fp8"). Returns (seconds per step, mean
-    unique experts per step)."""
+    """One decode layer per step over the rotating layer copies; shared: list of SharedExpert copies (bf16 or FP8),
+    rotated with the layers, computed inside the two decode launches ("fused") or, bf16, as its own launches first
+    ("separate"), or of (w8.W8 w13, w8.W8 w2) FP8 copies run as two FP8 GEMMs and a SwiGLU first ("fp8"). Returns
+    (seconds per step, mean unique experts per step)."""
     from dsv41_amd import moe, quant
     logits = routing_stream(torch, dev, steps, M, seed)
     gx = torch.Generator(device=dev).manual_seed(seed + 1)
@@ -667,9 +667,12 @@ def main():
                           torch.randint(118, 122, (H // 32, I // 32), generator=g, dtype=torch.uint8, device=dev)))
                    for _ in range(N_COPIES)]
         t_fp8, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared8, shared_mode="fp8")
-        extra["shared_expert"]["layer_us_fp8_weights"] = round(t_fp8 * 1e6, 2)
-        extra["shared_expert"]["us_added_fp8_weights"] = round((t_fp8 - t_routed) * 1e6, 2)
-        extra["shared_expert"]["fp8_bytes"] = 3 * I * H + 3 * (I // 32) * (H // 32)
+        t_fp8f, _ = bench_decode(torch, dev, layers, K, W, 1, shared=[moe.SharedExpert.of(p) for p in shared8], shared_mode="fused")
+        fp8_bytes = 3 * I * H + 3 * (I // 32) * (H // 32)
+        extra["shared_expert"].update({"fp8_bytes": fp8_bytes, "layer_us_fp8_fused": round(t_fp8f * 1e6, 2),
+                                       "us_added_fp8_fused": round((t_fp8f - t_routed) * 1e6, 2),
+                                       "layer_TBps_fp8_fused": round((sel_bytes + fp8_bytes) / t_fp8f / 1e12, 3),
+                                       "layer_us_fp8_separate": round(t_fp8 * 1e6, 2), "us_added_fp8_separate": round((t_fp8 - t_routed) * 1e6, 2)})
         del shared8
         progress("layer with shared expert")
         extra["fp8_dense_gemv"] = bench_fp8_dense(torch, dev, K, W)

@@ -252,6 +252,27 @@ __device__ __forceinline__ int buffer_load_byte(__amdgpu_buffer_rsrc_t r, uint32
 #define DSV41_PF_UP 8
 #endif
 
+// ------------------------------------------------------------------------------------------ E4M3 weights -> bf16 MFMA operands
+typedef __bf16 v8bf16_t __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf16_t __attribute__((ext_vector_type(2)));
+
+// 16 E4M3 bytes -> two bf16x8 MFMA operands (bytes 0..7, 8..15), each value times the scale `sc` (a power of two:
+// E4M3 x 2^e has at most 4 significant bits, so the product is exact in bf16 over its normal range)
+__device__ __forceinline__ void decode16(const v4i w, float sc, v8bf16_t& lo, v8bf16_t& hi) {
+    const v2bf16_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.x, sc, false);
+    const v2bf16_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.x, sc, true);
+    const v2bf16_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.y, sc, false);
+    const v2bf16_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.y, sc, true);
+    const v2bf16_t q0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.z, sc, false);
+    const v2bf16_t q1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.z, sc, true);
+    const v2bf16_t q2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.w, sc, false);
+    const v2bf16_t q3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.w, sc, true);
+    lo = __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+    hi = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3), __builtin_shufflevector(q2, q3, 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // ------------------------------------------------------------------------------------------ load pipeline
 // Software pipeline over n iterations with PF register slots: load(slot, it) fills a slot, use(slot) consumes
 // it. The steady-state loop has no guards (every load in bounds); only the peeled drain has uniform (scalar)

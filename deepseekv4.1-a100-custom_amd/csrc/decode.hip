@@ -41,6 +41,9 @@ struct DecodeUpArgs {
     // blocks of Ws13 (2 I rows, bf16 [2I][ldws]), each over the full K; gus = bf16(x . Ws13^T) [M][ldgus]
     const uint16_t* Ws13; long long ldws; uint16_t* gus; long long ldgus; int sh_y;
     int sh_tiled;   // Ws13 in 16 x 32 tiles of 1 KiB ([2I/16][H/32][16][32], ldws = H) instead of row-major
+    // SH == 2: the shared expert's [w1; w3] is FP8 E4M3 (Ws13 read as bytes, ldws = H bytes per row) in the w8 tile
+    // order [2I/16][H/64][4][16][16 B], with E8M0 scales Ss13 [2I/32][ldss] per 32 x 32 block
+    const uint8_t* Ss13; long long ldss;
 };
 
 // One 16-row block of the shared expert's [w1; w3] (bf16) over the full K for M tokens: the 8 waves split K into
@@ -85,6 +88,52 @@ __device__ __forceinline__ void shared_up_unit(const DecodeUpArgs& a, v4f (*s_re
     o[3] = (uint16_t)f32_to_bf16_bits(sum.w);
 }
 
+// The same unit for an FP8 shared expert: 64-k chunks of 1 KiB (lane l holds row l % 16, k 16 (l / 16) .. +15), each
+// decoded with its 32 x 32 block's scale into two bf16 MFMA operands (decode16: exact), against the token rows at the
+// same k. Gate/up are stored rounded to bf16, as linear_w's FP8 GEMM returns them (w8.py:102-113).
+template <int PF>
+__device__ __forceinline__ void shared_up_unit_fp8(const DecodeUpArgs& a, v4f (*s_red)[64]) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.y * gridDim.x + blockIdx.x;            // 16-row block of Ws13
+    const int nc = a.H >> 6;                                        // 64-k chunks
+    const int c0 = nc * wave / UP_WAVES, c1 = nc * (wave + 1) / UP_WAVES;
+    const int col = lane & 15, kb = lane >> 4;
+    const uint8_t* W = (const uint8_t*)a.Ws13;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(W + (long long)rb * 16 * a.ldws, (uint32_t)(16 * a.ldws));
+    const uint32_t wv = (uint32_t)lane * 16u + (uint32_t)c0 * 1024u;
+    const bool ok = col < a.M;                                      // columns past the tokens read row 0, unused
+    const uint16_t* xr = a.x + (long long)(ok ? col : 0) * a.ldx + kb * 16 + (long long)c0 * 64;
+    const uint8_t* sr = a.Ss13 + (long long)(rb >> 1) * a.ldss + 2 * c0 + (kb >> 1);
+    v4i A[PF], X0[PF], X1[PF];
+    int SB[PF];
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    pipelined<PF>(c1 - c0,
+        [&](int slot, int c) {
+            A[slot] = buffer_load_tile(wr, wv, (uint32_t)c * 1024u);
+            SB[slot] = sr[2 * c];
+            X0[slot] = *(const v4i*)(xr + (long long)c * 64);
+            X1[slot] = *(const v4i*)(xr + (long long)c * 64 + 8);
+        },
+        [&](int slot) {
+            v8bf16_t lo, hi;
+            decode16(A[slot], e8m0_to_f32((uint32_t)SB[slot]), lo, hi);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf, X0[slot]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf, X1[slot]), acc, 0, 0, 0);
+        });
+    s_red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || !ok) return;
+    v4f sum = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < UP_WAVES; ++w) sum += s_red[w][lane];
+    uint16_t* o = a.gus + (long long)col * a.ldgus + rb * 16 + 4 * kb;
+    o[0] = (uint16_t)f32_to_bf16_bits(sum.x);
+    o[1] = (uint16_t)f32_to_bf16_bits(sum.y);
+    o[2] = (uint16_t)f32_to_bf16_bits(sum.z);
+    o[3] = (uint16_t)f32_to_bf16_bits(sum.w);
+}
+
 template <int TILED, int PF, int PER, int EARLY, int SCL, int SH>
 __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const DecodeUpArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];   // staged activation rows (codes) then their E8M0 bytes
@@ -97,7 +146,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ v4f s_acc[UP_WAVES][64];
     __shared__ __align__(16) uint8_t s_wsc[SCL ? UP_WAVES * UP_WSC : 16];
     if (SH && (int)blockIdx.y < a.sh_y) {   // a shared-expert row block (uniform over the workgroup)
-        shared_up_unit<8>(a, s_acc);
+        if (SH == 2) shared_up_unit_fp8<6>(a, s_acc);
+        else shared_up_unit<8>(a, s_acc);
         return;
     }
 
@@ -509,7 +559,8 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
                             long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                             int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                             int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
-                            const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream) {
+                            const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, const uint8_t* Ss13,
+                            long long ldss13, void* stream) {
     if ((!logits && (!eid_in || !wt_in)) || !x || !W13 || !S13 || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || !wt_sorted)
         return DSV41_EINVAL;
     if (M < 1 || M > UP_MAXM || topk < 1 || topk > UP_MAXK || topk > E || E < 1 || E > UP_MAXE || score_func < 0 || score_func > 2)
@@ -520,8 +571,13 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
     if (ldhc < I || ldhs < I / 32) return DSV41_EINVAL;
     // the shared expert's [w1; w3] (bf16 [2I][ldws]) and its gate/up output (bf16 [M][ldgus]): 16-row blocks addressed
     // with 32-bit offsets, 16-byte row pieces
-    if (Ws13 && (!gus || ldws < H || (ldws & 7) || (((uintptr_t)Ws13) & 15) || 16 * ldws * 2 > 0xFFFFFFFFll || ldgus < 2 * I ||
-                 (sh_tiled && ldws != H)))
+    const bool sh_fp8 = Ws13 && Ss13;
+    if (Ws13 && !sh_fp8 && (!gus || ldws < H || (ldws & 7) || (((uintptr_t)Ws13) & 15) || 16 * ldws * 2 > 0xFFFFFFFFll || ldgus < 2 * I ||
+                            (sh_tiled && ldws != H)))
+        return DSV41_EINVAL;
+    // FP8 shared expert: E4M3 bytes in the w8 tile order (ldws = H bytes per row), E8M0 [2I/32][ldss13]
+    if (sh_fp8 && (!gus || !sh_tiled || ldws != H || (((uintptr_t)Ws13) & 15) || 16LL * ldws > 0xFFFFFFFFll || ldgus < 2 * I ||
+                   ldss13 < H / 32 || (I & 15)))
         return DSV41_EINVAL;
     // one expert's weights must be addressable with 32-bit offsets, and hold 2 I rows of H / 2 bytes
     if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll ||
@@ -543,7 +599,7 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
     const int sh_y = Ws13 ? (2 * I / 16) / (I / 32) : 0;
     DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
                    stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted,
-                   Ws13, ldws, gus, ldgus, sh_y, sh_tiled};
+                   Ws13, ldws, gus, ldgus, sh_y, sh_tiled, Ss13, ldss13};
     const size_t lds = rows * row_bytes;
     const dim3 grid(I / 32, M * topk + sh_y), block(UP_WAVES * 64);
     hipStream_t st = (hipStream_t)stream;
@@ -555,7 +611,7 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
     } while (0)
 #define UP_LAUNCH(T, PER)                                                                                         \
     do {                                                                                                      \
-        if (sh_y) UP_LAUNCH_SH(T, PER, 1); else UP_LAUNCH_SH(T, PER, 0);                                      \
+        if (sh_fp8) UP_LAUNCH_SH(T, PER, 2); else if (sh_y) UP_LAUNCH_SH(T, PER, 1); else UP_LAUNCH_SH(T, PER, 0); \
     } while (0)
     if (E <= 256) { if (tiled) UP_LAUNCH(1, 4); else UP_LAUNCH(0, 4); }
     else if (E <= 384) { if (tiled) UP_LAUNCH(1, 6); else UP_LAUNCH(0, 6); }
@@ -570,8 +626,9 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
                                    long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                                    int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                                    int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
-                                   const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream) {
+                                   const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, const uint8_t* Ss13,
+                                   long long ldss13, void* stream) {
     return decode_up_launch(logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, x, ldx, W13,
                             stride_we, S13, stride_se, tiled, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start,
-                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, stream);
+                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, Ss13, ldss13, stream);
 }

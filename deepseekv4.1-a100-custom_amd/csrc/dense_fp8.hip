@@ -21,9 +21,6 @@
 // made each such workgroup cost microseconds.
 #include "common.h"
 
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-
 struct Fp8Args {
     const uint8_t* W; long long ldw;     // bytes per row (natural layout); tiled: ldw == K
     const uint8_t* S; long long lds;     // E8M0 row stride in bytes (one row per 32 weight rows)
@@ -34,22 +31,6 @@ struct Fp8Args {
     float* out; long long ldo;           // optional fp32 [M][ldo]
     uint16_t* outb; long long ldob;      // optional bf16 [M][ldob]
 };
-
-// 16 E4M3 bytes -> two bf16x8 MFMA operands (bytes 0..7, 8..15), each value times the scale `sc`
-__device__ __forceinline__ void decode16(const v4i w, float sc, v8bf& lo, v8bf& hi) {
-    const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.x, sc, false);
-    const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.x, sc, true);
-    const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.y, sc, false);
-    const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.y, sc, true);
-    const v2bf q0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.z, sc, false);
-    const v2bf q1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.z, sc, true);
-    const v2bf q2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.w, sc, false);
-    const v2bf q3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((uint32_t)w.w, sc, true);
-    lo = __builtin_shufflevector(__builtin_shufflevector(p0, p1, 0, 1, 2, 3), __builtin_shufflevector(p2, p3, 0, 1, 2, 3),
-                                 0, 1, 2, 3, 4, 5, 6, 7);
-    hi = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3), __builtin_shufflevector(q2, q3, 0, 1, 2, 3),
-                                 0, 1, 2, 3, 4, 5, 6, 7);
-}
 
 template <int MT>
 __device__ __forceinline__ void fp8_store(const Fp8Args& a, const v4f (&sum)[MT], int n0, int r) {
@@ -104,12 +85,12 @@ __global__ void __launch_bounds__(WPG * 64) fp8_gemm_kernel(const Fp8Args a) {
             }
         },
         [&](int s) {
-            v8bf lo, hi;
+            v8bf16_t lo, hi;
             decode16(A[s], e8m0_to_f32((uint32_t)SB[s]), lo, hi);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf, X[s][mt][0]), acc[mt], 0, 0, 0);
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf, X[s][mt][1]), acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf16_t, X[s][mt][0]), acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf16_t, X[s][mt][1]), acc[mt], 0, 0, 0);
             }
         });
 #pragma unroll
@@ -188,11 +169,11 @@ __device__ __forceinline__ v4f fp8_lds_wave(const Fp8Args& a, int cpw, uint8_t* 
     pipeline_finish<P>(n,
         [&](int s, int c) { A[s] = __builtin_nontemporal_load((const v4i*)(wp + (long long)c * wstep)); },
         [&](int s) {
-            v8bf lo, hi;
+            v8bf16_t lo, hi;
             decode16(A[s], e8m0_to_f32((uint32_t)st[2 * ci]), lo, hi);
             const v4i X0 = *(const v4i*)(xt + ci * 64), X1 = *(const v4i*)(xt + ci * 64 + 8);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf, X0), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf, X1), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf16_t, X0), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf16_t, X1), acc, 0, 0, 0);
             ++ci;
         });
     return acc;

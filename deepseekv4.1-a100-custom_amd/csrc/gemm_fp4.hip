@@ -188,6 +188,9 @@ struct DownSumArgs {
     // each of the 4 residual streams r_i (bf16, token t's streams at hres + 4 N t + N i) <- bf16(post[t][i] x +
     // sum_j comb[t][j][i] r_j), in place (post fp32 [M][4], comb fp32 [M][4][4])
     uint16_t* hres; const float* hpost; const float* hcomb;
+    // SH == 2: Ws2 is FP8 E4M3 (read as bytes, ldws2 = K bytes per row) in the w8 tile order [N/16][K/64][4][16][16 B],
+    // with E8M0 scales Ss2 [N/32][ldss2] per 32 x 32 block
+    const uint8_t* Ss2; long long ldss2;
 };
 
 #define DS_MAX_SLOTS 256
@@ -196,6 +199,7 @@ struct DownSumArgs {
 #define DS_HS 4          // H_LDS: h E8M0 bytes per thread (rows * K / 32 <= 2048 whenever the rows fit 60 KiB)
 #define DS_HV_SH 4       // SH: the same with the shared expert's registers beside them (at most 32 KiB of h rows)
 #define DS_SHC 7         // SH: the shared expert's 32-k chunks per wave (K / 32 <= 8 DS_SHC)
+#define DS_SHC8 5        // SH == 2 (FP8): its 64-k chunks per wave (K / 64 <= 8 DS_SHC8)
 #define DS_HS_SH 2
 #ifndef DS_PF_SH
 #define DS_PF_SH 12      // SH: weight tiles in flight per wave
@@ -460,10 +464,25 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     // SH: this wave's share of the shared expert's 32-k chunks (a contiguous range of at most DS_SHC), issued behind the
     // routed first tiles into their own registers and consumed after the routed pipeline (slots past the range read
     // zeros: offset beyond the descriptor)
-    const int shc = SH ? (K >> 5) : 0;
+    constexpr int NSH = SH == 2 ? DS_SHC8 : DS_SHC;
+    const int shc = SH == 2 ? (K >> 6) : SH ? (K >> 5) : 0;
     const int sc0 = SH ? shc * wave / DS_WAVES : 0, n_sh = SH ? shc * (wave + 1) / DS_WAVES - sc0 : 0;
-    v4i SW[SH ? DS_SHC : 1];
-    if (SH) {
+    v4i SW[SH ? NSH : 1];
+    int SWS[SH == 2 ? NSH : 1];
+    if (SH == 2) {
+        // FP8: chunk c of row block nb is the 1 KiB tile at (nb K / 64 + c) 1024, lane l's 16 bytes at 16 l (row l % 16,
+        // k 64 c + 16 (l / 16) .. +15); each lane's block scale byte travels with its tile (chunks past the range read an
+        // in-range scale: finite, and the zero tile makes the product 0)
+        const uint8_t* W2s = (const uint8_t*)a.Ws2;
+        const __amdgpu_buffer_rsrc_t s2r = buffer_rsrc(W2s + (long long)nb * 16 * a.ldws2, (uint32_t)(16 * a.ldws2));
+        const uint32_t wv2 = (uint32_t)lane * 16u + (uint32_t)sc0 * 1024u;
+        const uint8_t* ssr = a.Ss2 + (long long)(nb >> 1) * a.ldss2 + (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < NSH; ++j) {
+            SW[j] = buffer_load_tile(s2r, j < n_sh ? wv2 : 0xFFFFFFF0u, (uint32_t)j * 1024u);
+            SWS[j] = ssr[2 * min(sc0 + j, shc - 1)];
+        }
+    } else if (SH) {
         const __amdgpu_buffer_rsrc_t s2r = buffer_rsrc(a.Ws2 + (long long)nb * 16 * a.ldws2, (uint32_t)(16 * a.ldws2 * 2));
         // lane (col, kb)'s 16 bytes of chunk c: row col, k [32 c + 8 kb, +8); tiled: at 1024 c + 64 col + 16 kb
         const uint32_t cs = a.sh_tiled ? 1024u : 64u;
@@ -553,7 +572,20 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
         pipelined<PF>(total, load, use);
     }
     v4f acc_s = v4f{0.f, 0.f, 0.f, 0.f};
-    if (SH) {
+    if (SH == 2) {
+        // FP8 chunks: lane (col, kb) takes token col's h_s k [64 c + 16 kb, +16) as two bf16 operands against the decoded
+        // tile's lower and upper 8 k
+        const uint8_t* hl = hsh + (size_t)(col < a.M ? col : 0) * hss + kb * 32;
+#pragma unroll
+        for (int j = 0; j < NSH; ++j) {
+            const int c = min(sc0 + j, shc - 1);
+            v8bf16_t lo, hi;
+            decode16(SW[j], e8m0_to_f32((uint32_t)SWS[j]), lo, hi);
+            const v4i b0 = *(const v4i*)(hl + c * 128), b1 = *(const v4i*)(hl + c * 128 + 16);
+            acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf, b0), acc_s, 0, 0, 0);
+            acc_s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf, b1), acc_s, 0, 0, 0);
+        }
+    } else if (SH) {
         // the wave's shared-expert chunks: bf16 products of Ws2's 16 rows with h_s (lane (col, kb): token col's k
         // [32 c + 8 kb, +8); columns past the tokens read token 0, unused). Slots past the wave's range hold zeros and
         // read an in-range chunk of h_s (finite), so they add exactly 0.
@@ -674,16 +706,18 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
                                   float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                                   int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
                                   long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, uint16_t* hres,
-                                  const float* hpost, const float* hcomb, void* stream) {
+                                  const float* hpost, const float* hcomb, const uint8_t* Ss2, long long ldss2, void* stream) {
     if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || (!y && !yb && !ys_out && !hres)) return DSV41_EINVAL;
     if (hres && (!hpost || !hcomb || (((uintptr_t)hres) & 7))) return DSV41_EINVAL;
     // the fused shared expert: its gate/up (bf16 [M][ldgus], 2 K columns) and Ws2 (bf16 [N][ldws2], 16-byte row pieces,
     // 16-row blocks addressed with 32-bit offsets); it replaces a given ys
     const bool sh = Ws2 != nullptr;
+    const bool sh_fp8 = sh && Ss2 != nullptr;   // FP8 E4M3 Ws2 in the w8 tile order (ldws2 = K bytes), E8M0 Ss2
     if (sh && (!gus || ys || ldgus < 2LL * K || ldws2 < K || (ldws2 & 7) || (((uintptr_t)Ws2) & 15) || 16 * ldws2 * 2 > 0xFFFFFFFFll ||
                (ldgus & 7) || (((uintptr_t)gus) & 15) || (sh_tiled && ldws2 != K) || (long long)M * 4 * K > 16LL * DS_WAVES * 64 * DS_GUV ||
                (long long)M * 4 * K > (long long)sizeof(v4f) * 2 * DS_WAVES * 64 || (ys_out && ldyso < N)))
         return DSV41_EINVAL;
+    if (sh_fp8 && (!sh_tiled || ldws2 != K || (K & 63) || ldss2 < K / 32 || K / 64 > DS_SHC8 * DS_WAVES)) return DSV41_EINVAL;
     if (!sh && !y && !yb && !hres) return DSV41_EINVAL;
     // zero_row is kept in the kernel's 16-bit pair table
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16 || zero_row < 0 || zero_row > 32767)
@@ -696,7 +730,7 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     if ((y && ldy < N) || (yb && ldyb < N) || (yb && ys && ldys < N)) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, zero_row, grp_expert, grp_start, tok_sorted, n_slots, M,
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, gus, ldgus, Ws2, ldws2, limit, ys_out, ldyso, sh_tiled,
-                  hres, hpost, hcomb};
+                  hres, hpost, hcomb, Ss2, ldss2};
     hipStream_t st = (hipStream_t)stream;
     // dynamic LDS: the h rows (codes, then their E8M0 bytes) and, with the shared expert, its bf16 h_s rows
     const size_t lds_h = (size_t)(zero_row + 1) * (K + 16) + (size_t)(zero_row + 1) * (K / 32);
@@ -717,14 +751,19 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     const bool gs = !h_lds && h32 && K / 128 <= 16 && K >= 512 && (((uintptr_t)S) & 15) == 0 && (stride_se & 15) == 0 &&
                     (ldhs & 3) == 0 && (((uintptr_t)hs) & 3) == 0;
     // the fused shared expert runs with the h rows staged in LDS only, through fewer staging registers
-    if (sh && !(h_lds && K / 32 <= DS_SHC * DS_WAVES && (long long)(zero_row + 1) * (K / 16) <= DS_HV_SH * DS_WAVES * 64 &&
+    if (sh && !(h_lds && (sh_fp8 || K / 32 <= DS_SHC * DS_WAVES) && (long long)(zero_row + 1) * (K / 16) <= DS_HV_SH * DS_WAVES * 64 &&
                 (long long)(zero_row + 1) * (K / 32) <= DS_HS_SH * DS_WAVES * 64))
         return DSV41_EINVAL;
 #define DS_LAUNCH(T, PF, NK, HL, SC) moe_down_sum_kernel<T, PF, NK, HL, SC><<<grid, block, HL ? lds : 0, st>>>(a)
-#define DS_LAUNCH_SH(T, SC) moe_down_sum_kernel<T, DS_PF_SH, 0, 1, SC, 1><<<grid, block, lds, st>>>(a)
+#define DS_LAUNCH_SH(T, SC, SHV) moe_down_sum_kernel<T, DS_PF_SH, 0, 1, SC, SHV><<<grid, block, lds, st>>>(a)
+    if (sh_fp8) {
+        if (scl) { if (tiled) DS_LAUNCH_SH(1, 1, 2); else DS_LAUNCH_SH(0, 1, 2); }
+        else { if (tiled) DS_LAUNCH_SH(1, 0, 2); else DS_LAUNCH_SH(0, 0, 2); }
+        return (int)hipGetLastError();
+    }
     if (sh) {
-        if (scl) { if (tiled) DS_LAUNCH_SH(1, 1); else DS_LAUNCH_SH(0, 1); }
-        else { if (tiled) DS_LAUNCH_SH(1, 0); else DS_LAUNCH_SH(0, 0); }
+        if (scl) { if (tiled) DS_LAUNCH_SH(1, 1, 1); else DS_LAUNCH_SH(0, 1, 1); }
+        else { if (tiled) DS_LAUNCH_SH(1, 0, 1); else DS_LAUNCH_SH(0, 0, 1); }
         return (int)hipGetLastError();
     }
 #undef DS_LAUNCH_SH

@@ -77,7 +77,7 @@ extern "C" int dsv41_moe_experts_noalloc(const float* logits, long long ldl, int
     float* wt_sorted = (float*)(base + off_wt);
     int r = dsv41_moe_decode_up(logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, x, ldx,
                                 W13, stride_w13, S13, stride_s13, tiled, H, I, limit, hc, I, hs, I / 32, eid_out, wt_out, grp_expert,
-                                grp_start, tok_sorted, wt_sorted, nullptr, 0, 0, nullptr, 0, stream);
+                                grp_start, tok_sorted, wt_sorted, nullptr, 0, 0, nullptr, 0, nullptr, 0, stream);
     if (r) return r;
     // row P, left behind by an earlier call with more pairs, holds that call's h: cleared after the up projection
     // (which writes rows < P only) and before the down projection reads it; a kernel, not a memset node, so the call
@@ -86,5 +86,6 @@ extern "C" int dsv41_moe_experts_noalloc(const float* logits, long long ldl, int
     r = (int)hipGetLastError();
     if (r) return r;
     return dsv41_moe_down_sum(W2, stride_w2, S2, stride_s2, tiled, H, I, hc, I, hs, I / 32, P, grp_expert, grp_start, tok_sorted, P, M, y, ldy,
-                              ys, ldys, yb, ldyb, 0, E, nullptr, 0, nullptr, 0, 0, 0.f, nullptr, 0, nullptr, nullptr, nullptr, stream);
+                              ys, ldys, yb, ldyb, 0, E, nullptr, 0, nullptr, 0, 0, 0.f, nullptr, 0, nullptr, nullptr, nullptr, nullptr, 0,
+                              stream);
 }

@@ -61,23 +61,33 @@ class ExpertWeights:
 
 @dataclass
 class SharedExpert:
-    """The bf16 shared expert of a layer (model.py:385-387, 409-412): w13 = [w1; w3] bf16 [2I, H] (gate rows, then up
-    rows) and w2 bf16 [H, I]; `tiled`: both in the tile_bf16 layout (16 x 32 tiles of 1 KiB, one contiguous block per
-    wave-load), which the decode kernels stream faster than row-major rows."""
+    """The shared expert of a layer (model.py:385-387, 409-412): w13 = [w1; w3] [2I, H] (gate rows, then up rows) and
+    w2 [H, I]. bf16 (s13 / s2 None): `tiled` puts both in the tile_bf16 layout (16 x 32 tiles of 1 KiB, one contiguous
+    block per wave-load), which the decode kernels stream faster than row-major rows. FP8 (the checkpoint's format,
+    w8.W8): w13 / w2 hold the E4M3 bytes in the w8 tile order and s13 / s2 their E8M0 block scales."""
     w13: torch.Tensor
     w2: torch.Tensor
     tiled: bool = False
+    s13: torch.Tensor | None = None
+    s2: torch.Tensor | None = None
 
     @property
     def I(self) -> int:
         return self.w2.shape[1]
 
+    @property
+    def fp8(self) -> bool:
+        return self.s13 is not None
+
     @classmethod
     def of(cls, shared) -> "SharedExpert | None":
-        """A SharedExpert from one, or from a (w13, w2) row-major pair; None stays None."""
+        """A SharedExpert from one, from a (w13, w2) row-major bf16 pair, or from a (W8, W8) pair; None stays None."""
         if shared is None or isinstance(shared, SharedExpert):
             return shared
         w13, w2 = shared
+        from .w8 import W8
+        if isinstance(w13, W8):
+            return cls.prepare_w8(w13, w2)
         return cls(w13, w2, False)
 
     @classmethod
@@ -87,10 +97,21 @@ class SharedExpert:
         w13, w2 = w13.to(torch.bfloat16).contiguous(), w2.to(torch.bfloat16).contiguous()
         return cls(tile_bf16(w13), tile_bf16(w2), True) if tiled else cls(w13, w2, False)
 
+    @classmethod
+    def prepare_w8(cls, w13, w2) -> "SharedExpert":
+        """From W8 [w1; w3] and w2 as loaded (tiled FP8 bytes + E8M0 block scales): no copy."""
+        assert w13.tiled and w2.tiled, "the fused FP8 shared expert reads the w8 tile order"
+        return cls(w13.w8, w2.w8, True, w13.s8, w2.s8)
+
     def check(self, H: int, I: int):
-        assert self.w13.dtype == torch.bfloat16 and self.w2.dtype == torch.bfloat16
         assert tuple(self.w13.shape) == (2 * I, H) and tuple(self.w2.shape) == (H, I)
         assert self.w13.stride(1) == 1 and self.w2.stride(1) == 1
+        if self.fp8:
+            assert self.w13.dtype == torch.uint8 and self.w2.dtype == torch.uint8 and self.tiled
+            assert self.w13.is_contiguous() and self.w2.is_contiguous() and self.s13.is_contiguous() and self.s2.is_contiguous()
+            assert tuple(self.s13.shape) == ((2 * I + 31) // 32, H // 32) and tuple(self.s2.shape) == ((H + 31) // 32, I // 32)
+            return
+        assert self.w13.dtype == torch.bfloat16 and self.w2.dtype == torch.bfloat16
         if self.tiled:
             assert self.w13.is_contiguous() and self.w2.is_contiguous()
 
@@ -114,14 +135,15 @@ class _Workspace:
         self.shared = None                                          # the SharedExpert of the last decode_up, if fused
 
 
-def fused_shared_ok(M: int, k: int, I: int) -> bool:
-    """Whether the bf16 shared expert can ride in the two decode launches (dsv41_moe_down_sum's limits: the h rows,
-    their scales and M bf16 h_s rows in 60 KiB with at most 4 h vectors per thread, M I <= 4096, I / 32 <= 56 chunks);
-    otherwise it runs as its own launches."""
+def fused_shared_ok(M: int, k: int, I: int, fp8: bool = False) -> bool:
+    """Whether the shared expert can ride in the two decode launches (dsv41_moe_down_sum's limits: the h rows, their
+    scales and M bf16 h_s rows in 60 KiB with at most 4 h vectors per thread, M I <= 4096; bf16: I / 32 <= 56 chunks
+    per row block, FP8: I / 64 <= 40); otherwise it runs as its own launches."""
     P = M * k
     lds = (((P + 1) * (I + 16) + (P + 1) * (I // 32) + 15) & ~15) + M * (I + 8) * 2
+    chunks_ok = (I % 64 == 0 and I // 64 <= 5 * 8) if fp8 else I // 32 <= 7 * 8
     return (lds <= 60 * 1024 and (P + 1) * (I // 16) <= 4 * 512 and (P + 1) * (I // 32) <= 2 * 512 and M * I <= 4096 and P <= 256
-            and I // 32 <= 7 * 8)
+            and chunks_ok)
 
 
 _WS: dict = {}
@@ -168,17 +190,17 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
         eid32, wt32 = _as(eid, torch.int32), _as(wt, torch.float32)
         route = (None, ex.E, 1, 0, None, 1.0, 1.0, 0, 0, _lib.ptr(eid32), _lib.ptr(wt32))
     sh = SharedExpert.of(shared)
-    Ws13 = None
+    Ws13 = Ss13 = None
     if sh is not None:
         sh.check(H, ex.I)
-        assert fused_shared_ok(M, k, ex.I)
-        Ws13 = sh.w13
+        assert fused_shared_ok(M, k, ex.I, sh.fp8)
+        Ws13, Ss13 = sh.w13, sh.s13
     ws.shared = sh
     _lib.call("dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, H, ex.I, float(limit), _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0),
               _lib.ptr(eid_out), _lib.ptr(wt_out), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.tok_sorted),
               _lib.ptr(ws.wt_sorted), _lib.ptr(Ws13), H if Ws13 is None else Ws13.stride(0), 1 if sh is not None and sh.tiled else 0,
-              _lib.ptr(ws.gus), ws.gus.stride(0), _lib.stream(dev))
+              _lib.ptr(ws.gus), ws.gus.stride(0), _lib.ptr(Ss13), 0 if Ss13 is None else Ss13.stride(0), _lib.stream(dev))
     return ws
 
 
@@ -198,9 +220,9 @@ def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, 
     M, H = ws.M, ex.H
     y = ws.y if y32 is None else y32
     want_y = (out is None and hc is None) or y32 is not None
-    Ws2 = None
+    Ws2 = Ss2 = None
     if ws.shared is not None:
-        Ws2 = ws.shared.w2
+        Ws2, Ss2 = ws.shared.w2, ws.shared.s2
         assert ys is None
     _lib.call("dsv41_moe_down_sum", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H, ex.I,
               _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), ws.P, _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start),
@@ -208,7 +230,7 @@ def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, 
               _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.ptr(ws.gus) if Ws2 is not None else None, ws.gus.stride(0),
               _lib.ptr(Ws2), ex.I if Ws2 is None else Ws2.stride(0), 1 if Ws2 is not None and ws.shared.tiled else 0, float(limit),
               _lib.ptr(ys_out), H if ys_out is None else ys_out.stride(0), _lib.ptr(hres), _lib.ptr(hpost), _lib.ptr(hcomb),
-              _lib.stream(dev))
+              _lib.ptr(Ss2), 0 if Ss2 is None else Ss2.stride(0), _lib.stream(dev))
     if hc is not None and out is None:
         return hres
     return out if out is not None else y
@@ -221,8 +243,16 @@ def _shared_plan(xq, shared, ys, k, ex, limit, ys_out):
     if sh is None:
         return None, ys
     assert ys is None, "give either the shared expert's weights or its output"
-    if fused_shared_ok(xq.shape[0], k, ex.I):
+    if fused_shared_ok(xq.shape[0], k, ex.I, sh.fp8):
         return sh, None
+    if sh.fp8:
+        from .w8 import W8
+        w13 = W8(sh.w13, sh.s13, permuted=True, tiled=True)
+        w2 = W8(sh.w2, sh.s2, permuted=True, tiled=True)
+        y_s = shared_expert_rows(xq, w13, w2, ex.I, limit)
+        if ys_out is not None:
+            ys_out.copy_(y_s)
+        return None, y_s
     return None, shared_expert(xq, sh.w13, sh.w2, limit, ys=ys_out, tiled=sh.tiled)
 
 
@@ -512,9 +542,12 @@ class MoE:
         from .w8 import W8
         self.shared = None
         if isinstance(sh_w13, W8):
-            # FP8 shared expert (the checkpoint's format, kept as FP8): its own FP8 GEMM launches at every row count
+            # FP8 shared expert (the checkpoint's format, kept as FP8): inside the decode launches when it fits them, else
+            # (and beyond 16 tokens) its own FP8 GEMM launches
             assert isinstance(sh_w2, W8)
             self.sh_w13, self.sh_w2 = sh_w13, sh_w2
+            if sh_w13.tiled and sh_w2.tiled:
+                self.shared = SharedExpert.prepare_w8(sh_w13, sh_w2)
         else:
             self.sh_w13 = None if sh_w13 is None else sh_w13.to(torch.bfloat16).contiguous()   # [w1; w3] row-major
             self.sh_w2 = None if sh_w2 is None else sh_w2.to(torch.bfloat16).contiguous()
@@ -544,7 +577,7 @@ class MoE:
         """fp32 [T, dim] = linear_w(swiglu_quant(linear_fp8(x, sh_w13)), sh_w2) (model.py:409-412)."""
         from .quant import fake_quant_fp8
         xq = fake_quant_fp8(x.to(torch.bfloat16))
-        if x.shape[0] <= 16 and self.shared is not None:
+        if x.shape[0] <= 16 and self.shared is not None and not self.shared.fp8:
             return shared_expert(xq.contiguous(), self.shared.w13, self.shared.w2, self.swiglu_limit, tiled=self.shared.tiled).float()
         return self._shared_rows(xq).float()
 

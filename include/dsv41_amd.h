@@ -71,13 +71,16 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
  * fused.py:283-345; p2p.cu:90-132).
  * Optional bf16 shared expert (Ws13 = [w1; w3] bf16 [2I][ldws], or NULL; sh_tiled = 1: in 16 x 32 tiles of 1 KiB,
  * [2I/16][H/32][16][32] with ldws = H): the same launch also writes its gate/up gus = bf16(x . Ws13^T) as bf16
- * [M][ldgus] (linear_w(xq, sh_w13), decode.py:368), for dsv41_moe_down_sum. */
+ * [M][ldgus] (linear_w(xq, sh_w13), decode.py:368), for dsv41_moe_down_sum. With Ss13 non-NULL the shared expert is FP8
+ * (w8.W8, w8.py:57-124): Ws13 points at E4M3 bytes in the w8 tile order [2I/16][H/64][4][16][16 B] (sh_tiled = 1,
+ * ldws = H bytes) and Ss13 at its E8M0 block scales [2I/32][ldss13]; gus is the same bf16 gate/up. */
 int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
                         float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E, const uint16_t* x,
                         long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13, long long stride_se,
                         int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                         int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
-                        const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, void* stream);
+                        const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, const uint8_t* Ss13,
+                        long long ldss13, void* stream);
 
 /* Decode down projection and per-token combine: y[t][n] = sum over groups g and their pair p of token t of
  * h_p . deq(W2[e_g])[n]  (M <= 16 tokens, n_slots <= 256 group slots; slots with expert -1 are unused).
@@ -93,14 +96,17 @@ int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long lon
  * ((n_slots + 1)(K + 16 + K / 32) + 2 M (K + 8) bytes, e.g. M <= 2 at K = 1664) and M K <= 4096; else -1.
  * Optional hyper-connection post mix in the same epilogue (hres bf16 residual, token t's 4 streams at hres + 4 N t + N i;
  * hpost fp32 [M][4]; hcomb fp32 [M][4][4]; or NULL): r_i <- bf16(post[t][i] x + sum_j comb[t][j][i] r_j) with
- * x = bf16(y + ys), in place (fused2.hc_post2_, fused2.py:476-508), replacing its separate launch. */
+ * x = bf16(y + ys), in place (fused2.hc_post2_, fused2.py:476-508), replacing its separate launch.
+ * With Ss2 non-NULL the shared expert is FP8: Ws2 points at E4M3 bytes in the w8 tile order [N/16][K/64][4][16][16 B]
+ * (sh_tiled = 1, ldws2 = K bytes, K / 64 <= 40) and Ss2 at its E8M0 block scales [N/32][ldss2]. */
 int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
                        int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, int zero_row,
                        const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
                        float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
                        int shard_start, int shard_n, const uint16_t* gus, long long ldgus, const uint16_t* Ws2,
                        long long ldws2, int sh_tiled, float limit, uint16_t* ys_out, long long ldyso, uint16_t* hres,
-                       const float* hpost, const float* hcomb, void* stream);
+                       const float* hpost, const float* hcomb, const uint8_t* Ss2,
+                       long long ldss2, void* stream);
 
 /* Prefill w13 + SwiGLU: for every group g of <= 128 expert-sorted pairs (moe_dispatch tables with gmax 128),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;

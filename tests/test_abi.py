@@ -53,7 +53,8 @@ def test_invalid_arguments_are_rejected_without_launch():
     # decode down projection: h rows shorter than K (codes or scales), an output row stride below N
     p = ctypes.c_void_p(16)
     down = lambda ldh, ldhs, ldy: L.dsv41_moe_down_sum(p, 7168 * 832, p, 7168 * 52, 1, 7168, 1664, p, ldh, p, ldhs, 8, p, p, p, 8, 1,
-                                                      p, ldy, None, 7168, None, 7168, 0, 384, None, 0, None, 0, 0, 0.0, None, 0, None, None, None, None)
+                                                      p, ldy, None, 7168, None, 7168, 0, 384, None, 0, None, 0, 0, 0.0, None, 0, None, None, None,
+                                                      None, 0, None)
     assert down(1600, 52, 7168) == -1
     assert down(1664, 51, 7168) == -1
     assert down(1664, 52, 7000) == -1
@@ -88,13 +89,14 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
 
     def up(ldhc, ldhs):
         return L.dsv41_moe_decode_up(None, 0, 1, 0, None, 1.0, 1.0, 2, 1, p, p, 1, 8, 384, p, H, p, 2 * I * H // 2, p, 2 * I * H // 32,
-                                     1, H, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p, None, 0, 0, None, 0, None)
+                                     1, H, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p, None, 0, 0, None, 0, None, 0, None)
     assert up(I - 32, I // 32) == -1
     assert up(I, I // 32 - 1) == -1
 
     def down(zero_row, Ws2=None, M=1, ys=None):
         return L.dsv41_moe_down_sum(p, H * (I // 2), p, H * (I // 32), 1, H, I, p, I, p, I // 32, zero_row, p, p, p, 8, M,
-                                    p, H, ys, H, None, H, 0, 384, p if Ws2 else None, 2 * I, Ws2, I, 0, ctypes.c_float(10.0), None, H, None, None, None, None)
+                                    p, H, ys, H, None, H, 0, 384, p if Ws2 else None, 2 * I, Ws2, I, 0, ctypes.c_float(10.0), None, H, None, None, None,
+                                    None, 0, None)
     assert down(32768) == -1
     assert down(-1) == -1
     # the fused shared expert: not together with a given ys, and only while its M h_s rows fit (M I / 32 <= 128)

@@ -798,6 +798,47 @@ def test_decode_fused_shared_expert(full_layer, M, tiled):
     close(y32.cpu().numpy(), ref, f"routed part with the shared expert fused M={M}")
 
 
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_fused_fp8_shared_expert(full_layer, M):
+    """The FP8 shared expert (w8.W8 weights, the checkpoint's format) in the two decode launches: its gate/up row blocks
+    decode E4M3 tiles with their block scales into bf16 MFMA operands, its down projection likewise in every down
+    workgroup. ys against the oracle's shared expert on the dequantised weights (the decode is exact, so only the fp32
+    summation order differs), the routed part unchanged bit for bit, out = bf16(routed + ys) exactly, and ys close to
+    the W8 linear_w path's (two FP8 GEMM launches + SwiGLU)."""
+    from dsv41_amd import moe, quant, w8
+    E, H, I, ws, ex = full_layer
+    assert moe.fused_shared_ok(M, 8, I, fp8=True)
+    g = torch.Generator().manual_seed(890 + M)
+
+    def fp8_weight(n, k):
+        c = torch.randint(0, 256, (n, k), generator=g, dtype=torch.uint8)
+        c[(c & 0x7F) == 0x7F] = 0
+        c[(c & 0x78) >= 0x60] &= 0xA7            # moderate magnitudes (exponent field < 12)
+        return c, torch.randint(116, 122, ((n + 31) // 32, k // 32), generator=g, dtype=torch.uint8)
+    c13, s13 = fp8_weight(2 * I, H)
+    c2, s2 = fp8_weight(H, I)
+    W13, W2 = w8.W8(c13.to(DEV), s13.to(DEV)), w8.W8(c2.to(DEV), s2.to(DEV))
+    sh = moe.SharedExpert.of((W13, W2))
+    assert sh.fp8
+    eid, wt = rand_routing(M, E, 8, 891 + M)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 892 + M).to(DEV))
+    ed, wd = torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    y32 = torch.empty(M, H, device=DEV)
+    ys = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    moe.moe_experts(xq, ed, wd, ex, 10.0, out=out, y32=y32, shared=sh, ys_out=ys)
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    ys_ref = O.shared_expert(bf16_vals(xq), O.dequant_fp8_block(c13.numpy(), s13.numpy()), O.dequant_fp8_block(c2.numpy(), s2.numpy()),
+                             I, 10.0)
+    close(bf16_vals(ys), ys_ref, f"fused FP8 shared expert M={M}")
+    y_plain = moe.moe_experts(xq, ed, wd, ex, 10.0).clone()
+    assert torch.equal(y32, y_plain), "the routed sum changed with the FP8 shared expert fused in"
+    comp = O.f32_to_bf16_bits((y32.cpu().numpy() + bf16_vals(ys)).astype(np.float32))
+    assert np.array_equal(u16(out), comp)
+    ys_w8 = moe.shared_expert_rows(xq, W13, W2, I, 10.0)
+    close(bf16_vals(ys), bf16_vals(ys_w8), f"fused vs linear_w FP8 shared expert M={M}")
+
+
 @pytest.mark.parametrize("T", [1, 3, 40])
 def test_moe_layer_class(T):
     """model.MoE.__call__'s surface (moe.MoE): fp32 router weights, sigmoid gate with bias and route scale, FP8 x, routed
