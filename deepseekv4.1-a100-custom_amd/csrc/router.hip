@@ -8,8 +8,8 @@
 // write xn and xq = fake_quant_fp8(xn) (quant.py:34-54) for the experts and the next step: the workgroups of
 // row block 0 each write their own k range.
 // Each workgroup recomputes the rms statistics of all M rows (M x 28 KB of L2 reads, one round trip per row)
-// rather than waiting on another launch; its 16 x 512 weight tile and its slice of the norm weight are in flight
-// meanwhile, and the threads that hold its own k range of r keep it in LDS, so nothing is loaded twice.
+// rather than waiting on another launch; its 16 x 1024 weight tile is in flight meanwhile, and the threads that hold
+// its own k range of r keep it in LDS, so nothing is loaded twice.
 #include "common.h"
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -29,8 +29,7 @@ struct RouterArgs {
     uint16_t* xq; long long ldq;
 };
 
-__device__ __forceinline__ void load8(const uint16_t* p, float* f) {
-    const v4i v = *(const v4i*)p;
+__device__ __forceinline__ void unpack8(const v4i v, float* f) {
     const uint32_t w[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -39,15 +38,45 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* f) {
     }
 }
 
-// r = bf16(x + y) for 8 consecutive elements of row t (y NULL: r = x)
-__device__ __forceinline__ void load_r8(const RouterArgs& a, int t, int k, float* f) {
-    float g[8];
-    load8(a.x + (long long)t * a.ldx + k, f);
-    if (a.y) {
-        load8(a.y + (long long)t * a.ldy + k, g);
+// The x and y vectors of a thread's two 8-element pieces of row t (pieces tid and tid + 512, clamped to the row;
+// y NULL: x again, ignored), all four loads issued together.
+struct RowRaw { v4i x[2], y[2]; };
+__device__ __forceinline__ RowRaw load_row_raw(const RouterArgs& a, int t, int tid, int nvec) {
+    const uint16_t* yb = a.y ? a.y : a.x;
+    const long long ly = a.y ? a.ldy : a.ldx;
+    RowRaw r;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) f[j] = bf16_round(f[j] + g[j]);
+    for (int u = 0; u < 2; ++u) {
+        const int k = min(tid + u * RT_THREADS, nvec - 1) * 8;
+        r.x[u] = *(const v4i*)(a.x + (long long)t * a.ldx + k);
+        r.y[u] = *(const v4i*)(yb + (long long)t * ly + k);
     }
+    return r;
+}
+
+// Row t's share of this thread: r = bf16(x + y) (y NULL: r = x) of its two pieces; returns their sum of squares
+// (pieces past the row weighted 0) and keeps the pieces of this workgroup's k range in s_r.
+__device__ __forceinline__ float row_sumsq(const RouterArgs& a, const RowRaw& raw, int t, int tid, int nvec, int ks,
+                                           float (*s_r)[RT_KC]) {
+    const int nkv = RT_KC / 8;
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        float f[8], g[8];
+        unpack8(raw.x[u], f);
+        unpack8(raw.y[u], g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] = a.y ? bf16_round(f[j] + g[j]) : f[j];
+        const float m = tid + u * RT_THREADS < nvec ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += m * f[j] * f[j];
+        const int v = tid + u * RT_THREADS - ks * nkv;
+        if (v >= 0 && v < nkv) {
+            *(v4f*)&s_r[t][v * 8] = v4f{f[0], f[1], f[2], f[3]};
+            *(v4f*)&s_r[t][v * 8 + 4] = v4f{f[4], f[5], f[6], f[7]};
+        }
+    }
+    return ss;
 }
 
 __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArgs a) {
@@ -63,44 +92,31 @@ __global__ void __launch_bounds__(RT_THREADS) router_norm_kernel(const RouterArg
     const int col = lane & 15, kg = lane >> 4;
     const int k0 = ks * RT_KC + wave * 128;
 
-    // this wave's weight tile (16 rows x 128 k) goes out first: 4 loads of 16 B per lane
+    // Row 0 of r and the norm weight of this workgroup's k range (thread tid < 128 holds 8 values; NULL: ones) are
+    // L2 hits; their sum of squares is taken before the weight tiles go out. Issued behind the tiles (which come
+    // from HBM, and loads return in issue order) they kept the whole rms chain waiting on them: 5.8 -> 4.8 us.
+    const int nkv = RT_KC / 8;
+    const RowRaw row0 = load_row_raw(a, 0, tid, nvec);
+    const v4i wraw = *(const v4i*)((a.w ? a.w : a.x) + ks * RT_KC + min(tid, nkv - 1) * 8);
+    float ss0 = row_sumsq(a, row0, 0, tid, nvec, ks, s_r);
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's weight tile (16 rows x 128 k): 4 loads of 16 B per lane
     v4i A[4];
     const uint16_t* gp = a.G + (long long)(rb * 16 + col) * a.ldg + k0 + kg * 8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) A[i] = __builtin_nontemporal_load((const v4i*)(gp + i * 32));
-    // the norm weight of this workgroup's k range: thread tid < 128 holds 8 values
-    const int nkv = RT_KC / 8;
-    float wv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) wv[j] = 1.f;
-    if (a.w && tid < nkv) load8(a.w + ks * RT_KC + tid * 8, wv);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- sum of squares of r per row. A thread owns vectors tid, tid + 512, ... (at most 2 for H <= 8192);
-    // their loads are issued together (indices clamped, out-of-range vectors weighted 0), one round trip per row.
+    // ---- sum of squares of r per row (a thread owns pieces tid and tid + 512: H <= 8192), one round trip per row
     for (int t = 0; t < M; ++t) {
-        float f[2][8];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) load_r8(a, t, min(tid + u * RT_THREADS, nvec - 1) * 8, f[u]);
-        float ss = 0.f;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const float m = tid + u * RT_THREADS < nvec ? 1.f : 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) ss += m * f[u][j] * f[u][j];
-        }
-        // vectors ks * 128 .. + 127 of the row are this workgroup's k range: kept for the normalisation below
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int v = tid + u * RT_THREADS - ks * nkv;
-            if (v >= 0 && v < nkv) {
-                *(v4f*)&s_r[t][v * 8] = v4f{f[u][0], f[u][1], f[u][2], f[u][3]};
-                *(v4f*)&s_r[t][v * 8 + 4] = v4f{f[u][4], f[u][5], f[u][6], f[u][7]};
-            }
-        }
-        ss = wave_reduce_sum(ss);
+        const float ss = wave_reduce_sum(t == 0 ? ss0 : row_sumsq(a, load_row_raw(a, t, tid, nvec), t, tid, nvec, ks, s_r));
         if (lane == 0) s_ss[wave][t] = ss;
     }
-    if (tid < nkv) {   // its loads went out at entry, ahead of the rows'
+    if (tid < nkv) {
+        float wv[8];
+        unpack8(wraw, wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) wv[j] = a.w ? wv[j] : 1.f;
         *(v4f*)&s_w[tid * 8] = v4f{wv[0], wv[1], wv[2], wv[3]};
         *(v4f*)&s_w[tid * 8 + 4] = v4f{wv[4], wv[5], wv[6], wv[7]};
     }
@@ -191,6 +207,13 @@ __global__ void __launch_bounds__(RF_THREADS) router_f32w_kernel(const uint16_t*
     const int rb = blockIdx.x, ks = blockIdx.y;
     const int k0 = ks * RT_KC;
     const int col = lane & 15, kg = lane >> 4;
+    // stage the activations first (16 bytes per thread per step; rows past M are not read): they are L2 hits, and
+    // behind the weight loads they would return only after them (loads return in issue order)
+    for (int i = tid; i < M * (RT_KC / 8); i += RF_THREADS) {
+        const int t = i / (RT_KC / 8), v = i - t * (RT_KC / 8);
+        *(v4i*)&s_x[t][v * 8] = *(const v4i*)(x + (long long)t * ldx + k0 + v * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // the wave's 16 blocks of 16 k: all 16 weight loads in flight at once
     const int kw = k0 + wave * (RT_KC / (RF_THREADS / 64));
     // rows past E (the last block when E % 16 != 0) read row E - 1; their outputs are not stored
@@ -198,11 +221,6 @@ __global__ void __launch_bounds__(RF_THREADS) router_f32w_kernel(const uint16_t*
     v4f A[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) A[j] = __builtin_nontemporal_load((const v4f*)(wr + 16 * j));
-    // stage the activations (16 bytes per thread per step; rows past M are not read)
-    for (int i = tid; i < M * (RT_KC / 8); i += RF_THREADS) {
-        const int t = i / (RT_KC / 8), v = i - t * (RT_KC / 8);
-        *(v4i*)&s_x[t][v * 8] = *(const v4i*)(x + (long long)t * ldx + k0 + v * 8);
-    }
     __syncthreads();
     const uint16_t* xr = &s_x[col < M ? col : 0][wave * (RT_KC / (RF_THREADS / 64)) + 4 * kg];
     v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
