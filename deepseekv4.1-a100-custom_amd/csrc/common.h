@@ -210,6 +210,21 @@ __device__ __forceinline__ unsigned float_order_key(float f) {
 __device__ __forceinline__ v4f mfma_fp4w_fp8x(v8i a, v8i b, v4f c, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, 0, sa, 0, sb);
 }
+// The same with the two E8M0 bytes taken from byte ja of sa and byte jb of sb (the instruction's scale byte selects;
+// ja, jb must fold to constants 0..3)
+template <int JA, int JB>
+__device__ __forceinline__ v4f mfma_fp4w_fp8x_b(v8i a, v8i b, v4f c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 4, 0, JA, sa, JB, sb);
+}
+__device__ __forceinline__ v4f mfma_fp4w_fp8x_sel(int ja, int jb, v8i a, v8i b, v4f c, int sa, int sb) {
+#define MFMA_SEL(A, B) case (A) * 4 + (B): return mfma_fp4w_fp8x_b<A, B>(a, b, c, sa, sb);
+    switch (ja * 4 + jb) {
+        MFMA_SEL(0, 0) MFMA_SEL(0, 1) MFMA_SEL(0, 2) MFMA_SEL(0, 3) MFMA_SEL(1, 0) MFMA_SEL(1, 1) MFMA_SEL(1, 2) MFMA_SEL(1, 3)
+        MFMA_SEL(2, 0) MFMA_SEL(2, 1) MFMA_SEL(2, 2) MFMA_SEL(2, 3) MFMA_SEL(3, 0) MFMA_SEL(3, 1) MFMA_SEL(3, 2)
+        default: return mfma_fp4w_fp8x_b<3, 3>(a, b, c, sa, sb);
+    }
+#undef MFMA_SEL
+}
 
 // ------------------------------------------------------------------------------------------ weight tiles
 // Byte offset of lane `lane`'s 16 weight bytes for 16-row block nb, k-chunk kc (128 k), and of its scale byte.

@@ -34,9 +34,10 @@ struct PrefillArgs {
     float limit;
     uint8_t* hc; long long ldhc; uint8_t* hs; long long ldhs;   // MODE 0 outputs
     float* y; long long ldy;                                     // MODE 1 output fp32 [pairs][ldy]
-    int n_cb;                                 // column blocks (MODE 0: I / 64, MODE 1: N / 128)
+    int n_cb;                                 // column blocks (MODE 0: I / 128, MODE 1: N / 256)
     int g_pad;                                // G rounded up to a multiple of 8 (XCD remap)
     int n_pairs;                              // group ranges are clamped to [0, n_pairs)
+    int cbw, n_it;                            // column blocks per workgroup, workgroups per group (ceil(n_cb / cbw))
 };
 
 // ------------------------------------------------------------------------------------------ direct-to-LDS variant
@@ -63,7 +64,19 @@ struct PrefillArgs {
 #define PV_B 17408
 #define PV_BS 33792
 #define PV_STAGE 34304
+#ifndef PV_CBW0
+#define PV_CBW0 1   // column blocks per workgroup, w13 (MODE 0: 56 k-steps each at configs[3])
+#endif
+#ifndef PV_CBW1
+#define PV_CBW1 2   // and w2 (MODE 1: 13 k-steps each)
+#endif
 typedef __attribute__((address_space(3))) void lds_void;
+// Global-memory views for the epilogue stores inside the k-loop: through a generic pointer they would be FLAT stores,
+// which count on the LDS counter too, and the compiler would then wait for every LDS-DMA step in flight before each
+// operand read instead of only the one it needs.
+typedef __attribute__((address_space(1))) uint32_t gmem_u32;
+typedef __attribute__((address_space(1))) uint8_t gmem_u8;
+typedef __attribute__((address_space(1))) v4f gmem_v4f;
 
 __device__ __forceinline__ void wait_vm(int n) {   // s_waitcnt vmcnt(n), 0 <= n <= 20
 #define PV_W(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); break;
@@ -87,13 +100,18 @@ struct IntC {
 
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
+    // more than one column block per workgroup (the epilogue inside the k-loop) or one (the epilogue after it)
+    constexpr bool CBL = (MODE == 0 ? PV_CBW0 : PV_CBW1) > 1;
     extern __shared__ __align__(16) uint8_t smem[];   // PV_NS stages of PV_STAGE bytes
     __shared__ int s_row[PG_T];
 
     const int L = blockIdx.x;
-    const int jx = L >> 3, gi = jx / a.n_cb;
-    const int g = gi * 8 + (L & 7), cb = jx - gi * a.n_cb;
-    if (g >= a.G || cb >= a.n_cb) return;
+    const int jx = L >> 3, gi = jx / a.n_it;
+    const int g = gi * 8 + (L & 7), cbi = jx - gi * a.n_it;
+    if (g >= a.G || cbi >= a.n_it) return;
+    // this workgroup's column blocks cb0 .. cb0 + ncb - 1 of group g, one after another through one k-pipeline
+    const int cb0 = cbi * a.cbw, ncb = CBL ? min(a.cbw, a.n_cb - cb0) : 1;
+    if (ncb <= 0) return;
     const int e = a.grp_expert[g];
     if (e < 0 || e >= a.E) return;
     const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), m = min(min(a.grp_start[g + 1], a.n_pairs) - p0, PG_T);
@@ -105,11 +123,13 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     const int col = lane & 15, kb = lane >> 4;
     const int K = a.K, nk = K >> 7, Kh = K >> 1, Ks = K >> 5;
     const int I = a.N >> 1;
-    // 16-row weight block of tile slot b = 0..15 (MODE 0: slots 0-7 gate blocks, 8-15 the matching up blocks)
-    auto block_of = [&](int b) {
+    // 16-row weight block of tile slot b = 0..15 in column block cb (MODE 0: slots 0-7 gate blocks, 8-15 the
+    // matching up blocks); the next column block's blocks are PV_DNB further on
+    auto block_of = [&](int b, int cb) {
         if (MODE == 0) return b < 8 ? (cb * 128 + 16 * b) >> 4 : (I + cb * 128 + 16 * (b - 8)) >> 4;
         return cb * 16 + b;
     };
+    constexpr int PV_DNB = MODE == 0 ? 8 : 16;
     int slot_of[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) slot_of[j] = MODE == 0 ? (j < 2 ? 2 * cg + j : 8 + 2 * cg + (j - 2)) : 4 * cg + j;
@@ -134,18 +154,20 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     __syncthreads();
 
     // ---- DMA descriptors (MFMA A layout: lane l takes row l % 16, k chunk l / 16)
-    const int nbw0 = block_of(2 * wave), nbw1 = block_of(2 * wave + 1);
+    const int nbw0 = block_of(2 * wave, cb0), nbw1 = block_of(2 * wave + 1, cb0);
     auto a_off = [&](int nb) {
         return TILED ? (uint32_t)(nb * nk * 1024 + col * 64 + kb * 16) : (uint32_t)((nb * 16 + col) * Kh + kb * 16);
     };
     const uint32_t a_voff0 = a_off(nbw0), a_voff1 = a_off(nbw1);
     const int a_ks = TILED ? 1024 : 64;
+    const uint32_t a_cs = TILED ? (uint32_t)(PV_DNB * nk * 1024) : (uint32_t)(PV_DNB * 16 * Kh);   // per column block
     // weight scales of the 16 slots (64 bytes each per k-step). Tiled: a slot's 64 bytes are contiguous, so wave 0
     // fetches all 1 KB with 16 bytes per lane (lane l: slot l / 4, bytes 16 (l % 4)). Row-major: 4 bytes per row,
     // waves 0-3 fetch 4 slots each with 4 bytes per lane (lane l: slot 4 w + l / 16, row l % 16).
-    const int asb = TILED ? block_of(lane >> 2) : block_of(4 * (wave & 3) + (lane >> 4)), asr = lane & 15;
+    const int asb = TILED ? block_of(lane >> 2, cb0) : block_of(4 * (wave & 3) + (lane >> 4), cb0), asr = lane & 15;
     const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + (lane & 3) * 16) : (uint32_t)((asb * 16 + asr) * Ks);
     const int as_ks = TILED ? 64 : 4;
+    const uint32_t as_cs = TILED ? (uint32_t)(PV_DNB * nk * 64) : (uint32_t)(PV_DNB * 16 * Ks);
     // MFMA B layout of token block `wave`: half h, lane l takes pair 16 wave + l % 16, k chunk 4 h + l / 16
     // activation rows through buffer descriptors too: reads past x_rows return 0, and with no FLAT-encoded load in
     // flight the compiler's waits on the LDS operand reads stay partial instead of draining all of them
@@ -157,13 +179,15 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     const int per_step = 2 + (lda ? 1 : 0) + (ldb ? 2 : 0) + (ldbs ? 1 : 0);
     // `full` (a compile-time flag inside the k-loop): the group holds all 128 pairs, so every wave loads its token
     // block and computes all four of its blocks, and the per-step checks of tb_on / ldb drop out
-    auto issue = [&](int kc, int st, auto full_c) {
+    // k-step kc of column block cb0 + c; aso / sso: its offsets into the expert's weights and scales (kc a_ks +
+    // c a_cs, kc as_ks + c as_cs)
+    auto issue = [&](uint32_t aso, uint32_t sso, int kc, int st, auto full_c) {
         uint8_t* so = smem + st * PV_STAGE;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + 2 * wave * 1024), 16, a_voff0, (uint32_t)(kc * a_ks), 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + (2 * wave + 1) * 1024), 16, a_voff1, (uint32_t)(kc * a_ks), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + 2 * wave * 1024), 16, a_voff0, aso, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + PV_A + (2 * wave + 1) * 1024), 16, a_voff1, aso, 0, 0);
         if (lda) {
-            if (TILED) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS), 16, as_voff, (uint32_t)(kc * as_ks), 0, 0);
-            else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, (uint32_t)(kc * as_ks), 0, 0);
+            if (TILED) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS), 16, as_voff, sso, 0, 0);
+            else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + PV_AS + wave * 256), 4, as_voff, sso, 0, 0);
         }
         if (decltype(full_c)::value || ldb) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + PV_B + wave * 2048), 16, b0off, (uint32_t)(kc * 128), 0, 0);
@@ -179,25 +203,29 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
 #pragma unroll
     for (int u = 0; u < 4; ++u) tb_on[u] = 64 * ph + 16 * u < m;
     v4i OA[2][4], OB0[2][4], OB1[2][4];
-    uint8_t OSA[2][4], OSB[2][4];   // E8M0 bytes, widened at the MFMA that uses them
+    uint32_t OSA[2], OSB[2];   // E8M0 bytes of the 4 weight slots / 4 token blocks, byte j each (MFMA byte select)
     auto read_ops = [&](int kk, int r, auto full_c) {
         constexpr bool full = decltype(full_c)::value;
         const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
         if (full || tb_on[0]) {   // wave-uniform: a wave whose half of the group is empty runs no MFMA
+            uint32_t sa = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
-                OSA[r][j] = st[PV_AS + slot_of[j] * 64 + col * 4 + kb];
+                sa |= (uint32_t)st[PV_AS + slot_of[j] * 64 + col * 4 + kb] << (8 * j);
             }
+            OSA[r] = sa;
         }
+        uint32_t sb = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             if (!full && !tb_on[u]) continue;
             const uint8_t* bt = st + PV_B + (4 * ph + u) * 2048 + lofs;
             OB0[r][u] = *(const v4i*)bt;
             OB1[r][u] = *(const v4i*)(bt + 1024);
-            OSB[r][u] = st[PV_BS + (64 * ph + 16 * u + col) * 4 + kb];
+            sb |= (uint32_t)st[PV_BS + (64 * ph + 16 * u + col) * 4 + kb] << (8 * u);
         }
+        OSB[r] = sb;
     };
     v4f acc[4][4];
 #pragma unroll
@@ -212,43 +240,129 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
             const v8i bv = v8i{OB0[r][u].x, OB0[r][u].y, OB0[r][u].z, OB0[r][u].w, OB1[r][u].x, OB1[r][u].y, OB1[r][u].z, OB1[r][u].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc[j][u] = mfma_fp4w_fp8x(v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], (int)OSA[r][j], (int)OSB[r][u]);
+                acc[j][u] = mfma_fp4w_fp8x_sel(j, u, v8i{OA[r][j].x, OA[r][j].y, OA[r][j].z, OA[r][j].w, 0, 0, 0, 0}, bv, acc[j][u], (int)OSA[r], (int)OSB[r]);
         }
     };
-    // The k-loop, instantiated per value of this wave's DMA count per step (2 .. 5, fixed for the item), so the
-    // steady-state wait below is one constant s_waitcnt instead of a compare-and-branch tree on a runtime count.
+    // The tile of column block cb out of the accumulators: MODE 0 h = fq8(SwiGLU) of its 128 columns, MODE 1 the fp32
+    // y2 rows; then the accumulators restart from zero for the next column block.
+    auto epilogue = [&](int cb) __attribute__((always_inline)) {
+        if (MODE == 0) {
+            // acc[0..1][u]: gate rows of columns cb * 128 + 32 cg + 16 j + 4 kb + i (j = 0, 1); acc[2..3][u]: up rows
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (!tb_on[u]) continue;   // wave-uniform: no pair of this token block is in the group
+                const int pr = 64 * ph + 16 * u + col;
+                float h[2][4];
+                float mx = 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float gv[4] = {acc[j][u].x, acc[j][u].y, acc[j][u].z, acc[j][u].w};
+                    const float uv[4] = {acc[2 + j][u].x, acc[2 + j][u].y, acc[2 + j][u].z, acc[2 + j][u].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float gg = gv[i], uu = uv[i];
+                        if (a.limit > 0.f) {
+                            uu = fminf(fmaxf(uu, -a.limit), a.limit);
+                            gg = fminf(gg, a.limit);
+                        }
+                        float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
+                        hv = bf16_round(hv * wgt[u]);
+                        h[j][i] = hv;
+                        mx = fmaxf(mx, fabsf(hv));
+                    }
+                }
+                // the 32 columns of pair pr sit in the 4 lanes col + 16 kb: one FP8 group
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const int ex = fq8_exponent(mx);
+                if (pr < m) {
+                    const long long p = p0 + pr;
+                    const int c0 = cb * 128 + 32 * cg;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        uint32_t codes = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
+                        *(gmem_u32*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
+                    }
+                    if (kb == 0) *(gmem_u8*)(a.hs + p * a.ldhs + (c0 >> 5)) = (uint8_t)(ex + 127);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int pr = 64 * ph + 16 * u + col;
+                if (tb_on[u] && pr < m) {
+                    // rows block_of(slot_of[j], cb) * 16 + 4 kb .. = cb * 256 + 64 cg + 16 j + 4 kb ..
+                    float* o = a.y + (long long)(p0 + pr) * a.ldy + cb * 256 + 64 * cg + 4 * kb;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) *(gmem_v4f*)(o + 16 * j) = acc[j][u];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[j][u] = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    // The k-loop over the ncb x nk steps of this workgroup's column blocks (the DMA pipeline runs on across a column
+    // block's end, so the next block's first steps are in flight during the epilogue), instantiated per value of this
+    // wave's DMA count per step (2 .. 5, fixed for the item), so the steady-state wait below is one constant
+    // s_waitcnt instead of a compare-and-branch tree on a runtime count.
     auto kloop = [&](auto ps_c, auto full_c) {
         constexpr int PS = decltype(ps_c)::value;
+        const int T = ncb * nk;
         // step kk's data in LDS, visible to every wave. Issued before this point: steps 0 .. PV_NS - 1 (prologue)
-        // and one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, nk - 1) for kk = 0
-        // and min(PV_NS - 2, nk - 1 - kk) after that.
+        // and one refill per earlier sync, so the steps issued after kk number min(PV_NS - 1, T - 1) for kk = 0
+        // and min(PV_NS - 2, T - 1 - kk) after that.
         auto sync_step = [&](int kk) {
-            const int after = kk == 0 ? min(PV_NS - 1, nk - 1) : min(PV_NS - 2, nk - 1 - kk);
+            const int after = kk == 0 ? min(PV_NS - 1, T - 1) : min(PV_NS - 2, T - 1 - kk);
             if (after == PV_NS - 2) wait_vm_c<PS * (PV_NS - 2)>();
             else wait_vm(PS * after);
             __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         };
+        // the next step to issue (steps are issued in order): its k-step within the column block and its offsets
+        int ikc = 0;
+        uint32_t iao = 0, iso = 0;
+        auto issue_next = [&](int st) {
+            issue(iao, iso, ikc, st, full_c);
+            iao += a_ks;
+            iso += as_ks;
+            if (++ikc == nk) {
+                ikc = 0;
+                iao += a_cs - (uint32_t)(nk * a_ks);
+                iso += as_cs - (uint32_t)(nk * as_ks);
+            }
+        };
+        int ekc = 0, ec = 0;   // column block and k-step of the next step whose MFMAs run
+        auto step_done = [&]() {
+            if constexpr (CBL) {
+                if (++ekc == nk) { epilogue(cb0 + ec); ekc = 0; ++ec; }
+            }
+        };
 
         for (int s0 = 0; s0 < PV_NS; ++s0)
-            if (s0 < nk) issue(s0, s0, full_c);
+            if (s0 < T) issue_next(s0);
         sync_step(0);
         read_ops(0, 0, full_c);
-        for (int kk = 0; kk < nk; kk += 2) {
-            if (kk + 1 < nk) {
+        for (int kk = 0; kk < T; kk += 2) {
+            if (kk + 1 < T) {
                 sync_step(kk + 1);                                    // every wave has read step kk: refill its stage
-                if (kk + PV_NS < nk) issue(kk + PV_NS, kk % PV_NS, full_c);
+                if (kk + PV_NS < T) issue_next(kk % PV_NS);
                 read_ops(kk + 1, 1, full_c);
             }
             mfmas(0, full_c);
-            if (kk + 1 >= nk) break;
-            if (kk + 2 < nk) {
+            step_done();
+            if (kk + 1 >= T) break;
+            if (kk + 2 < T) {
                 sync_step(kk + 2);
-                if (kk + 1 + PV_NS < nk) issue(kk + 1 + PV_NS, (kk + 1) % PV_NS, full_c);
+                if (kk + 1 + PV_NS < T) issue_next((kk + 1) % PV_NS);
                 read_ops(kk + 2, 0, full_c);
             }
             mfmas(1, full_c);
+            step_done();
         }
     };
     // per_step = 2 (weight tiles) + 1 (weight scales: wave 0 tiled, waves 0-3 row-major) + 2 (a token block) + 1
@@ -265,61 +379,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
             default: kloop(IntC<5>{}, IntC<0>{}); break;
         }
     }
-    __syncthreads();
-
-    if (MODE == 0) {
-        // acc[0..1][u]: gate rows of columns cb * 128 + 32 cg + 16 j + 4 kb + i (j = 0, 1); acc[2..3][u]: up rows
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (!tb_on[u]) continue;   // wave-uniform: no pair of this token block is in the group
-            const int pr = 64 * ph + 16 * u + col;
-            float h[2][4];
-            float mx = 0.f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float gv[4] = {acc[j][u].x, acc[j][u].y, acc[j][u].z, acc[j][u].w};
-                const float uv[4] = {acc[2 + j][u].x, acc[2 + j][u].y, acc[2 + j][u].z, acc[2 + j][u].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float gg = gv[i], uu = uv[i];
-                    if (a.limit > 0.f) {
-                        uu = fminf(fmaxf(uu, -a.limit), a.limit);
-                        gg = fminf(gg, a.limit);
-                    }
-                    float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
-                    hv = bf16_round(hv * wgt[u]);
-                    h[j][i] = hv;
-                    mx = fmaxf(mx, fabsf(hv));
-                }
-            }
-            // the 32 columns of pair pr sit in the 4 lanes col + 16 kb: one FP8 group
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const int ex = fq8_exponent(mx);
-            if (pr < m) {
-                const long long p = p0 + pr;
-                const int c0 = cb * 128 + 32 * cg;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    uint32_t codes = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
-                    *(uint32_t*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
-                }
-                if (kb == 0) a.hs[p * a.ldhs + (c0 >> 5)] = (uint8_t)(ex + 127);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int pr = 64 * ph + 16 * u + col;
-            if (tb_on[u] && pr < m) {
-                float* o = a.y + (long long)(p0 + pr) * a.ldy;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) *(v4f*)(o + block_of(slot_of[j]) * 16 + 4 * kb) = acc[j][u];
-            }
-        }
-    }
+    if constexpr (!CBL) epilogue(cb0);   // one column block: the epilogue once, after the loop
 }
 
 // y[t][n] = bf16(sum_j y2[inv[t * topk + j]][n] (+ ys[t][n])), j ascending (model.py:589-591: view(n, k, dim).sum(1)
@@ -369,7 +429,9 @@ __global__ void __launch_bounds__(256) combine_pairs_kernel(const float* __restr
 
 static int launch_prefill(PrefillArgs& a, int mode, int tiled, hipStream_t st) {
     a.g_pad = (a.G + 7) & ~7;
-    const long long items = (long long)a.n_cb * a.g_pad;   // a multiple of 8
+    a.cbw = mode == 0 ? PV_CBW0 : PV_CBW1;
+    a.n_it = (a.n_cb + a.cbw - 1) / a.cbw;
+    const long long items = (long long)a.n_it * a.g_pad;   // a multiple of 8
     if (items > 0x7FFFFFFFll) return DSV41_EINVAL;
     const dim3 grid((unsigned)items), block(PG_THREADS);
     const size_t lds = (size_t)PV_NS * PV_STAGE;
