@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
     ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
+    ap.add_argument("--shared-only", choices=["bf16", "fp8"], default=None,
+                    help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
     ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
                     "mixes): the attainable matrix rate the prefill kernels are measured against")
     ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
@@ -593,6 +595,24 @@ def progress(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def make_shared_bf16(torch, dev, g):
+    """N_COPIES bf16 shared experts of configs[1]'s dims (one per layer copy, in the fused launches' tiled layout)."""
+    from dsv41_amd import moe
+    return [moe.SharedExpert.prepare((torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16),
+                                     (torch.randn(H, I, generator=g, device=dev) / I ** 0.5).to(torch.bfloat16), tiled=True)
+            for _ in range(N_COPIES)]
+
+
+def make_shared_fp8(torch, dev, g):
+    """N_COPIES shared experts as the checkpoint stores them (FP8 E4M3 with 32 x 32 E8M0 block scales, w8.W8 pairs)."""
+    from dsv41_amd import w8
+    return [(w8.W8(torch.randint(0, 256, (2 * I, H), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
+                   torch.randint(118, 122, (2 * I // 32, H // 32), generator=g, dtype=torch.uint8, device=dev)),
+             w8.W8(torch.randint(0, 256, (H, I), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
+                   torch.randint(118, 122, (H // 32, I // 32), generator=g, dtype=torch.uint8, device=dev)))
+            for _ in range(N_COPIES)]
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -623,6 +643,19 @@ def main():
         print(json.dumps({"workload": f"configs[2] decode, M = {M}", "us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                           "TBps": round(uniq * eb / t_m / 1e12, 3), "w2_bytes_per_expert": H * (I // 2) + H * (I // 32)}))
         return
+    if args.shared_only:
+        # the configs[1] layer with its shared expert inside the two decode launches, for profiling those kernels
+        from dsv41_amd import moe
+        g = torch.Generator(device=dev).manual_seed(5)
+        if args.shared_only == "bf16":
+            shared, sh_bytes = make_shared_bf16(torch, dev, g), 2 * I * H * 2 + H * I * 2
+        else:
+            shared, sh_bytes = [moe.SharedExpert.of(p) for p in make_shared_fp8(torch, dev, g)], 3 * I * H + 3 * (I // 32) * (H // 32)
+        t_l, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared, shared_mode="fused")
+        print(json.dumps({"workload": f"configs[1] decode, M = 1, {args.shared_only} shared expert in the two launches",
+                          "us": round(t_l * 1e6, 2), "bytes": TOPK * eb + sh_bytes, "TBps": round((TOPK * eb + sh_bytes) / t_l / 1e12, 3),
+                          "shared_bytes": sh_bytes}))
+        return
     sel_bytes = TOPK * eb
 
     progress("layers resident")
@@ -645,9 +678,7 @@ def main():
         # more than the 256 MB Infinity Cache holds)
         from dsv41_amd import moe
         g = torch.Generator(device=dev).manual_seed(5)
-        shared = [moe.SharedExpert.prepare((torch.randn(2 * I, H, generator=g, device=dev) / H ** 0.5).to(torch.bfloat16),
-                                           (torch.randn(H, I, generator=g, device=dev) / I ** 0.5).to(torch.bfloat16), tiled=True)
-                  for _ in range(N_COPIES)]
+        shared = make_shared_bf16(torch, dev, g)
         t_layer, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared, shared_mode="fused")
         t_sep, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared, shared_mode="separate")
         sh_bytes = 2 * I * H * 2 + H * I * 2
@@ -660,12 +691,7 @@ def main():
                                           "the routed experts; 4 rotating copies"}
         del shared
         # the same shared expert as the checkpoint stores it (FP8 E4M3, 32 x 32 E8M0 block scales, kept as w8.W8)
-        from dsv41_amd import w8
-        shared8 = [(w8.W8(torch.randint(0, 256, (2 * I, H), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
-                          torch.randint(118, 122, (2 * I // 32, H // 32), generator=g, dtype=torch.uint8, device=dev)),
-                    w8.W8(torch.randint(0, 256, (H, I), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
-                          torch.randint(118, 122, (H // 32, I // 32), generator=g, dtype=torch.uint8, device=dev)))
-                   for _ in range(N_COPIES)]
+        shared8 = make_shared_fp8(torch, dev, g)
         t_fp8, _ = bench_decode(torch, dev, layers, K, W, 1, shared=shared8, shared_mode="fp8")
         t_fp8f, _ = bench_decode(torch, dev, layers, K, W, 1, shared=[moe.SharedExpert.of(p) for p in shared8], shared_mode="fused")
         fp8_bytes = 3 * I * H + 3 * (I // 32) * (H // 32)
