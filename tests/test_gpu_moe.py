@@ -537,13 +537,15 @@ def _e4m3_values(codes, scales):
 
 @pytest.mark.parametrize("tiled", [True, False])
 @pytest.mark.parametrize("limit", [10.0, 0.0])
-def test_prefill_stages_vs_oracle(tiled, limit):
+@pytest.mark.parametrize("H", [512, 768])
+def test_prefill_stages_vs_oracle(tiled, limit, H):
     """Prefill stage by stage (T = 200 tokens, top-4 of 16 experts, expert 3 in every token: 200 pairs = two
     groups). h: the oracle's SwiGLU + fq8 of gu = x . deq(W13)^T, element for element, except where fp32
     summation order moves a value across an E4M3 rounding boundary (one code step, rare). y2: fp64 product of the
-    kernel's own h with deq(W2), tolerance of the spec. Combine: slot-ordered sum, bit-exact."""
+    kernel's own h with deq(W2), tolerance of the spec. Combine: slot-ordered sum, bit-exact. H = 768: three 256-row
+    column blocks in w2, so a workgroup taking two column blocks also meets one with a single block."""
     from dsv41_amd import moe, quant
-    E, H, I, k, T = 16, 512, 384, 4, 200
+    E, I, k, T = 16, 384, 4, 200
     ws = make_experts(E, H, I, 500 + int(tiled))
     ex = to_ex(*ws, tiled)
     eid, wt = _skewed_routing(T, E, k, 3, 7)
