@@ -56,6 +56,8 @@ def parse():
                     help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
     ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
                     "mixes): the attainable matrix rate the prefill kernels are measured against")
+    ap.add_argument("--stream-probe", action="store_true", help="only the HBM stream-rate probe: the decode byte volumes read in "
+                    "several launch shapes (and with a per-step workgroup barrier), graph-timed over rotating regions")
     ap.add_argument("--calib", action="store_true", help="also time a plain 512 MiB device copy (the reference kernel for "
                                                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
@@ -590,6 +592,40 @@ def mfma_rate(torch, dev, iters=2000):
     return res
 
 
+def stream_probe(torch, dev):
+    """What a plain read of the decode byte volumes attains (dsv41_selftest_stream): the down projection's 50.7 MB, the
+    up projection's 101.4 MB, the layer's 152.1 MB and 1 GiB, each in several launch shapes (workgroups x waves), graph-
+    timed (20 launches per graph, median of 3 replays) over rotating 160 MiB regions (640 MiB > the 256 MB Infinity
+    Cache; 1 GiB alternates two regions). sync: a workgroup barrier after every second tile, as the prefill kernels
+    synchronise each k-step. fit: t = F + bytes / R by least squares over the four volumes for one shape."""
+    from dsv41_amd import _lib
+    buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    out = torch.zeros(4, dtype=torch.int32, device=dev)
+    vols = {"down_50.7MB": 50692096, "up_101.4MB": 101384192, "layer_152.1MB": 152076288, "1GiB": 1 << 30}
+    shapes = [(256, 8), (416, 8), (448, 8), (512, 8), (1024, 8), (2048, 4)]
+    res = {"us": {}, "TBps": {}}
+    for vname, nb in vols.items():
+        tiles = nb // 1024
+        reg, nreg = (160 << 20, 4) if nb < (1 << 30) else (1 << 30, 2)
+        runs = [(b, w, 0) for b, w in shapes] + [(416, 8, 1), (512, 8, 1)]
+        for blocks, waves, sync in runs:
+            def launch(i, blocks=blocks, waves=waves, sync=sync):
+                _lib.call("dsv41_selftest_stream", buf.data_ptr() + (i % nreg) * reg, tiles, blocks, waves, sync, _lib.ptr(out), _lib.stream(dev))
+            t, _ = graph_time(torch, launch, 20, 4)
+            key = f"{vname}_{blocks}x{waves}" + ("_sync" if sync else "")
+            res["us"][key] = round(t * 1e6, 2)
+            res["TBps"][key] = round(nb / t / 1e12, 3)
+    for blocks, waves in ((416, 8), (512, 8)):
+        import numpy as np
+        xs = np.array([float(v) for v in vols.values()])
+        ys = np.array([res["us"][f"{k}_{blocks}x{waves}"] * 1e-6 for k in vols])
+        A = np.stack([np.ones_like(xs), xs], 1)
+        (F, invR), *_ = np.linalg.lstsq(A, ys, rcond=None)
+        res[f"fit_{blocks}x{waves}"] = {"F_us": round(F * 1e6, 2), "R_TBps": round(1 / invR / 1e12, 3)}
+    return res
+
+
 def progress(msg):
     """One line per finished phase on stderr (the JSON result is the only stdout line)."""
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -629,6 +665,9 @@ def main():
     K, W = args.steps, args.warmup
     if args.mfma_rate:
         print(json.dumps(mfma_rate(torch, dev)))
+        return
+    if args.stream_probe:
+        print(json.dumps({"stream_probe": stream_probe(torch, dev)}))
         return
     if args.prefill_only:
         layers = make_layers(torch, dev, 1, 1000)

@@ -68,3 +68,41 @@ extern "C" int dsv41_selftest_mfma_rate(int mode, int blocks, int iters, float* 
     else selftest_mfma_rate_kernel<4, 4><<<blocks, 256, 0, st>>>(iters, out, 3);
     return (int)hipGetLastError();
 }
+
+// HBM stream-rate probe: `blocks` workgroups of WAVES waves read `tiles` 1 KiB tiles of src once. Workgroup b takes the
+// contiguous tiles [tiles b / blocks, tiles (b + 1) / blocks); its waves interleave over them (wave j: tile j, j + WAVES,
+// ...), 8 tiles in flight per wave, with the decode kernels' nontemporal buffer loads. Every wave of a workgroup runs the
+// same number of iterations (a last iteration past the workgroup's tiles reads zeros through the descriptor bound), so
+// SYNC = 1 can add a workgroup barrier after every second tile, as the prefill kernels synchronise each k-step. out is
+// written only if the bytes XOR to one particular word (keeps the loads live).
+template <int WAVES, int SYNC>
+__global__ void __launch_bounds__(WAVES * 64) selftest_stream_kernel(const uint8_t* src, long long tiles, unsigned* out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const long long t0 = tiles * blockIdx.x / gridDim.x, t1 = tiles * (blockIdx.x + 1) / gridDim.x;
+    const int n = (int)((t1 - t0 + WAVES - 1) / WAVES);
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(src + t0 * 1024, (uint32_t)((t1 - t0) * 1024));
+    const uint32_t voff = (uint32_t)(wave * 1024 + lane * 16);
+    v4i A[8];
+    unsigned x = 0;
+    int used = 0;
+    pipelined<8>(n, [&](int slot, int i) { A[slot] = buffer_load_tile(r, voff, (uint32_t)i * (WAVES * 1024u)); },
+                 [&](int slot) {
+                     x ^= (unsigned)(A[slot].x ^ A[slot].y ^ A[slot].z ^ A[slot].w);
+                     if (SYNC && (++used & 1) == 0) __builtin_amdgcn_s_barrier();
+                 });
+    if (x == 0x9E3779B9u) out[0] = x;   // keeps the loads live (a store only if the bytes happen to XOR to this word)
+}
+
+extern "C" int dsv41_selftest_stream(const uint8_t* src, long long tiles, int blocks, int waves, int sync, unsigned* out, void* stream) {
+    if (!src || !out || tiles < 1 || blocks < 1 || (waves != 4 && waves != 8) || sync < 0 || sync > 1) return DSV41_EINVAL;
+    if ((tiles + blocks - 1) / blocks * 1024 > 0xFFFFFFFFll) return DSV41_EINVAL;   // one workgroup's bytes: 32-bit offsets
+    hipStream_t st = (hipStream_t)stream;
+    if (waves == 8) {
+        if (sync) selftest_stream_kernel<8, 1><<<blocks, 512, 0, st>>>(src, tiles, out);
+        else selftest_stream_kernel<8, 0><<<blocks, 512, 0, st>>>(src, tiles, out);
+    } else {
+        if (sync) selftest_stream_kernel<4, 1><<<blocks, 256, 0, st>>>(src, tiles, out);
+        else selftest_stream_kernel<4, 0><<<blocks, 256, 0, st>>>(src, tiles, out);
+    }
+    return (int)hipGetLastError();
+}

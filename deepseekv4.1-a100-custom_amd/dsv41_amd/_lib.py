@@ -51,6 +51,7 @@ SIGNATURES = {
                                   P, LL, P],
     "dsv41_selftest_mfma_scale": [P, P, P, P, P, I, I, P],
     "dsv41_selftest_mfma_rate": [I, I, I, P, P],
+    "dsv41_selftest_stream": [P, LL, I, I, I, P, P],
     "dsv41_selftest_mfma_bf16": [P, P, P, P],
 }
 

@@ -247,6 +247,13 @@ int dsv41_selftest_mfma_bf16(const uint16_t* a, const uint16_t* b, float* c, voi
  * case that does not occur (keeps the work live). */
 int dsv41_selftest_mfma_rate(int mode, int blocks, int iters, float* out, void* stream);
 
+/* Diagnostic: the HBM stream rate of a launch shape (no counterpart in the reference): blocks workgroups of `waves` (4 or 8)
+ * waves read `tiles` 1 KiB tiles of src once with the decode kernels' nontemporal buffer loads, 8 tiles in flight per wave;
+ * workgroup b reads the contiguous tiles [tiles b / blocks, tiles (b + 1) / blocks), its waves interleaved. sync = 1 adds a
+ * workgroup barrier after every second tile (the prefill kernels' per-k-step synchronisation). out: one word, written only
+ * if the bytes read XOR to one particular word (keeps the loads live). Bytes read per launch = 1024 tiles. */
+int dsv41_selftest_stream(const uint8_t* src, long long tiles, int blocks, int waves, int sync, unsigned* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
