@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of --prefill-only (2048: configs[3]; 16384: the probe)")
     ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
     ap.add_argument("--shared-only", choices=["bf16", "fp8"], default=None,
                     help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
@@ -592,36 +593,43 @@ def mfma_rate(torch, dev, iters=2000):
     return res
 
 
-def stream_probe(torch, dev):
-    """What a plain read of the decode byte volumes attains (dsv41_selftest_stream): the down projection's 50.7 MB, the
-    up projection's 101.4 MB, the layer's 152.1 MB and 1 GiB, each in several launch shapes (workgroups x waves), graph-
-    timed (20 launches per graph, median of 3 replays) over rotating 160 MiB regions (640 MiB > the 256 MB Infinity
-    Cache; 1 GiB alternates two regions). sync: a workgroup barrier after every second tile, as the prefill kernels
-    synchronise each k-step. fit: t = F + bytes / R by least squares over the four volumes for one shape."""
+def plain_read_us(torch, dev, buf, nbytes, blocks, waves, sync=0, steps=20):
+    """Seconds per launch of a plain read of nbytes (dsv41_selftest_stream) in one launch shape, graph-timed (steps launches
+    per graph, median of 3 replays) over rotating regions of buf: 160 MiB regions (4 of them, 640 MiB > the 256 MB
+    Infinity Cache) below 1 GiB, else two regions of nbytes."""
     from dsv41_amd import _lib
+    out = torch.zeros(4, dtype=torch.int32, device=dev)
+    reg, nreg = (160 << 20, 4) if nbytes < (1 << 30) else (nbytes, 2)
+    assert buf.numel() >= reg * nreg
+
+    def launch(i):
+        _lib.call("dsv41_selftest_stream", buf.data_ptr() + (i % nreg) * reg, nbytes // 1024, blocks, waves, sync, _lib.ptr(out), _lib.stream(dev))
+
+    t, _ = graph_time(torch, launch, steps, 4)
+    return t
+
+
+def stream_probe(torch, dev):
+    """What a plain read of the decode byte volumes attains: the down projection's 50.7 MB, the up projection's 101.4 MB,
+    the layer's 152.1 MB and 1 GiB, each in several launch shapes (workgroups x waves), plain_read_us each. sync: a
+    workgroup barrier after every second tile, as the prefill kernels synchronise each k-step. fit: t = F + bytes / R by
+    least squares over the four volumes for one shape."""
+    import numpy as np
     buf = torch.empty(2 << 30, dtype=torch.uint8, device=dev)
     buf.random_(0, 256)
-    out = torch.zeros(4, dtype=torch.int32, device=dev)
     vols = {"down_50.7MB": 50692096, "up_101.4MB": 101384192, "layer_152.1MB": 152076288, "1GiB": 1 << 30}
     shapes = [(256, 8), (416, 8), (448, 8), (512, 8), (1024, 8), (2048, 4)]
     res = {"us": {}, "TBps": {}}
     for vname, nb in vols.items():
-        tiles = nb // 1024
-        reg, nreg = (160 << 20, 4) if nb < (1 << 30) else (1 << 30, 2)
-        runs = [(b, w, 0) for b, w in shapes] + [(416, 8, 1), (512, 8, 1)]
-        for blocks, waves, sync in runs:
-            def launch(i, blocks=blocks, waves=waves, sync=sync):
-                _lib.call("dsv41_selftest_stream", buf.data_ptr() + (i % nreg) * reg, tiles, blocks, waves, sync, _lib.ptr(out), _lib.stream(dev))
-            t, _ = graph_time(torch, launch, 20, 4)
+        for blocks, waves, sync in [(b, w, 0) for b, w in shapes] + [(416, 8, 1), (512, 8, 1)]:
+            t = plain_read_us(torch, dev, buf, nb, blocks, waves, sync)
             key = f"{vname}_{blocks}x{waves}" + ("_sync" if sync else "")
             res["us"][key] = round(t * 1e6, 2)
             res["TBps"][key] = round(nb / t / 1e12, 3)
     for blocks, waves in ((416, 8), (512, 8)):
-        import numpy as np
         xs = np.array([float(v) for v in vols.values()])
         ys = np.array([res["us"][f"{k}_{blocks}x{waves}"] * 1e-6 for k in vols])
-        A = np.stack([np.ones_like(xs), xs], 1)
-        (F, invR), *_ = np.linalg.lstsq(A, ys, rcond=None)
+        (F, invR), *_ = np.linalg.lstsq(np.stack([np.ones_like(xs), xs], 1), ys, rcond=None)
         res[f"fit_{blocks}x{waves}"] = {"F_us": round(F * 1e6, 2), "R_TBps": round(1 / invR / 1e12, 3)}
     return res
 
@@ -671,8 +679,9 @@ def main():
         return
     if args.prefill_only:
         layers = make_layers(torch, dev, 1, 1000)
-        print(json.dumps(dict(bench_prefill(torch, dev, layers[0], 2048, iters=K),
-                              workload="configs[3]: 2048 tokens x top-8, Zipf(1.1) routing, full expert path")))
+        T = args.prefill_tokens
+        print(json.dumps(dict(bench_prefill(torch, dev, layers[0], T, iters=K),
+                              workload=("configs[3]: " if T == 2048 else "") + f"{T} tokens x top-8, Zipf(1.1) routing, full expert path")))
         return
     layers = make_layers(torch, dev, N_COPIES, 1000)
     eb = expert_bytes()
@@ -712,6 +721,21 @@ def main():
             "algorithmic_bytes": w13_bytes}
     extra["down_sum_us_est"] = round((t_routed - t_up) * 1e6, 2)
     progress(f"up kernel alone {t_up * 1e6:.2f} us")
+    # the floor this layer is measured against on the same box: plain reads of the two launches' byte volumes in the
+    # kernels' own launch shapes (up: 416 workgroups x 8 waves over 8 x (W13 + S13); down: 448 x 8 over 8 x (W2 + S2))
+    buf = torch.empty(640 << 20, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    w2_bytes = sel_bytes - w13_bytes
+    r_up = plain_read_us(torch, dev, buf, w13_bytes, I // 32 * TOPK, 8)
+    r_dn = plain_read_us(torch, dev, buf, w2_bytes, H // 16, 8)
+    del buf
+    extra["plain_read_floor"] = {"up_volume_us": round(r_up * 1e6, 2), "down_volume_us": round(r_dn * 1e6, 2),
+                                 "two_reads_us": round((r_up + r_dn) * 1e6, 2), "layer_over_two_reads": round((r_up + r_dn) / t_routed, 4),
+                                 "up_kernel_over_its_read": round(r_up / t_up, 4),
+                                 "note": "dsv41_selftest_stream: a bare read of the same bytes in the same launch shape, same box, "
+                                         "graph-timed over rotating regions; the layer adds routing, the down launch's table fetch, "
+                                         "the MFMAs and the reductions to two such reads"}
+    progress(f"plain reads of the two volumes {(r_up + r_dn) * 1e6:.2f} us")
     if not args.quick:
         # the bf16 shared expert, one copy per layer copy (4 x 71.6 MB: with the routed bytes between two uses of a copy,
         # more than the 256 MB Infinity Cache holds)

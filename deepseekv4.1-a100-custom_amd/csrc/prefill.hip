@@ -64,6 +64,9 @@ struct PrefillArgs {
 #define PV_B 17408
 #define PV_BS 33792
 #define PV_STAGE 34304
+#ifndef PV_PP
+#define PV_PP 1     // full groups run the ping-pong k-loop
+#endif
 #ifndef PV_CBW0
 #define PV_CBW0 1   // column blocks per workgroup, w13 (MODE 0: 56 k-steps each at configs[3])
 #endif
@@ -365,10 +368,72 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
             step_done();
         }
     };
+    // Full groups: a ping-pong k-loop. Waves 0-3 (pairs 0-63) and waves 4-7 (pairs 64-127) share the SIMDs pairwise
+    // (wave w and w + 4 on SIMD w % 4) and would otherwise run their 16 MFMAs per step at the same time and their
+    // DMA issue and operand reads at the same time. Here every step has two barriers, and waves 4-7 pass one barrier
+    // before the loop, so their barrier j meets barrier j + 1 of waves 0-3: while one half runs step k's MFMAs, the
+    // other half issues its DMA and reads step k's (or k + 1's) operands from LDS, and the matrix pipe of each SIMD
+    // serves the two halves in turn. Data of step k is complete before either half reads it: waves 0-3 wait for
+    // their own DMA of step k before their first barrier of step k, waves 4-7 for their DMA of step k + 1 before
+    // their second barrier of step k (the one that releases waves 0-3 into step k + 1). A stage is refilled only
+    // after both halves have read it (each half waits for its own LDS reads before its second barrier of the step).
+    auto kloop_pp = [&](auto ps_c) {
+        constexpr int PS = decltype(ps_c)::value;
+        const int T = ncb * nk;
+        const bool lag = ph == 1;   // wave-uniform
+        int ikc = 0;
+        uint32_t iao = 0, iso = 0;
+        auto issue_next = [&](int st) {
+            issue(iao, iso, ikc, st, IntC<1>{});
+            iao += a_ks;
+            iso += as_ks;
+            if (++ikc == nk) {
+                ikc = 0;
+                iao += a_cs - (uint32_t)(nk * a_ks);
+                iso += as_cs - (uint32_t)(nk * as_ks);
+            }
+        };
+        int ekc = 0, ec = 0;
+        auto step_done = [&]() {
+            if constexpr (CBL) {
+                if (++ekc == nk) { epilogue(cb0 + ec); ekc = 0; ++ec; }
+            }
+        };
+        // own DMA of a step complete, with `after` later steps of this wave still in flight
+        auto wait_own = [&](int after) {
+            if (after == PV_NS - 2) wait_vm_c<PS * (PV_NS - 2)>();
+            else wait_vm(PS * after);
+        };
+        auto barrier = [&]() {
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        };
+        for (int s0 = 0; s0 < PV_NS - 1; ++s0)   // steps 0 .. PV_NS - 2; step k + PV_NS - 1 is issued in step k
+            if (s0 < T) issue_next(s0);
+        if (lag) {
+            wait_own(min(PV_NS - 2, T - 1));     // own DMA of step 0
+            barrier();                        // meets the first barrier of waves 0-3
+        }
+        for (int kk = 0; kk < T; ++kk) {
+            if (!lag) wait_own(min(PV_NS - 2, T - 1 - kk));   // own DMA of step kk (steps up to kk + PV_NS - 2 issued)
+            barrier();
+            if (kk + PV_NS - 1 < T) issue_next((kk + PV_NS - 1) % PV_NS);   // the stage of step kk - 1: read by both halves
+            read_ops(kk, 0, IntC<1>{});
+            if (lag && kk + 1 < T) wait_own(min(PV_NS - 2, T - 2 - kk));   // own DMA of step kk + 1
+            __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
+            barrier();
+            mfmas(0, IntC<1>{});
+            step_done();
+        }
+        if (!lag) barrier();                  // meets the last barrier of waves 4-7
+    };
     // per_step = 2 (weight tiles) + 1 (weight scales: wave 0 tiled, waves 0-3 row-major) + 2 (a token block) + 1
     // (token scales: waves 4-5), never both scale streams in one wave: 2 .. 5; a full group loads every token
     // block (4 or 5)
-    if (m == PG_T) {
+    if (m == PG_T && PV_PP) {
+        if (per_step == 4) kloop_pp(IntC<4>{});
+        else kloop_pp(IntC<5>{});
+    } else if (m == PG_T) {
         if (per_step == 4) kloop(IntC<4>{}, IntC<1>{});
         else kloop(IntC<5>{}, IntC<1>{});
     } else {
