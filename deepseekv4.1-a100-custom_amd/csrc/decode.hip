@@ -29,6 +29,7 @@ struct DecodeUpArgs {
     const float* bias; float temp; float route_scale; int score_func; int norm;
     const int* eid_in; const float* wt_in;   // precomputed routing [M][topk] when logits is NULL
     int M, topk, E;
+    int pairs;                               // M tokens through the one-token path, one workgroup row per pair
     int rows;                                // activation rows LDS holds (members staged per pass)
     const uint16_t* x; long long ldx;        // bf16 [M][H] activations on the FP8 grid
     const uint8_t* W13; long long stride_we; const uint8_t* S13; long long stride_se;
@@ -201,11 +202,15 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     // workgroups a CU holds do not run their gates on the same SIMD
     const int gw = (int)((blockIdx.x + blockIdx.y * gridDim.x) & 3);
     const int g = (int)blockIdx.y - (SH ? a.sh_y : 0);   // this workgroup's group slot (the g-th selected expert)
+    // The one-token path also serves M tokens pair by pair (a.pairs): row g is then pair g = pick pk of token tok, whose
+    // h row is g itself (no bucketing: an expert two tokens share streams once per pair). One token: tok 0, pick g.
+    const int tok = early ? g / topk : 0, pk = early ? g - tok * topk : g;
+    const float* lrow = a.logits ? a.logits + (long long)tok * a.ldl : nullptr;
     const bool gwave = early && wave == gw;
-    if (gwave && a.logits) gr.load_logits(a.logits, E, a.nparts, a.pstride);
+    if (gwave && a.logits) gr.load_logits(lrow, E, a.nparts, a.pstride);
     const int xq = (wave - (wave > gw ? 1 : 0)) * 64 + lane;   // early: the lane's 16 values of row 0 among the stagers
     v4i xr0, xr1;
-    if (early && !gwave && xq < per_row) x_load(0, xq, xr0, xr1);
+    if (early && !gwave && xq < per_row) x_load(tok, xq, xr0, xr1);
     if (tid < UP_MAXE / 64) s_bits[tid] = 0ull;
     if (tid == 0) {
         s_pick = -2;
@@ -279,14 +284,14 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             int ki = -1;
             float kw = 0.f;   // lane k keeps pick k
             if (a.logits) {
-                gr.prepare(a.logits, a.nparts, a.pstride, a.bias, E, a.temp, a.score_func);
+                gr.prepare(lrow, a.nparts, a.pstride, a.bias, E, a.temp, a.score_func);
                 float wsum = 0.f;
                 for (int k = 0; k < topk; ++k) {
                     int id;
                     float w;
                     gr.pick(k, &id, &w);
                     wsum += w;
-                    if (k == g) {
+                    if (k == pk) {
                         eg = (id >= 0 && id < E) ? id : -1;
                         if (lane == 0) __hip_atomic_store(&s_pick, eg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                         if (eg >= 0) {
@@ -300,8 +305,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
                 kw = gate_weight(kw, wsum, a.route_scale, a.norm);
             } else {
                 if (lane < topk) {
-                    ki = a.eid_in[lane];
-                    kw = a.wt_in[lane];
+                    ki = a.eid_in[tok * topk + lane];
+                    kw = a.wt_in[tok * topk + lane];
                 }
                 eg = __builtin_amdgcn_readfirstlane(a.eid_in[g]);
                 if (!(eg >= 0 && eg < E)) eg = -1;
@@ -321,9 +326,9 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             if (kv) atomicOr(&s_bits[ki >> 6], 1ull << (ki & 63));
             const int rank = __popcll(__ballot(kv && ki < eg));
             const unsigned long long mine = __ballot(kv && ki == eg);
-            const float pw = __shfl(kw, mine ? (int)__builtin_ctzll(mine) : 0);
+            const float pw = __shfl(kw, a.pairs ? pk : (mine ? (int)__builtin_ctzll(mine) : 0));
             if (lane == 0) {
-                s_slot[0] = rank;
+                s_slot[0] = a.pairs ? g : rank;
                 s_pw[0] = pw;
             }
             if (eg >= 0) scale_store();   // its scale loads went out with the first tiles, at the pick
@@ -371,7 +376,9 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             }
         }
     }
-    const bool publish = blockIdx.x == 0 && g == 0;
+    // the tables of the down projection: one token, workgroup (0, 0) writes them all; pairs, workgroup (0, g) the entries
+    // of pair g (group g = that pair alone)
+    const bool publish = blockIdx.x == 0 && (g == 0 || a.pairs);
     int mg = 1;
     if (early) {
         if (eg < 0 && !publish) return;   // uniform: an invalid id (given routing only)
@@ -519,6 +526,21 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         }
     }
 
+    // ---- pairs: pair g's routing and table entries (group g holds pair g alone; an invalid id makes it an empty group)
+    if (publish && a.pairs) {
+        if (tid == 0) {
+            const int e = s_eid[pk];
+            const float w = s_wt[pk];
+            if (a.eid_out) a.eid_out[g] = e;
+            if (a.wt_out) a.wt_out[g] = w;
+            a.grp_expert[g] = e;
+            a.grp_start[g] = g;
+            a.tok_sorted[g] = tok;
+            a.wt_sorted[g] = w;
+            if (g == 0) a.grp_start[P] = P;
+        }
+        return;
+    }
     // ---- workgroup (0, 0) publishes the routing and the tables of the down projection (off the critical path:
     // the down projection is the next launch)
     if (publish) {
@@ -560,7 +582,7 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
                             int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs, long long ldhs,
                             int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted, float* wt_sorted,
                             const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, const uint8_t* Ss13,
-                            long long ldss13, void* stream) {
+                            long long ldss13, bool pairs, void* stream) {
     if ((!logits && (!eid_in || !wt_in)) || !x || !W13 || !S13 || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || !wt_sorted)
         return DSV41_EINVAL;
     if (M < 1 || M > UP_MAXM || topk < 1 || topk > UP_MAXK || topk > E || E < 1 || E > UP_MAXE || score_func < 0 || score_func > 2)
@@ -587,7 +609,10 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
     // M > 1: members are staged after the bucketing, up to `rows` per pass, as many as fit in 44 KiB of LDS (60 KiB
     // without the staged weight scales), so two workgroups fit per CU
     const size_t row_bytes = (size_t)(H + 16) + (size_t)(H / 32);
-    const bool early = M == 1 && H / 16 <= (UP_WAVES - 1) * 64;
+    // pairs: M tokens through the same path, one grid row per (token, pick) pair
+    if (pairs && H / 16 > (UP_WAVES - 1) * 64) return DSV41_EINVAL;
+    pairs = pairs && M > 1;
+    const bool early = (M == 1 || pairs) && H / 16 <= (UP_WAVES - 1) * 64;
     // M tokens: weight scales through LDS (16 KiB per workgroup) when a wave's stream has <= 32 k-chunks; the rows
     // then get 44 KiB, so two workgroups still fit per CU
     const bool scl = early || (H / 128 + 1) / 2 <= UP_WSC / 64;
@@ -597,7 +622,7 @@ static int decode_up_launch(const float* logits, long long ldl, int nparts, long
     // the shared expert's 2 I / 16 row blocks take sh_y = 4 extra grid rows of I / 32 workgroups, ahead of the routed
     // ones (the hardware dispatches workgroups in linear order, so their streams start first)
     const int sh_y = Ws13 ? (2 * I / 16) / (I / 32) : 0;
-    DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, rows, x, ldx, W13, stride_we, S13,
+    DecodeUpArgs a{logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, pairs ? 1 : 0, rows, x, ldx, W13, stride_we, S13,
                    stride_se, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start, tok_sorted, wt_sorted,
                    Ws13, ldws, gus, ldgus, sh_y, sh_tiled, Ss13, ldss13};
     const size_t lds = rows * row_bytes;
@@ -630,5 +655,17 @@ extern "C" int dsv41_moe_decode_up(const float* logits, long long ldl, int npart
                                    long long ldss13, void* stream) {
     return decode_up_launch(logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, x, ldx, W13,
                             stride_we, S13, stride_se, tiled, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start,
-                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, Ss13, ldss13, stream);
+                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, Ss13, ldss13, false, stream);
+}
+
+extern "C" int dsv41_moe_decode_up_pairs(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                                         float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E,
+                                         const uint16_t* x, long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13,
+                                         long long stride_se, int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs,
+                                         long long ldhs, int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted,
+                                         float* wt_sorted, const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus,
+                                         const uint8_t* Ss13, long long ldss13, void* stream) {
+    return decode_up_launch(logits, ldl, nparts, part_stride, bias, temp, route_scale, score_func, norm, eid_in, wt_in, M, topk, E, x, ldx, W13,
+                            stride_we, S13, stride_se, tiled, H, I, limit, hc, ldhc, hs, ldhs, eid_out, wt_out, grp_expert, grp_start,
+                            tok_sorted, wt_sorted, Ws13, ldws, sh_tiled, gus, ldgus, Ss13, ldss13, true, stream);
 }

@@ -31,6 +31,8 @@ SIGNATURES = {
     "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
     "dsv41_moe_decode_up": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P,
                             P, LL, I, P, LL, P, LL, P],
+    "dsv41_moe_decode_up_pairs": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P,
+                                  P, P, LL, I, P, LL, P, LL, P],
     "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, LL, P, LL, I, F, P, LL,
                            P, P, P, P, LL, P],
     "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],

@@ -165,11 +165,13 @@ def _as(t: torch.Tensor, dtype) -> torch.Tensor:
 
 
 def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=None, eid=None, wt=None, eid_out=None, wt_out=None,
-              shared=None):
+              shared=None, pairs: bool = False):
     """The first of the two decode launches (dsv41_moe_decode_up): routing (from `logits` with gate = (bias,
     temp, route_scale, score_func, norm), or the given eid / wt), bucketing, up projection and SwiGLU; with
     shared (a SharedExpert or a row-major (w13, w2) pair) also the shared expert's gate/up (decode_down finishes it).
-    Returns the workspace holding h (codes + E8M0, expert-sorted pair rows) and the tables for decode_down."""
+    Returns the workspace holding h (codes + E8M0, expert-sorted pair rows) and the tables for decode_down.
+    pairs (M > 1): the tokens pair by pair (dsv41_moe_decode_up_pairs): every (token, pick) pair is its own group and h
+    row, routed inside the launch from that token's logits (no gate launch, no bucketing)."""
     dev = _lib.require_cuda(xq, logits, eid, wt)
     M, H = xq.shape
     assert 1 <= M <= 16, "decode path: at most 16 tokens (use the prefill path beyond)"
@@ -196,7 +198,7 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
         assert fused_shared_ok(M, k, ex.I, sh.fp8)
         Ws13, Ss13 = sh.w13, sh.s13
     ws.shared = sh
-    _lib.call("dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
+    _lib.call("dsv41_moe_decode_up_pairs" if pairs else "dsv41_moe_decode_up", *route, M, k, ex.E, _lib.ptr(xq), xq.stride(0), _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, H, ex.I, float(limit), _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0),
               _lib.ptr(eid_out), _lib.ptr(wt_out), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start), _lib.ptr(ws.tok_sorted),
               _lib.ptr(ws.wt_sorted), _lib.ptr(Ws13), H if Ws13 is None else Ws13.stride(0), 1 if sh is not None and sh.tiled else 0,
@@ -273,6 +275,11 @@ def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Exper
     return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None, hc=hc)
 
 
+# largest token count routed pair by pair inside the up launch (moe_route_experts): below it the gate launch and the
+# bucketing cost more than reading the few experts two tokens share twice
+PAIRS_MAX_M = 4
+
+
 def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor | None, temp: float, topk: int, route_scale: float,
                       score_func: str, norm: bool, ex: ExpertWeights, limit: float, ys: torch.Tensor | None = None,
                       out: torch.Tensor | None = None, y32: torch.Tensor | None = None, eid_out: torch.Tensor | None = None,
@@ -281,13 +288,14 @@ def moe_route_experts(xq: torch.Tensor, logits: torch.Tensor, bias: torch.Tensor
     """gate_topk (fused2.py:418-452) with the routed experts: logits fp32 [M, E] -> routing (written to
     eid_out int32 / wt_out fp32 [M, topk] when given) -> the same outputs as moe_experts.
     M = 1: the routing runs inside the up-projection launch (every workgroup routes the one token while its
-    activations load). M > 1: one gate launch first; the up projection then reads the ids (routing M tokens in
-    each of its workgroups would cost more than the extra launch)."""
+    activations load). 1 < M <= PAIRS_MAX_M: the same, pair by pair (each (token, pick) pair's workgroups route its
+    token; an expert several tokens picked is read once per pair). Larger M: one gate launch first; the up projection
+    then reads the ids and streams each selected expert once for all its tokens."""
     M = xq.shape[0]
     gate = (bias, temp, route_scale, score_func, norm)
     fused, ys = _shared_plan(xq, shared, ys, topk, ex, limit, ys_out)
-    if M == 1:
-        ws = decode_up(xq, ex, limit, topk, logits=logits, gate=gate, eid_out=eid_out, wt_out=wt_out, shared=fused)
+    if M == 1 or (M <= PAIRS_MAX_M and ex.H // 16 <= 448):
+        ws = decode_up(xq, ex, limit, topk, logits=logits, gate=gate, eid_out=eid_out, wt_out=wt_out, shared=fused, pairs=M > 1)
     else:
         from .fused2 import gate_topk
         ws0 = _workspace(_lib.require_cuda(xq), M, topk, ex.H, ex.I)

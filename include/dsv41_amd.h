@@ -82,6 +82,22 @@ int dsv41_moe_decode_up(const float* logits, long long ldl, int nparts, long lon
                         const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus, const uint8_t* Ss13,
                         long long ldss13, void* stream);
 
+/* The same launch with the M tokens taken pair by pair (same arguments and outputs; for M = 1 identical to
+ * dsv41_moe_decode_up). Grid row g is pair g = (token g / topk, pick g % topk): its workgroups route that token
+ * themselves (one wave runs the token's gate and posts pick g % topk as soon as its round is done, the token's row is
+ * staged meanwhile) and stream that pick's expert; h of pair g goes to row g. The tables describe P groups of one pair
+ * each: grp_expert[g] = the pair's expert (-1 for an id outside [0, E)), grp_start[g] = g, tok_sorted[g] = g / topk,
+ * wt_sorted[g] = its weight, grp_start[P] = P. No separate gate launch and no bucketing; an expert that several tokens
+ * picked is read once per pair. Replaces the same reference steps as dsv41_moe_decode_up (decode.py:354-361,
+ * 316-335). H / 16 <= 448. */
+int dsv41_moe_decode_up_pairs(const float* logits, long long ldl, int nparts, long long part_stride, const float* bias, float temp,
+                              float route_scale, int score_func, int norm, const int* eid_in, const float* wt_in, int M, int topk, int E,
+                              const uint16_t* x, long long ldx, const uint8_t* W13, long long stride_we, const uint8_t* S13,
+                              long long stride_se, int tiled, int H, int I, float limit, uint8_t* hc, long long ldhc, uint8_t* hs,
+                              long long ldhs, int* eid_out, float* wt_out, int* grp_expert, int* grp_start, int* tok_sorted,
+                              float* wt_sorted, const uint16_t* Ws13, long long ldws, int sh_tiled, uint16_t* gus, long long ldgus,
+                              const uint8_t* Ss13, long long ldss13, void* stream);
+
 /* Decode down projection and per-token combine: y[t][n] = sum over groups g and their pair p of token t of
  * h_p . deq(W2[e_g])[n]  (M <= 16 tokens, n_slots <= 256 group slots; slots with expert -1 are unused).
  * zero_row: index of an all-zero row of hc and hs (read for tokens a group does not contain).

@@ -344,8 +344,16 @@ def test_decode_up_routing_and_tables(M, func, norm):
     w_dev = wo.cpu().numpy()
     tok, wts, _, g_e, g_s, _ = O.moe_dispatch(eid, w_dev, k, E, 16)
     wsp = moe._WS[(DEV, M, k, H, I)]
-    for got, ref in ((wsp.tok_sorted, tok), (wsp.wt_sorted, wts), (wsp.grp_expert, g_e), (wsp.grp_start, g_s)):
-        assert np.array_equal(got.cpu().numpy(), ref)
+    if 1 < M <= moe.PAIRS_MAX_M:
+        # routed pair by pair: group p = pair p alone (token p // k, its pick p % k)
+        P = M * k
+        pair_tables = ((wsp.tok_sorted, np.arange(P) // k), (wsp.wt_sorted, w_dev.reshape(-1)), (wsp.grp_expert, eid.reshape(-1)),
+                       (wsp.grp_start, np.arange(P + 1)))
+        for got, ref_p in pair_tables:
+            assert np.array_equal(got.cpu().numpy(), ref_p)
+    else:
+        for got, ref in ((wsp.tok_sorted, tok), (wsp.wt_sorted, wts), (wsp.grp_expert, g_e), (wsp.grp_start, g_s)):
+            assert np.array_equal(got.cpu().numpy(), ref)
     ref = O.moe_layer_routed(bf16_vals(xq), eid, w_dev, *[w.cpu().numpy() for w in ws], I, 10.0)
     close(y.cpu().numpy(), ref, f"decode routed from logits M={M} {func}")
     # the up-projection launch routing all M tokens itself (moe_route_experts uses it at M = 1 only)
@@ -355,7 +363,46 @@ def test_decode_up_routing_and_tables(M, func, norm):
     for got, ref_t in ((wsp2.tok_sorted, tok), (wsp2.wt_sorted, wts), (wsp2.grp_expert, g_e), (wsp2.grp_start, g_s)):
         assert np.array_equal(got.cpu().numpy(), ref_t)
     y2 = moe.decode_down(wsp2, ex)
-    assert torch.equal(y2, y)
+    if 1 < M <= moe.PAIRS_MAX_M:   # pairs sum a token's experts in pick order, the bucketed form in expert order
+        assert O.rel_l2(y2.cpu().numpy(), y.cpu().numpy()) < 1e-5
+    else:
+        assert torch.equal(y2, y)
+
+
+@pytest.mark.parametrize("M", [2, 3, 8, 16])
+@pytest.mark.parametrize("given", [False, True])
+def test_decode_up_pairs(M, given):
+    """dsv41_moe_decode_up_pairs: routing from the logits (or given ids / weights), one group per (token, pick) pair with
+    its h row p; ids and weights equal the gate kernel's exactly, tables are the pair identity, the layer equals the
+    bucketed launch's (sums in pick order instead of expert order) and the oracle's. Tokens that share experts (here
+    many, E = 24) read them once per pair."""
+    from dsv41_amd import fused2, moe, quant
+    E, H, I, k = 24, 512, 128, 6
+    ws = make_experts(E, H, I, 500 + M)
+    ex = to_ex(*ws, True)
+    rng = np.random.default_rng(600 + M)
+    lg = torch.from_numpy((rng.standard_normal((M, E)) * 2).astype(np.float32)).to(DEV)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 9 + M).to(DEV))
+    gate = (None, 1.0, 1.0, "softmax", True)
+    ei, wi = fused2.gate_topk(lg, None, 1.0, k, 1.0, "softmax", True, eid=torch.empty(M, k, dtype=torch.int32, device=DEV),
+                              wt=torch.empty(M, k, device=DEV))
+    eo, wo = torch.full((M, k), -7, dtype=torch.int32, device=DEV), torch.empty(M, k, device=DEV)
+    if given:
+        wsp = moe.decode_up(xq, ex, 10.0, k, eid=ei, wt=wi, pairs=True)
+    else:
+        wsp = moe.decode_up(xq, ex, 10.0, k, logits=lg, gate=gate, eid_out=eo, wt_out=wo, pairs=True)
+        assert torch.equal(eo, ei) and torch.equal(wo, wi)
+    P = M * k
+    e_np, w_np = ei.cpu().numpy(), wi.cpu().numpy()
+    assert np.array_equal(wsp.grp_expert.cpu().numpy(), e_np.reshape(-1))
+    assert np.array_equal(wsp.grp_start.cpu().numpy(), np.arange(P + 1))
+    assert np.array_equal(wsp.tok_sorted.cpu().numpy(), np.arange(P) // k)
+    assert np.array_equal(wsp.wt_sorted.cpu().numpy(), w_np.reshape(-1))
+    y = moe.decode_down(wsp, ex).clone()
+    yb = moe.moe_experts(xq, ei, wi, ex, 10.0)
+    assert O.rel_l2(y.cpu().numpy(), yb.cpu().numpy()) < 1e-5
+    ref = O.moe_layer_routed(bf16_vals(xq), e_np, w_np, *[w.cpu().numpy() for w in ws], I, 10.0)
+    close(y.cpu().numpy(), ref, f"decode pairs M={M} given={given}")
 
 
 @pytest.fixture(scope="module")
