@@ -954,3 +954,47 @@ def test_decode_hc_post_fused(full_layer, M, with_shared):
     moe.moe_experts(xq, ed, wd, ex, 10.0, shared=shared, hc=(res, post, comb))
     torch.cuda.synchronize()
     assert torch.equal(res, res_ref)
+
+
+@pytest.mark.parametrize("M", [2, 4])   # M = 2: the shared expert in the two launches; M = 4 (M I > 4096): its own launches
+def test_decode_pairs_shared_and_hc(full_layer, M):
+    """moe_route_experts at 2-4 tokens routes pair by pair (dsv41_moe_decode_up_pairs) with the bf16 shared expert (in
+    the two launches, or its own when it does not fit them) and the hyper-connection post mix in the down launch: the
+    shared expert's output equals the
+    bucketed launches' bit for bit, the routed sums match theirs (pick order instead of expert order), out is
+    bf16(routed + ys) exactly, the post mix equals the standalone hc_post2_ on out, and token 0's routed sum matches
+    the oracle."""
+    from dsv41_amd import fused2, moe, quant
+    E, H, I, ws, ex = full_layer
+    assert 1 < M <= moe.PAIRS_MAX_M and moe.fused_shared_ok(M, 8, I) == (M == 2)
+    rng = np.random.default_rng(1200 + M)
+    lg = torch.from_numpy(rng.standard_normal((M, E)).astype(np.float32)).to(DEV)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 1201 + M).to(DEV))
+    g = torch.Generator(device=DEV).manual_seed(1202 + M)
+    shared = moe.SharedExpert.prepare((torch.randn(2 * I, H, generator=g, device=DEV) / H ** 0.5).to(torch.bfloat16),
+                                      (torch.randn(H, I, generator=g, device=DEV) / I ** 0.5).to(torch.bfloat16))
+    eo, wo = torch.empty(M, 8, dtype=torch.int32, device=DEV), torch.empty(M, 8, device=DEV)
+    out, ys = torch.empty(M, H, dtype=torch.bfloat16, device=DEV), torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    y32 = torch.empty(M, H, device=DEV)
+    route = (xq, lg, None, 1.0, 8, 1.0, "softmax", True, ex, 10.0)
+    moe.moe_route_experts(*route, out=out, y32=y32, eid_out=eo, wt_out=wo, shared=shared, ys_out=ys)
+    out_b, ys_b, y32_b = torch.empty_like(out), torch.empty_like(ys), torch.empty_like(y32)
+    moe.moe_experts(xq, eo, wo, ex, 10.0, out=out_b, y32=y32_b, shared=shared, ys_out=ys_b)
+    torch.cuda.synchronize()
+    assert torch.equal(ys, ys_b)
+    assert O.rel_l2(y32.cpu().numpy(), y32_b.cpu().numpy()) < 1e-5   # the routed sums, in pick order vs expert order
+    # out = bf16(routed + ys) exactly (model.py:590-591)
+    ref_out = O.bf16_round(y32.cpu().numpy() + ys.float().cpu().numpy())
+    assert np.array_equal(out.float().cpu().numpy(), ref_out)
+    res0 = torch.from_numpy(O.f32_to_bf16_bits(rng.standard_normal((M, 1, 4, H)).astype(np.float32)).view(np.int16)).view(torch.bfloat16).to(DEV)
+    post = torch.from_numpy(rng.standard_normal((M, 4)).astype(np.float32)).to(DEV)
+    comb = torch.from_numpy(rng.standard_normal((M, 4, 4)).astype(np.float32)).to(DEV)
+    res, res_ref = res0.clone(), res0.clone()
+    moe.moe_route_experts(*route, shared=shared, hc=(res, post, comb))
+    fused2.hc_post2_(out, res_ref, post, comb)
+    torch.cuda.synchronize()
+    assert torch.equal(res, res_ref)
+    eid, wt = eo.cpu().numpy(), wo.cpu().numpy()
+    W13, S13, W2, S2 = host_subset(ws, set(eid[0].tolist()))
+    y0 = O.moe_layer_routed(bf16_vals(xq[0:1]), eid[0:1], wt[0:1], W13, S13, W2, S2, I, 10.0)
+    close(y32[0:1].cpu().numpy(), y0, f"pairs M={M} token 0 routed layer")
