@@ -262,7 +262,8 @@ def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Exper
                 ys: torch.Tensor | None = None, out: torch.Tensor | None = None, y32: torch.Tensor | None = None,
                 shared: tuple | None = None, ys_out: torch.Tensor | None = None, hc: tuple | None = None) -> torch.Tensor:
     """Routed experts of one layer for M <= 16 tokens with given routing.
-    xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int [M, k] (distinct per token); wt fp32 [M, k].
+    xq: bf16 [M, H] on the FP8 grid (fake_quant_fp8 output); eid int [M, k] (distinct per token, except for 2 <= M <=
+    PAIRS_MAX_M, which runs pair by pair); wt fp32 [M, k].
     Returns fp32 [M, H] = sum_j w_j-weighted expert outputs (routing weight folded into h, fused.py:297-302),
     or, when `out` (bf16 [M, H]) is given, writes out = bf16(y + ys) (ys: bf16 shared-expert output or None);
     y32 (fp32 [M, H]) additionally receives y. shared (a SharedExpert, or a row-major (w13, w2) bf16 pair) computes
@@ -270,13 +271,16 @@ def moe_experts(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Exper
     (fused_shared_ok), else as its own launches first; ys_out (bf16 [M, H]) receives its output. hc = (residual, post,
     comb) applies the hyper-connection post mix to bf16(y + ys) in the same launch (decode_down)."""
     k = eid.shape[-1]
+    M = xq.shape[0]
     fused, ys = _shared_plan(xq, shared, ys, k, ex, limit, ys_out)
-    ws = decode_up(xq, ex, limit, k, eid=eid, wt=wt, shared=fused)
+    # 2 <= M <= PAIRS_MAX_M: pair by pair (faster at these sizes, and a token may then name an expert twice)
+    pairs = 1 < M <= PAIRS_MAX_M and ex.H // 16 <= 448
+    ws = decode_up(xq, ex, limit, k, eid=eid, wt=wt, shared=fused, pairs=pairs)
     return decode_down(ws, ex, ys, out, y32, limit=limit, ys_out=ys_out if fused is not None else None, hc=hc)
 
 
-# largest token count routed pair by pair inside the up launch (moe_route_experts): below it the gate launch and the
-# bucketing cost more than reading the few experts two tokens share twice
+# largest token count run pair by pair (moe_route_experts: routed inside the up launch; moe_experts: given ids): up to
+# it the gate launch and the bucketing cost more than reading the few experts two tokens share twice
 PAIRS_MAX_M = 4
 
 

@@ -469,9 +469,9 @@ def moe_layer_routed(xq, eid, wt, W13, S13, W2, S2, inter: int, limit: float) ->
     for e in experts:
         A2 = dense_weights(W2[e], S2[e])
         for t, gu in gu_all[e].items():
-            j = [int(v) for v in eid[t]].index(e)
-            h = swiglu_quant(gu.reshape(1, -1), np.array([wt[t][j]], F32), inter, limit)[0]
-            y2[(t, j)] = (A2 @ h).astype(F32)
+            for j in [jj for jj, v in enumerate(eid[t]) if int(v) == e]:   # every pair of t naming e (ids may repeat)
+                h = swiglu_quant(gu.reshape(1, -1), np.array([wt[t][j]], F32), inter, limit)[0]
+                y2[(t, j)] = (A2 @ h).astype(F32)
         del A2
     for t in range(M):
         acc = np.zeros(H, F32)

@@ -956,6 +956,24 @@ def test_decode_hc_post_fused(full_layer, M, with_shared):
     assert torch.equal(res, res_ref)
 
 
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_decode_pairs_duplicate_ids(M):
+    """moe_experts at 2-4 tokens runs pair by pair, so a token may name one expert twice (each pair is its own group and
+    h row): the layer equals the oracle's sum over the pairs, duplicates included."""
+    from dsv41_amd import moe, quant
+    E, H, I, k = 24, 512, 128, 6
+    ws = make_experts(E, H, I, 700 + M)
+    ex = to_ex(*ws, True)
+    rng = np.random.default_rng(710 + M)
+    eid = rng.integers(0, E, (M, k)).astype(np.int32)
+    eid[:, 1] = eid[:, 0]                        # every token names its first expert twice
+    wt = rng.random((M, k)).astype(np.float32)
+    xq = quant.fake_quant_fp8(rand_x(M, H, 720 + M).to(DEV))
+    y = moe.moe_experts(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, 10.0)
+    ref = O.moe_layer_routed(bf16_vals(xq), eid, wt, *[w.cpu().numpy() for w in ws], I, 10.0)
+    close(y.cpu().numpy(), ref, f"decode pairs M={M} with duplicate ids")
+
+
 @pytest.mark.parametrize("M", [2, 4])   # M = 2: the shared expert in the two launches; M = 4 (M I > 4096): its own launches
 def test_decode_pairs_shared_and_hc(full_layer, M):
     """moe_route_experts at 2-4 tokens routes pair by pair (dsv41_moe_decode_up_pairs) with the bf16 shared expert (in
