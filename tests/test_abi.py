@@ -93,6 +93,15 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert up(I - 32, I // 32) == -1
     assert up(I, I // 32 - 1) == -1
 
+    # the pair-by-pair entry: the same checks, and its one-row staging needs H / 16 <= 448 (H = 8192 is too wide)
+    def up_pairs(ldhc, ldhs, M=2, H_=H):
+        return L.dsv41_moe_decode_up_pairs(None, 0, 1, 0, None, 1.0, 1.0, 2, 1, p, p, M, 8, 384, p, H_, p, 2 * I * H_ // 2, p,
+                                           2 * I * H_ // 32, 1, H_, I, ctypes.c_float(10.0), p, ldhc, p, ldhs, None, None, p, p, p, p,
+                                           None, 0, 0, None, 0, None, 0, None)
+    assert up_pairs(I - 32, I // 32) == -1
+    assert up_pairs(I, I // 32, M=17) == -1
+    assert up_pairs(I, I // 32, H_=8192) == -1
+
     def down(zero_row, Ws2=None, M=1, ys=None):
         return L.dsv41_moe_down_sum(p, H * (I // 2), p, H * (I // 32), 1, H, I, p, I, p, I // 32, zero_row, p, p, p, 8, M,
                                     p, H, ys, H, None, H, 0, 384, p if Ws2 else None, 2 * I, Ws2, I, 0, ctypes.c_float(10.0), None, H, None, None, None,
