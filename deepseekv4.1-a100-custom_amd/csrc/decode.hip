@@ -143,7 +143,8 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
     __shared__ unsigned long long s_bits[UP_MAXE / 64];   // selected experts
     __shared__ int s_tok[UP_MAXM * UP_MAXK], s_slot[UP_MAXM * UP_MAXK];   // members of this workgroup's group
     __shared__ float s_pw[UP_MAXM * UP_MAXK];
-    __shared__ int s_mg, s_pick, s_xready;
+    __shared__ int s_pick, s_xready;
+    __shared__ unsigned long long s_wmem[UP_WAVES], s_wlow[UP_WAVES];   // per wave: member / smaller-expert pair ballots
     __shared__ v4f s_acc[UP_WAVES][64];
     __shared__ __align__(16) uint8_t s_wsc[SCL ? UP_WAVES * UP_WSC : 16];
     if (SH && (int)blockIdx.y < a.sh_y) {   // a shared-expert row block (uniform over the workgroup)
@@ -410,25 +411,33 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
             if (SCL) scale_load();   // lands while the members are found and their rows staged
         }
 
-        // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots
-        if (tid == 0) s_mg = 0;
+        // ---- members of the group (tokens holding expert eg, ascending) and their sorted pair slots. Thread p looks at
+        // pair p (P <= 256 of 512 threads): ballots give the pairs of a smaller expert (the group's first slot) and
+        // the members before p (its rank; pairs are token-major, so in token order), in one pass
+        const int ep = (g < U && tid < P) ? s_eid[tid] : -1;
+        const bool is_mem = ep >= 0 && ep == eg;
+        const unsigned long long bmem = __ballot(is_mem), blow = __ballot(ep >= 0 && ep < eg);
+        if (lane == 0) {
+            s_wmem[wave] = bmem;
+            s_wlow[wave] = blow;
+        }
         __syncthreads();
-        if (g < U)
-            for (int p = tid; p < P; p += blockDim.x)
-                if (s_eid[p] == eg) {
-                    int lt = 0, same = 0;
-                    for (int q = 0; q < P; ++q) {
-                        const int eq = s_eid[q];
-                        lt += (eq >= 0 && eq < eg) ? 1 : 0;
-                        same += (eq == eg && q < p) ? 1 : 0;   // pairs are token-major: q < p = earlier token (or slot)
-                    }
-                    s_tok[same] = p / topk;
-                    s_slot[same] = lt + same;
-                    s_pw[same] = s_wt[p];
-                    atomicAdd(&s_mg, 1);
-                }
+        int lt = 0, before = 0, total = 0;
+#pragma unroll
+        for (int w = 0; w < UP_WAVES; ++w) {
+            const int c = __popcll(s_wmem[w]);
+            lt += __popcll(s_wlow[w]);
+            before += w < wave ? c : 0;
+            total += c;
+        }
+        if (is_mem) {
+            const int same = before + __popcll(bmem & ((1ull << lane) - 1ull));
+            s_tok[same] = tid / topk;
+            s_slot[same] = lt + same;
+            s_pw[same] = s_wt[tid];
+        }
         __syncthreads();
-        mg = g < U ? __builtin_amdgcn_readfirstlane(s_mg) : 0;
+        mg = g < U ? __builtin_amdgcn_readfirstlane(total) : 0;
     }
     const bool work = eg >= 0;
 
