@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (2048 tokens; for profiling its kernels)")
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of --prefill-only (2048: configs[3]; 16384: the probe)")
     ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
+    ap.add_argument("--stack-only", action="store_true", help="only the configs[4] 20-layer decode stack (for profiling its kernels)")
     ap.add_argument("--shared-only", choices=["bf16", "fp8"], default=None,
                     help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
     ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
@@ -690,6 +691,11 @@ def main():
         t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
         print(json.dumps({"workload": f"configs[2] decode, M = {M}", "us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                           "TBps": round(uniq * eb / t_m / 1e12, 3), "w2_bytes_per_expert": H * (I // 2) + H * (I // 32)}))
+        return
+    if args.stack_only:
+        t_s, b_s = bench_stack(torch, dev, layers, max(2, min(K, 10)), W)
+        print(json.dumps({"workload": "configs[4]: 20 layers, batch-1 decode, one graph", "us_per_step": round(t_s * 1e6, 1),
+                          "bytes_per_step": b_s, "GBps": round(b_s / t_s / 1e9, 1)}))
         return
     if args.shared_only:
         # the configs[1] layer with its shared expert inside the two decode launches, for profiling those kernels
