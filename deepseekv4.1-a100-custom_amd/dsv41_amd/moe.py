@@ -334,6 +334,10 @@ class PrefillState:
         self.__dict__.update(kw)
 
 
+# pairs per group of the prefill path's dispatch (the prefill kernels take groups of up to this many pairs)
+PREFILL_GROUP = 128
+
+
 def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float) -> PrefillState:
     """First half of the prefill path: xq bf16 [T, H] on the FP8 grid -> E4M3 codes (exact); (token, expert) pairs
     bucketed by expert in groups of <= 128 (moe_dispatch, p2p.cu:90-132); the w13 GEMM with the SwiGLU/FP8
@@ -347,8 +351,9 @@ def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Expert
     I = ex.I
     assert H == ex.H and xq.dtype == torch.bfloat16 and ex.E <= 512
     xc, xs = quant_fp8_e8m0(xq)
-    tok_sorted, wt_sorted, inv, grp_expert, grp_start = moe_dispatch(eid, wt, k, ex.E, 128, dev)
-    G = min(P, ex.E + (P + 127) // 128)   # groups of <= 128 pairs: at most E + P / 128 of them
+    gmax = PREFILL_GROUP
+    tok_sorted, wt_sorted, inv, grp_expert, grp_start = moe_dispatch(eid, wt, k, ex.E, gmax, dev)
+    G = min(P, ex.E + (P + gmax - 1) // gmax)   # groups of <= gmax pairs: at most E + P / gmax of them
     hc = torch.empty(P, I, dtype=torch.uint8, device=dev)
     hs = torch.empty(P, I // 32, dtype=torch.uint8, device=dev)
     _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), T, _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),

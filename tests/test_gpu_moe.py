@@ -586,13 +586,13 @@ def _e4m3_values(codes, scales):
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 @pytest.mark.parametrize("H", [512, 768])
 def test_prefill_stages_vs_oracle(tiled, limit, H):
-    """Prefill stage by stage (T = 200 tokens, top-4 of 16 experts, expert 3 in every token: 200 pairs = two
-    groups). h: the oracle's SwiGLU + fq8 of gu = x . deq(W13)^T, element for element, except where fp32
+    """Prefill stage by stage (T = 300 tokens, top-4 of 16 experts, expert 3 in every token: 300 pairs = several
+    groups, the last one partial). h: the oracle's SwiGLU + fq8 of gu = x . deq(W13)^T, element for element, except where fp32
     summation order moves a value across an E4M3 rounding boundary (one code step, rare). y2: fp64 product of the
     kernel's own h with deq(W2), tolerance of the spec. Combine: slot-ordered sum, bit-exact. H = 768: three 256-row
     column blocks in w2, so a workgroup taking two column blocks also meets one with a single block."""
     from dsv41_amd import moe, quant
-    E, I, k, T = 16, 384, 4, 200
+    E, I, k, T = 16, 384, 4, 300
     ws = make_experts(E, H, I, 500 + int(tiled))
     ex = to_ex(*ws, tiled)
     eid, wt = _skewed_routing(T, E, k, 3, 7)
@@ -600,7 +600,7 @@ def test_prefill_stages_vs_oracle(tiled, limit, H):
     st = moe.prefill_up(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, limit)
     tok = st.tok_sorted.cpu().numpy()
     ge, gs = st.grp_expert.cpu().numpy(), st.grp_start.cpu().numpy()
-    assert np.count_nonzero(ge == 3) == 2
+    assert np.count_nonzero(ge == 3) == -(-T // moe.PREFILL_GROUP) > 1
     W13, S13, W2, S2 = [w.cpu().numpy() for w in ws]
     x = bf16_vals(xq)
     gu = O.grouped_gemm(x, W13, S13, ge, gs, tok, int(np.count_nonzero(ge >= 0))).astype(np.float32)
