@@ -2,8 +2,9 @@
 // expert (model.MoE.__call__ beyond 16 tokens, model.py:539-551, 584-589; moe_kernels.grouped_fp4_gemm,
 // moe_kernels.py:127-200).
 //
-// The (token, expert) pairs arrive bucketed by expert in groups of <= 128 pairs (moe_dispatch tables, gmax 128).
-// One workgroup computes a 256-row x 128-pair tile of one group over the full K:
+// The (token, expert) pairs arrive bucketed by expert in groups of <= 256 pairs (moe_dispatch tables, gmax 256; the
+// reference-shaped grouped-GEMM surface: <= 128). One workgroup computes a 256-row x 128-pair tile of one group over
+// the full K (groups of more than 128 pairs: a 256-row x 256-pair tile, below):
 //   MODE 0 (w13): rows = 128 gate rows c0 .. c0 + 127 and the matching 128 up rows I + c0 .., so the epilogue
 //          turns the tile into h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) for 128 columns (four FP8
 //          groups) of every pair (fused.py:284-306) -- gate/up never reach HBM;
@@ -101,14 +102,14 @@ struct IntC {
     static constexpr int value = N;
 };
 
+// Item L of the launch order (group, column blocks) on the 128-pair tile.
 template <int MODE, int TILED>
-__global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
+__device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int L) {
     // more than one column block per workgroup (the epilogue inside the k-loop) or one (the epilogue after it)
     constexpr bool CBL = (MODE == 0 ? PV_CBW0 : PV_CBW1) > 1;
     extern __shared__ __align__(16) uint8_t smem[];   // PV_NS stages of PV_STAGE bytes
     __shared__ int s_row[PG_T];
 
-    const int L = blockIdx.x;
     const int jx = L >> 3, gi = jx / a.n_it;
     const int g = gi * 8 + (L & 7), cbi = jx - gi * a.n_it;
     if (g >= a.G || cbi >= a.n_it) return;
@@ -447,6 +448,11 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const Pref
     if constexpr (!CBL) epilogue(cb0);   // one column block: the epilogue once, after the loop
 }
 
+template <int MODE, int TILED>
+__global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
+    prefill_item128<MODE, TILED>(a, (int)blockIdx.x);
+}
+
 // y[t][n] = bf16(sum_j y2[inv[t * topk + j]][n] (+ ys[t][n])), j ascending (model.py:589-591: view(n, k, dim).sum(1)
 // then + shared, fp32); optional fp32 y32. One thread per 4 consecutive n.
 __global__ void __launch_bounds__(256) combine_pairs_kernel(const float* __restrict__ y2, long long ldy2, const int* __restrict__ inv,
@@ -492,23 +498,329 @@ __global__ void __launch_bounds__(256) combine_pairs_kernel(const float* __restr
     }
 }
 
-static int launch_prefill(PrefillArgs& a, int mode, int tiled, hipStream_t st) {
+// ------------------------------------------------------------------------------------------ 256-pair tiles
+// The prefill path takes groups of up to 256 pairs (moe_dispatch tables with gmax 256) and a launch whose items pick
+// their tile by the size of their group: groups of <= 128 pairs run the 128-pair tile above, larger ones a 256-row x
+// 256-pair tile. Against two 128-pair items the large tile doubles the MFMAs per byte of weights loaded and halves
+// how many groups (each re-reading its expert's weights) a popular expert takes. Wave w keeps the rows of the
+// 128-pair tile (row quarter cg = w & 3: MODE 0 gate blocks 2 cg, 2 cg + 1 and their up blocks, MODE 1 row blocks
+// 4 cg .. 4 cg + 3) for the 8 token blocks 2 u + ph of half ph = w >> 2 (alternate blocks, so both halves of every
+// SIMD compute for any group size): 4 row blocks x 8 token blocks = 32 MFMAs per k-step, 128 accumulator registers,
+// operands single-buffered. Stage (50 KB): weight slots 16 x 1 KB, their E8M0 bytes 16 x 64, token blocks 16 x 2 KB,
+// the pairs' E8M0 words 256 x 4. Three stages: step k + 2 is issued in step k, into the stage of step k - 1. The
+// k-loop is the ping-pong loop of the 128-pair tile (waves 4-7 one barrier behind waves 0-3).
+#define P2_T 256
+#define P2_NS 3
+#define P2_A 0
+#define P2_AS 16384
+#define P2_B 17408
+#define P2_BS 50176
+#define P2_STAGE 51200
+
+template <int MODE, int TILED>
+__device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int L) {
+    constexpr bool CBL = (MODE == 0 ? PV_CBW0 : PV_CBW1) > 1;
+    extern __shared__ __align__(16) uint8_t smem[];   // P2_NS stages of P2_STAGE bytes
+    __shared__ int s_row[P2_T];
+
+    const int jx = L >> 3, gi = jx / a.n_it;
+    const int g = gi * 8 + (L & 7), cbi = jx - gi * a.n_it;
+    if (g >= a.G || cbi >= a.n_it) return;
+    const int cb0 = cbi * a.cbw, ncb = CBL ? min(a.cbw, a.n_cb - cb0) : 1;
+    if (ncb <= 0) return;
+    const int e = a.grp_expert[g];
+    if (e < 0 || e >= a.E) return;
+    const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), m = min(min(a.grp_start[g + 1], a.n_pairs) - p0, P2_T);
+    if (m <= 0) return;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cg = wave & 3, ph = wave >> 2;
+    const int col = lane & 15, kb = lane >> 4;
+    const int K = a.K, nk = K >> 7, Kh = K >> 1, Ks = K >> 5;
+    const int I = a.N >> 1;
+    auto block_of = [&](int b, int cb) {
+        if (MODE == 0) return b < 8 ? (cb * 128 + 16 * b) >> 4 : (I + cb * 128 + 16 * (b - 8)) >> 4;
+        return cb * 16 + b;
+    };
+    constexpr int PV_DNB = MODE == 0 ? 8 : 16;
+    int slot_of[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) slot_of[j] = MODE == 0 ? (j < 2 ? 2 * cg + j : 8 + 2 * cg + (j - 2)) : 4 * cg + j;
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W + (long long)e * a.stride_we, (uint32_t)a.stride_we);
+    const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + (long long)e * a.stride_se, (uint32_t)a.stride_se);
+
+    if (tid < P2_T) {
+        const int p = p0 + (tid < m ? tid : 0);
+        const int r = a.row_of_pair ? a.row_of_pair[p] : p;
+        const int x_rows = (int)(a.xc_bytes / (uint32_t)a.ldx);
+        s_row[tid] = (r >= 0 && r < x_rows) ? r : x_rows;
+    }
+    // the routing weights of this lane's pairs (MODE 0 epilogue), fetched now
+    float wgt[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int pr = 16 * (2 * u + ph) + col;
+        wgt[u] = MODE == 0 && pr < m ? a.wt_sorted[p0 + pr] : 0.f;
+    }
+    __syncthreads();
+
+    // ---- DMA descriptors: weight slots 2 w, 2 w + 1; token blocks 2 w, 2 w + 1 (two 1 KB halves each); weight scales
+    // (tiled: wave 0, 16 B per lane; row-major: waves 0-3, 4 slots each); the pairs' E8M0 words (waves 4-7, 64 each)
+    const int nbw0 = block_of(2 * wave, cb0), nbw1 = block_of(2 * wave + 1, cb0);
+    auto a_off = [&](int nb) {
+        return TILED ? (uint32_t)(nb * nk * 1024 + col * 64 + kb * 16) : (uint32_t)((nb * 16 + col) * Kh + kb * 16);
+    };
+    const uint32_t a_voff0 = a_off(nbw0), a_voff1 = a_off(nbw1);
+    const int a_ks = TILED ? 1024 : 64;
+    const uint32_t a_cs = TILED ? (uint32_t)(PV_DNB * nk * 1024) : (uint32_t)(PV_DNB * 16 * Kh);
+    const int asb = TILED ? block_of(lane >> 2, cb0) : block_of(4 * (wave & 3) + (lane >> 4), cb0), asr = lane & 15;
+    const uint32_t as_voff = TILED ? (uint32_t)(asb * nk * 64 + (lane & 3) * 16) : (uint32_t)((asb * 16 + asr) * Ks);
+    const int as_ks = TILED ? 64 : 4;
+    const uint32_t as_cs = TILED ? (uint32_t)(PV_DNB * nk * 64) : (uint32_t)(PV_DNB * 16 * Ks);
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.xc, a.xc_bytes), xsr = buffer_rsrc(a.xs, a.xs_bytes);
+    const uint32_t b0off = (uint32_t)s_row[32 * wave + col] * (uint32_t)a.ldx + kb * 16;
+    const uint32_t b1off = (uint32_t)s_row[32 * wave + 16 + col] * (uint32_t)a.ldx + kb * 16;
+    const uint32_t bsoff = (uint32_t)s_row[(64 * (wave & 3) + lane) & (P2_T - 1)] * (uint32_t)a.ldxs;
+    const bool ldb0 = 32 * wave < m, ldb1 = 32 * wave + 16 < m;   // wave-uniform: the token block holds pairs
+    const bool lda = TILED ? wave == 0 : wave < 4, ldbs = wave >= 4 && 64 * (wave - 4) < m;
+    const int per_step = 2 + (lda ? 1 : 0) + (ldb0 ? 2 : 0) + (ldb1 ? 2 : 0) + (ldbs ? 1 : 0);
+
+    const int lofs = lane * 16;
+    bool tb_on[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) tb_on[u] = 16 * (2 * u + ph) < m;
+    const bool any_on = tb_on[0];
+    v4i OA[4], OB0[8], OB1[8];
+    uint32_t OSA, OSB[2];
+    // per-lane LDS offsets within a stage: weight slots relative to slot_of[0], token blocks of this half, scales
+    const uint32_t lofs_a = (uint32_t)(P2_A + slot_of[0] * 1024 + lofs), lofs_b = (uint32_t)(P2_B + ph * 2048 + lofs);
+    const uint32_t lofs_as = (uint32_t)(P2_AS + slot_of[0] * 64 + col * 4 + kb), lofs_bs = (uint32_t)(P2_BS + 16 * ph * 4 + col * 4 + kb);
+    auto read_ops = [&](int st) {
+        const uint32_t so = (uint32_t)st * P2_STAGE;
+        const uint32_t oa = lofs_a + so, ob = lofs_b + so, osa = lofs_as + so, osb = lofs_bs + so;
+        if (any_on) {   // wave-uniform: a wave whose half of the group is empty reads and computes nothing
+            uint32_t sa = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int dj = MODE == 0 ? (j < 2 ? j : 8 + (j - 2)) : j;   // slot_of[j] - slot_of[0]
+                OA[j] = *(const v4i*)(smem + oa + dj * 1024);
+                sa |= (uint32_t)smem[osa + dj * 64] << (8 * j);
+            }
+            OSA = sa;
+        }
+        uint32_t sb[2] = {0u, 0u};
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (!tb_on[u]) continue;
+            OB0[u] = *(const v4i*)(smem + ob + u * 4096);
+            OB1[u] = *(const v4i*)(smem + ob + u * 4096 + 1024);
+            sb[u >> 2] |= (uint32_t)smem[osb + u * 128] << (8 * (u & 3));
+        }
+        OSB[0] = sb[0];
+        OSB[1] = sb[1];
+    };
+    v4f acc[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[j][u] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto mfmas = [&]() {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (!tb_on[u]) continue;
+            const v8i bv = v8i{OB0[u].x, OB0[u].y, OB0[u].z, OB0[u].w, OB1[u].x, OB1[u].y, OB1[u].z, OB1[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[j][u] = mfma_fp4w_fp8x_sel(j, u & 3, v8i{OA[j].x, OA[j].y, OA[j].z, OA[j].w, 0, 0, 0, 0}, bv, acc[j][u], (int)OSA,
+                                               (int)OSB[u >> 2]);
+        }
+    };
+    auto epilogue = [&](int cb) __attribute__((always_inline)) {
+        if (MODE == 0) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (!tb_on[u]) continue;
+                const int pr = 16 * (2 * u + ph) + col;
+                float h[2][4];
+                float mx = 0.f;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float gv[4] = {acc[j][u].x, acc[j][u].y, acc[j][u].z, acc[j][u].w};
+                    const float uv[4] = {acc[2 + j][u].x, acc[2 + j][u].y, acc[2 + j][u].z, acc[2 + j][u].w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float gg = gv[i], uu = uv[i];
+                        if (a.limit > 0.f) {
+                            uu = fminf(fmaxf(uu, -a.limit), a.limit);
+                            gg = fminf(gg, a.limit);
+                        }
+                        float hv = gg * (1.0f / (1.0f + expf(-gg))) * uu;
+                        hv = bf16_round(hv * wgt[u]);
+                        h[j][i] = hv;
+                        mx = fmaxf(mx, fabsf(hv));
+                    }
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const int ex = fq8_exponent(mx);
+                if (pr < m) {
+                    const long long p = p0 + pr;
+                    const int c0 = cb * 128 + 32 * cg;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        uint32_t codes = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
+                        *(gmem_u32*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
+                    }
+                    if (kb == 0) *(gmem_u8*)(a.hs + p * a.ldhs + (c0 >> 5)) = (uint8_t)(ex + 127);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int pr = 16 * (2 * u + ph) + col;
+                if (tb_on[u] && pr < m) {
+                    float* o = a.y + (long long)(p0 + pr) * a.ldy + cb * 256 + 64 * cg + 4 * kb;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) *(gmem_v4f*)(o + 16 * j) = acc[j][u];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[j][u] = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    // The ping-pong k-loop over the ncb x nk steps with three stages: in step k, after its first barrier, the stage of
+    // step k - 1 (read by both halves by then) takes step k + 2. Instantiated per wave DMA count (2 .. 8), so the
+    // waits are constants.
+    auto kloop = [&](auto ps_c) {
+        constexpr int PS = decltype(ps_c)::value;
+        const int T = ncb * nk;
+        const bool lag = ph == 1;
+        uint32_t iao = 0, iso = 0, ixo = 0;
+        int ikc = 0;
+        auto issue_st = [&](int st) {
+            uint8_t* so = smem + st * P2_STAGE;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + P2_A + 2 * wave * 1024), 16, a_voff0, iao, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(so + P2_A + (2 * wave + 1) * 1024), 16, a_voff1, iao, 0, 0);
+            if (lda) {
+                if (TILED) __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + P2_AS), 16, as_voff, iso, 0, 0);
+                else __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(so + P2_AS + wave * 256), 4, as_voff, iso, 0, 0);
+            }
+            if (ldb0) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + P2_B + 2 * wave * 2048), 16, b0off, ixo, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + P2_B + 2 * wave * 2048 + 1024), 16, b0off + 64, ixo, 0, 0);
+            }
+            if (ldb1) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + P2_B + (2 * wave + 1) * 2048), 16, b1off, ixo, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(so + P2_B + (2 * wave + 1) * 2048 + 1024), 16, b1off + 64, ixo, 0, 0);
+            }
+            if (ldbs)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xsr, (lds_void*)(so + P2_BS + (wave - 4) * 256), 4, bsoff, ixo >> 5, 0, 0);
+            iao += a_ks;
+            iso += as_ks;
+            ixo += 128;
+            if constexpr (CBL) {
+                if (++ikc == nk) {
+                    ikc = 0;
+                    ixo = 0;
+                    iao += a_cs - (uint32_t)(nk * a_ks);
+                    iso += as_cs - (uint32_t)(nk * as_ks);
+                }
+            }
+        };
+        int ekc = 0, ec = 0;
+        auto step_done = [&]() {
+            if constexpr (CBL) {
+                if (++ekc == nk) { epilogue(cb0 + ec); ekc = 0; ++ec; }
+            }
+        };
+        auto barrier = [&]() {
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        };
+        // one k-step in stage st; ISS: it refills the stage of step k - 1 with step k + 2; WA / WB: later steps of this
+        // wave in flight when it waits for its DMA of this step (before the first barrier) and of the next (before
+        // the second; WB < 0: no wait). Both halves take both waits.
+        auto step = [&](int st, auto iss_c, auto wa_c, auto wb_c) {
+            constexpr int WA = decltype(wa_c)::value, WB = decltype(wb_c)::value;
+            wait_vm_c<PS * WA>();
+            barrier();
+            read_ops(st);
+            if constexpr (decltype(iss_c)::value != 0) issue_st(st == 0 ? 2 : st - 1);
+            if constexpr (WB >= 0) wait_vm_c<PS * WB>();
+            __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0): own LDS reads done
+            barrier();
+            mfmas();
+            step_done();
+        };
+        issue_st(0);   // steps 0, 1 (T >= PG_PF = 3)
+        issue_st(1);
+        if (lag) {
+            wait_vm_c<PS * 1>();              // own DMA of step 0
+            barrier();                        // meets the first barrier of waves 0-3
+        }
+        // steady state: steps 0 .. T - 3, each refilling and waiting with one later step in flight; then T - 2, T - 1
+        int st = 0;
+        for (int kk = 0; kk < T - 2; ++kk) {
+            step(st, IntC<1>{}, IntC<1>{}, IntC<1>{});
+            st = st == P2_NS - 1 ? 0 : st + 1;
+        }
+        step(st, IntC<0>{}, IntC<1>{}, IntC<0>{});
+        st = st == P2_NS - 1 ? 0 : st + 1;
+        step(st, IntC<0>{}, IntC<0>{}, IntC<-1>{});
+        if (!lag) barrier();                  // meets the last barrier of waves 4-7
+    };
+    switch (per_step) {
+        case 2: kloop(IntC<2>{}); break;
+        case 3: kloop(IntC<3>{}); break;
+        case 4: kloop(IntC<4>{}); break;
+        case 5: kloop(IntC<5>{}); break;
+        case 6: kloop(IntC<6>{}); break;
+        case 7: kloop(IntC<7>{}); break;
+        default: kloop(IntC<8>{}); break;
+    }
+    if constexpr (!CBL) epilogue(cb0);
+}
+
+
+// The prefill path's launch: each item takes the 256-pair tile when its group holds more than 128 pairs.
+template <int MODE, int TILED>
+__global__ void __launch_bounds__(PG_THREADS) prefill_gemm_mixed_kernel(const PrefillArgs a) {
+    const int L = (int)blockIdx.x;
+    const int jx = L >> 3, g = (jx / a.n_it) * 8 + (L & 7);
+    if (g >= a.G) return;
+    const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), m = min(a.grp_start[g + 1], a.n_pairs) - p0;
+    if (m > PG_T) prefill_item256<MODE, TILED>(a, L);
+    else prefill_item128<MODE, TILED>(a, L);
+}
+
+// mixed: groups of <= 256 pairs (the prefill path's launch); otherwise <= 128 (the 128-pair tile alone)
+static int launch_prefill(PrefillArgs& a, int mode, int tiled, bool mixed, hipStream_t st) {
     a.g_pad = (a.G + 7) & ~7;
     a.cbw = mode == 0 ? PV_CBW0 : PV_CBW1;
     a.n_it = (a.n_cb + a.cbw - 1) / a.cbw;
     const long long items = (long long)a.n_it * a.g_pad;   // a multiple of 8
     if (items > 0x7FFFFFFFll) return DSV41_EINVAL;
     const dim3 grid((unsigned)items), block(PG_THREADS);
-    const size_t lds = (size_t)PV_NS * PV_STAGE;
-#define PV_LAUNCH(M, T)                                                                                               \
+    const size_t lds = mixed ? (size_t)max(PV_NS * PV_STAGE, P2_NS * P2_STAGE) : (size_t)PV_NS * PV_STAGE;
+#define PV_LAUNCH(K, M, T)                                                                                            \
     do {                                                                                                          \
-        const hipError_t err = hipFuncSetAttribute((const void*)prefill_gemm_lds_kernel<M, T>,                    \
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);         \
+        const hipError_t err = hipFuncSetAttribute((const void*)K<M, T>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                                   (int)lds);                                                     \
         if (err != hipSuccess) return (int)err;                                                                   \
-        prefill_gemm_lds_kernel<M, T><<<grid, block, lds, st>>>(a);                                               \
+        K<M, T><<<grid, block, lds, st>>>(a);                                                                     \
     } while (0)
-    if (mode == 0) { if (tiled) PV_LAUNCH(0, 1); else PV_LAUNCH(0, 0); }
-    else { if (tiled) PV_LAUNCH(1, 1); else PV_LAUNCH(1, 0); }
+    if (mixed) {
+        if (mode == 0) { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 0, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 0, 0); }
+        else { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 0); }
+    } else {
+        if (mode == 0) { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 0, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 0, 0); }
+        else { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 1, 0); }
+    }
 #undef PV_LAUNCH
     return (int)hipGetLastError();
 }
@@ -528,7 +840,7 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W13, stride_we, S13, stride_se, 2 * I, H, E,
                   grp_expert, grp_start, G, tok_sorted, wt_sorted, limit, hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0, 0x7FFFFFFF};
-    return launch_prefill(a, 0, tiled, (hipStream_t)stream);
+    return launch_prefill(a, 0, tiled, true, (hipStream_t)stream);
 }
 
 extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, int h_rows, const uint8_t* W2, long long stride_we,
@@ -545,7 +857,7 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
     if (G == 0) return 0;
     PrefillArgs a{hc, ldhc, hs, ldhs, (uint32_t)(h_rows * ldhc), (uint32_t)(h_rows * ldhs), W2, stride_we, S2, stride_se, H, I, E,
                   grp_expert, grp_start, G, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0, h_rows};
-    return launch_prefill(a, 1, tiled, (hipStream_t)stream);
+    return launch_prefill(a, 1, tiled, true, (hipStream_t)stream);
 }
 
 extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const int* row_of_pair,
@@ -564,7 +876,7 @@ extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, con
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W, stride_we, S, stride_se, N, K, E,
                   grp_expert, grp_start, G, row_of_pair, nullptr, 0.f, nullptr, 0, nullptr, 0, y, ldy, N / 256, 0, n_pairs};
-    return launch_prefill(a, 1, tiled, (hipStream_t)stream);
+    return launch_prefill(a, 1, tiled, false, (hipStream_t)stream);
 }
 
 extern "C" int dsv41_combine_pairs(const float* y2, long long ldy2, const int* inv, int topk, int T, int N, const uint16_t* ys, long long ldys,

@@ -334,13 +334,14 @@ class PrefillState:
         self.__dict__.update(kw)
 
 
-# pairs per group of the prefill path's dispatch (the prefill kernels take groups of up to this many pairs)
-PREFILL_GROUP = 128
+# pairs per group of the prefill path's dispatch: its launches take groups of up to 256 pairs (groups of more than
+# 128 on a 256-pair tile), so a popular expert's weights are streamed by half as many groups
+PREFILL_GROUP = 256
 
 
 def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float) -> PrefillState:
     """First half of the prefill path: xq bf16 [T, H] on the FP8 grid -> E4M3 codes (exact); (token, expert) pairs
-    bucketed by expert in groups of <= 128 (moe_dispatch, p2p.cu:90-132); the w13 GEMM with the SwiGLU/FP8
+    bucketed by expert in groups of <= PREFILL_GROUP (moe_dispatch, p2p.cu:90-132); the w13 GEMM with the SwiGLU/FP8
     epilogue: h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) (model.py:584-587, fused.py:284-306)."""
     from .hipkern import moe_dispatch
     from .quant import quant_fp8_e8m0

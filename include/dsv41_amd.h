@@ -124,7 +124,8 @@ int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, 
                        const float* hpost, const float* hcomb, const uint8_t* Ss2,
                        long long ldss2, void* stream);
 
-/* Prefill w13 + SwiGLU: for every group g of <= 128 expert-sorted pairs (moe_dispatch tables with gmax 128),
+/* Prefill w13 + SwiGLU: for every group g of <= 256 expert-sorted pairs (moe_dispatch tables with gmax <= 256;
+ * groups of more than 128 pairs run on a 256-pair tile),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;
  * x as E4M3 codes xc [x_rows][ldx] + E8M0 xs [x_rows][ldxs] (x_rows * ldx < 2^32); h as FP8 codes hc [P][ldhc]
  * + E8M0 hs [P][ldhs] in sorted pair order. H % 128 == 0, H >= 384, I % 64 == 0. Replaces the w13 grouped_fp4_gemm + swiglu_quant of
