@@ -662,6 +662,240 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
     }
 }
 
+// ------------------------------------------------------------------------------------------ decode w2 + sum, split
+// For token counts whose h rows do not fit LDS at once (dsv41_moe_down_sum_split; M > 4 at top-8): the expert groups
+// are split into S runs of Q consecutive pair rows (a group belongs to the run holding its first row), and workgroup
+// (rb, s) computes output rows 128 rb .. 128 rb + 127 (wave w: the 16-row block 8 rb + w) over run s's groups. The
+// run's h rows (<= Q + M - 1 <= DX_ROWS - 1) and a zero row sit in LDS, so every 1 KiB weight tile costs one
+// vector-memory instruction and its B operand (column t = token t) comes from LDS; a group's weight scales take one
+// wide load when the wave enters it. part[s][t][n] receives the run's sums; down_reduce_kernel adds the S partials
+// in run order and applies the epilogue of moe_down_sum_kernel.
+#define DX_ROWS 32
+#define DX_MAXG 32
+
+template <int TILED, int PF>
+__global__ void __launch_bounds__(DS_WAVES * 64, 2) moe_down_split_kernel(const DownSumArgs a, float* __restrict__ part, int Q) {
+    extern __shared__ __align__(16) uint8_t smem[];   // h codes [DX_ROWS][K + 16], then their E8M0 bytes [DX_ROWS][K / 32]
+    __shared__ int s_gs[DS_MAX_SLOTS + 1];
+    __shared__ int s_ge[DS_MAX_SLOTS];
+    __shared__ short s_tok[DS_MAX_SLOTS];
+    __shared__ int s_ex[DX_MAXG];                      // expert of the run's j-th group with an expert of this shard
+    __shared__ signed char s_pair[DX_MAXG][16];        // LDS row of token t's pair in that group (DX_ROWS - 1: none)
+    __shared__ int s_lo, s_hi;
+    __shared__ __align__(16) uint8_t s_sc[DS_WAVES][1024];   // the wave's current group's weight scales
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.x, s = blockIdx.y;
+    const int K = a.K, Ks = K >> 5, LS = K + 16, nk = K >> 7, Kh = K >> 1;
+    const int n_slots = a.n_slots, M = a.M;
+    const int nb = rb * 8 + wave;
+    const int w0 = s * Q, w1 = w0 + Q;
+
+    // ---- tables, one round trip
+    for (int i = tid; i <= n_slots; i += DS_WAVES * 64) s_gs[i] = a.grp_start[i];
+    for (int i = tid; i < n_slots; i += DS_WAVES * 64) {
+        s_ge[i] = a.grp_expert[i];
+        s_tok[i] = (short)a.tok_sorted[i];
+    }
+    if (tid == 0) {
+        s_lo = DS_MAX_SLOTS;
+        s_hi = -1;
+    }
+    __syncthreads();
+    // the run's groups: first row in [w0, w1), expert id set (padding groups carry -1); they are consecutive
+    for (int g = tid; g < n_slots; g += DS_WAVES * 64) {
+        const int st = s_gs[g];
+        if (s_ge[g] >= 0 && st >= w0 && st < w1 && s_gs[g + 1] > st) {
+            atomicMin(&s_lo, g);
+            atomicMax(&s_hi, g);
+        }
+    }
+    __syncthreads();
+    const int g0 = s_lo, g1 = s_hi + 1;   // g1 <= g0 when the run is empty
+    const int ng = g1 > g0 ? g1 - g0 : 0;
+    const int r0 = ng ? s_gs[g0] : 0, nr = ng ? s_gs[g1] - r0 : 0;   // <= Q + M - 1 rows
+
+    // ---- the run's h rows into registers (16-byte vectors; past the rows the offset is beyond the descriptor: zeros)
+    const int vpr = K >> 4;
+    constexpr int NHV = (DX_ROWS * 2048 / 16 + DS_WAVES * 64 - 1) / (DS_WAVES * 64);   // K <= 2048
+    constexpr int NHS = (DX_ROWS * 64 + DS_WAVES * 64 - 1) / (DS_WAVES * 64);            // K / 32 <= 64
+    v4i HV[NHV];
+    int HS[NHS];
+    const __amdgpu_buffer_rsrc_t hr = buffer_rsrc(a.hc + (long long)r0 * a.ldh, (uint32_t)(nr > 0 ? (long long)(nr - 1) * a.ldh + K : 0));
+    const __amdgpu_buffer_rsrc_t hsr = buffer_rsrc(a.hs + (long long)r0 * a.ldhs, (uint32_t)(nr > 0 ? (long long)(nr - 1) * a.ldhs + Ks : 0));
+#pragma unroll
+    for (int i = 0; i < NHV; ++i) {
+        const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
+        HV[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(hr, r < nr ? (uint32_t)(r * a.ldh + v * 16) : 0xFFFFFFF0u, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < NHS; ++i) {
+        const int idx = i * DS_WAVES * 64 + tid, r = idx / Ks, v = idx - r * Ks;
+        HS[i] = buffer_load_byte(hsr, r < nr ? (uint32_t)(r * a.ldhs + v) : 0xFFFFFFF0u, 0);
+    }
+    // the run's groups with an expert of this shard, compacted in order (wave 0: one lane per group), with their
+    // token -> LDS row maps
+    if (wave == 0) {
+        const int g = g0 + lane;
+        int e = -1;
+        if (lane < ng) {
+            e = s_ge[g] - a.shard_start;
+            if (e >= a.shard_n) e = -1;
+        }
+        const unsigned long long vm = __ballot(e >= 0);
+        if (e >= 0) {
+            const int j = __popcll(vm & ((1ull << lane) - 1ull));
+            s_ex[j] = e;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) s_pair[j][t] = (signed char)(DX_ROWS - 1);
+            for (int q = s_gs[g]; q < s_gs[g + 1]; ++q) s_pair[j][s_tok[q] & 15] = (signed char)(q - r0);
+        }
+        if (lane == 0) s_lo = __popcll(vm);   // the count, read back after the barrier
+    }
+    // h rows into LDS (row DX_ROWS - 1: zeros, scale byte 127)
+    uint8_t* const hs_l = smem + (size_t)DX_ROWS * LS;
+#pragma unroll
+    for (int i = 0; i < NHV; ++i) {
+        const int idx = i * DS_WAVES * 64 + tid, r = idx / vpr, v = idx - r * vpr;
+        if (r < DX_ROWS - 1) *(v4i*)(smem + r * LS + v * 16) = HV[i];
+    }
+    for (int v = tid; v < vpr; v += DS_WAVES * 64) *(v4i*)(smem + (DX_ROWS - 1) * LS + v * 16) = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < NHS; ++i) {
+        const int idx = i * DS_WAVES * 64 + tid, r = idx / Ks;
+        if (r < DX_ROWS - 1) hs_l[idx] = (uint8_t)HS[i];
+    }
+    for (int v = tid; v < Ks; v += DS_WAVES * 64) hs_l[(DX_ROWS - 1) * Ks + v] = 127;
+    __syncthreads();
+
+    // ---- this wave's row block over the compacted groups: (group j, k-chunk kc) tiles through a PF-deep pipeline
+    const int nv = __builtin_amdgcn_readfirstlane(s_lo);
+    const int ex_l = lane < nv ? s_ex[lane] : 0;   // lane j holds group j's expert
+    const int col = lane & 15, kb = lane >> 4;
+    const uint32_t wv = (uint32_t)wtile_off<TILED>(nb, 0, nk, Kh, lane);
+    const int ws = TILED ? 1024 : 64;
+    const int total = nv * nk;
+    // producer iterator: group pj, k-chunk pkc, expert pe
+    int pj = 0, pkc = 0;
+    long long pe = nv > 0 ? __builtin_amdgcn_readlane(ex_l, 0) : 0;
+    v4i A[PF], GA[PF];
+    auto load = [&](int slot, int) {
+        const uint32_t wb = pj < nv ? (uint32_t)a.stride_we : 0u, sbn = pj < nv ? (uint32_t)a.stride_se : 0u;
+        if (pkc == 0) {   // the producer enters a group: its weight scales for this row block, with the slot's tile
+            const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + pe * a.stride_se, sbn);
+            if (TILED) {
+                GA[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                    sr, lane * 16 < nk * 64 ? (uint32_t)(nb * nk * 64 + lane * 16) : 0xFFFFFFF0u, 0, 0));
+            } else {
+                int gg[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    gg[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, kc < nk ? (uint32_t)((nb * 16 + r) * Ks + kc * 4) : 0xFFFFFFF0u, 0, 0);
+                }
+                GA[slot] = v4i{gg[0], gg[1], gg[2], gg[3]};
+            }
+        }
+        A[slot] = buffer_load_tile(buffer_rsrc(a.W + pe * a.stride_we, wb), wv, (uint32_t)(pkc * ws));
+        if (++pkc == nk) {
+            pkc = 0;
+            ++pj;
+            pe = pj < nv ? __builtin_amdgcn_readlane(ex_l, pj) : 0;
+        }
+    };
+    // consumer iterator: group cj, k-chunk ckc; the lane's h row (token col) of the current group
+    int cj = 0, ckc = 0;
+    const uint8_t* hb = smem;
+    const uint8_t* hsb = hs_l;
+    auto group_rows = [&]() {
+        const int q = cj < nv ? (int)s_pair[cj][col] : DX_ROWS - 1;
+        hb = smem + q * LS + kb * 16;
+        hsb = hs_l + q * Ks + kb;
+    };
+    group_rows();
+    uint8_t* const wsc = s_sc[wave];
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    auto use = [&](int slot) {
+        if (ckc == 0) {   // the consumer enters a group: its weight scales into the wave's LDS region (k-chunk kc at 64 kc)
+            if (TILED) {
+                if (lane * 16 < nk * 64) *(v4i*)(wsc + lane * 16) = GA[slot];
+            } else {
+                const int gg[4] = {GA[slot].x, GA[slot].y, GA[slot].z, GA[slot].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = 64 * i + lane, r = idx & 15, kc = idx >> 4;
+                    if (kc < nk) *(int*)(wsc + kc * 64 + r * 4) = gg[i];
+                }
+            }
+        }
+        const v4i b0 = *(const v4i*)hb;
+        const v4i b1 = *(const v4i*)(hb + 64);
+        const int sb = *hsb;
+        const int sa = wsc[ckc * 64 + col * 4 + kb];
+        hb += 128;
+        hsb += 4;
+        acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, sa, sb);
+        if (++ckc == nk) {
+            ckc = 0;
+            ++cj;
+            group_rows();
+        }
+    };
+    pipelined<PF>(total, load, use);
+    if (col < M) {
+        float* o = part + ((long long)s * M + col) * a.N + nb * 16 + 4 * kb;
+        *(v4f*)o = acc;
+    }
+}
+
+// y[t][n] = sum over the S runs of part[s][t][n] (run order), then the epilogue of moe_down_sum_kernel: the fp32 sum,
+// bf16(y + ys), the hyper-connection post mix. One thread per 4 consecutive n.
+__global__ void __launch_bounds__(256) down_reduce_kernel(const DownSumArgs a, const float* __restrict__ part, int S) {
+    const int M = a.M, N = a.N, nq = N >> 2;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * nq) return;
+    const int col = idx / nq, row0 = (idx - col * nq) * 4;
+    v4f sum = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < S; ++s) sum += *(const v4f*)(part + ((long long)s * M + col) * N + row0);
+    if (a.y) *(v4f*)(a.y + (long long)col * a.ldy + row0) = sum;
+    if (a.yb || a.hres) {
+        const float v[4] = {sum.x, sum.y, sum.z, sum.w};
+        float xo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = v[i];
+            if (a.ys) t += bf16_to_f32(a.ys[(long long)col * a.ldys + row0 + i]);
+            const uint32_t tb = f32_to_bf16_bits(t);
+            xo[i] = bf16_to_f32(tb);
+            if (a.yb) a.yb[(long long)col * a.ldyb + row0 + i] = (uint16_t)tb;
+        }
+        if (a.hres) {
+            uint16_t* r = a.hres + (long long)col * 4 * N + row0;
+            const float* pb = a.hpost + col * 4;
+            const float* cb = a.hcomb + col * 16;
+            float rv[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint2 u = *(const uint2*)(r + (long long)j * N);
+                rv[j][0] = bf16_to_f32(u.x & 0xFFFFu); rv[j][1] = bf16_to_f32(u.x >> 16);
+                rv[j][2] = bf16_to_f32(u.y & 0xFFFFu); rv[j][3] = bf16_to_f32(u.y >> 16);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t o[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float acc = pb[q] * xo[c];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc = fmaf(cb[j * 4 + q], rv[j][c], acc);
+                    o[c] = f32_to_bf16_bits(acc);
+                }
+                *(uint2*)(r + (long long)q * N) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------ C ABI
 #define B_LDS_MAX_BYTES (48 * 1024)
 
@@ -772,5 +1006,50 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     else if (gs) { if (tiled) DS_LAUNCH(1, 6, 0, 0, 2); else DS_LAUNCH(0, 6, 0, 0, 2); }
     else { if (tiled) DS_LAUNCH(1, 8, 0, 0, 0); else DS_LAUNCH(0, 8, 0, 0, 0); }
 #undef DS_LAUNCH
+    return (int)hipGetLastError();
+}
+
+// The down projection for M tokens through the run-split kernel and the fixed-order reduction (two launches); part:
+// fp32 workspace of at least S * M * N floats, S = ceil(n_slots / Q) (at least 1), Q = max(1, min(32 - M,
+// ceil(n_slots / 8))).
+extern "C" int dsv41_moe_down_sum_split(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
+                                        int N, int K, const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs,
+                                        const int* grp_expert, const int* grp_start, const int* tok_sorted, int n_slots, int M,
+                                        float* y, long long ldy, const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb,
+                                        int shard_start, int shard_n, uint16_t* hres, const float* hpost, const float* hcomb,
+                                        float* part, long long part_floats, void* stream) {
+    if (!W || !S || !hc || !hs || !grp_expert || !grp_start || !tok_sorted || !part || (!y && !yb && !hres)) return DSV41_EINVAL;
+    if (hres && (!hpost || !hcomb || (((uintptr_t)hres) & 7))) return DSV41_EINVAL;
+    if (N <= 0 || (N & 127) || K < 128 || K > 2048 || (K & 127) || n_slots < 0 || n_slots > DS_MAX_SLOTS || M < 1 || M > 16)
+        return DSV41_EINVAL;
+    if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
+        stride_se < (long long)N * (K / 32))
+        return DSV41_EINVAL;
+    // the weight scales take 16-byte loads (tiled) or 4-byte loads (row-major); h rows 16-byte vectors, 32-bit offsets
+    if ((((uintptr_t)S) & 15) || (stride_se & 15) || (ldh & 15) || (((uintptr_t)hc) & 15) || ldh < K || ldhs < K / 32 ||
+        (long long)n_slots * ldh + K > 0xFFFFFFFFll || (long long)n_slots * ldhs + K / 32 > 0xFFFFFFFFll)
+        return DSV41_EINVAL;
+    if ((y && (ldy < N || (ldy & 3) || (((uintptr_t)y) & 15))) || (yb && ldyb < N) || (yb && ys && ldys < N) || (((uintptr_t)part) & 15))
+        return DSV41_EINVAL;
+    // runs of Q pair rows: at least 8 runs (so the grid fills the CUs), at most 32 - M rows each (the LDS rows)
+    const int Q = max(1, min(32 - M, (n_slots + 7) / 8)), runs = n_slots > 0 ? (n_slots + Q - 1) / Q : 1;
+    if (part_floats < (long long)runs * M * N) return DSV41_EINVAL;
+    DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, n_slots, grp_expert, grp_start, tok_sorted, n_slots, M,
+                  y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, nullptr, 0, nullptr, 0, 0.f, nullptr, 0, 0,
+                  hres, hpost, hcomb, nullptr, 0};
+    hipStream_t st = (hipStream_t)stream;
+    const size_t lds = (size_t)DX_ROWS * (K + 16) + (size_t)DX_ROWS * (K / 32);
+    const dim3 grid(N / 128, runs), block(DS_WAVES * 64);
+#define DX_LAUNCH(T)                                                                                                  \
+    do {                                                                                                          \
+        const hipError_t err = hipFuncSetAttribute((const void*)moe_down_split_kernel<T, 8>,                     \
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);         \
+        if (err != hipSuccess) return (int)err;                                                                   \
+        moe_down_split_kernel<T, 8><<<grid, block, lds, st>>>(a, part, Q);                                        \
+    } while (0)
+    if (tiled) DX_LAUNCH(1); else DX_LAUNCH(0);
+#undef DX_LAUNCH
+    const int nthr = M * (N / 4);
+    down_reduce_kernel<<<(nthr + 255) / 256, 256, 0, st>>>(a, part, runs);
     return (int)hipGetLastError();
 }

@@ -133,6 +133,15 @@ class _Workspace:
         self.wt = torch.empty(M, k, dtype=f32, device=dev)
         self.gus = torch.empty(M, 2 * I, dtype=torch.bfloat16, device=dev)   # the fused shared expert's gate/up
         self.shared = None                                          # the SharedExpert of the last decode_up, if fused
+        self.part = None                                            # run-split down projection: partial sums
+
+
+def _down_split(ws: "_Workspace", ex: ExpertWeights) -> bool:
+    """Whether the down projection runs split over runs of pair rows (dsv41_moe_down_sum_split): when the h rows do not
+    fit the one-launch kernel's LDS (60 KiB with their E8M0 bytes), for intermediate sizes it takes."""
+    I, R = ex.I, ws.P + 1
+    staged = R * (I + 16 + I // 32) <= 60 * 1024 and R * (I // 16) <= 8 * 512 and R * (I // 32) <= 4 * 512
+    return not staged and I % 128 == 0 and I <= 2048 and ex.H % 128 == 0
 
 
 def fused_shared_ok(M: int, k: int, I: int, fp8: bool = False) -> bool:
@@ -206,12 +215,14 @@ def decode_up(xq, ex: ExpertWeights, limit: float, k: int, logits=None, gate=Non
     return ws
 
 
-def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, limit: float = 0.0, ys_out=None, hc=None):
+def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, limit: float = 0.0, ys_out=None, hc=None,
+                split: bool | None = None):
     """The second decode launch (dsv41_moe_down_sum): y[t] = sum over t's groups of h . deq(W2[e])^T (fp32, into
     y32 or the workspace) and/or out = bf16(y + ys). When decode_up ran with the shared expert, this launch finishes it
     (SwiGLU with `limit`, Ws2) and adds its bf16 output instead of `ys` (ys_out, bf16 [M, H], receives it).
     hc = (residual bf16 [M, 1, 4, H], post fp32 [M, 4], comb fp32 [M, 4, 4]): the hyper-connection post mix
-    (fused2.hc_post2_) applied to bf16(y + ys) in the same launch, in place on residual."""
+    (fused2.hc_post2_) applied to bf16(y + ys) in the same launch, in place on residual. split: run-split form
+    (dsv41_moe_down_sum_split) or not; None: when the h rows do not fit the one-launch kernel's LDS."""
     dev = _lib.require_cuda(ws.hc, ys, out, y32, ys_out)
     hres = hpost = hcomb = None
     if hc is not None:
@@ -226,6 +237,19 @@ def decode_down(ws: _Workspace, ex: ExpertWeights, ys=None, out=None, y32=None, 
     if ws.shared is not None:
         Ws2, Ss2 = ws.shared.w2, ws.shared.s2
         assert ys is None
+    elif _down_split(ws, ex) if split is None else split:
+        q = max(1, min(32 - M, (ws.P + 7) // 8))   # pair rows per run, as dsv41_moe_down_sum_split chooses them
+        runs = max(1, (ws.P + q - 1) // q)
+        if ws.part is None or ws.part.numel() < runs * M * H:
+            ws.part = torch.empty(runs * M * H, dtype=torch.float32, device=dev)
+        _lib.call("dsv41_moe_down_sum_split", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H,
+                  ex.I, _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start),
+                  _lib.ptr(ws.tok_sorted), ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),
+                  _lib.ptr(out), H if out is None else out.stride(0), 0, ex.E, _lib.ptr(hres), _lib.ptr(hpost), _lib.ptr(hcomb),
+                  _lib.ptr(ws.part), ws.part.numel(), _lib.stream(dev))
+        if hc is not None and out is None:
+            return hres
+        return out if out is not None else y
     _lib.call("dsv41_moe_down_sum", _lib.ptr(ex.w2), ex.w2.stride(0), _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, H, ex.I,
               _lib.ptr(ws.hc), ws.hc.stride(0), _lib.ptr(ws.hs), ws.hs.stride(0), ws.P, _lib.ptr(ws.grp_expert), _lib.ptr(ws.grp_start),
               _lib.ptr(ws.tok_sorted), ws.P, M, _lib.ptr(y) if want_y else None, y.stride(0), _lib.ptr(ys), H if ys is None else ys.stride(0),

@@ -124,6 +124,20 @@ int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const uint8_t* S, 
                        const float* hpost, const float* hcomb, const uint8_t* Ss2,
                        long long ldss2, void* stream);
 
+/* The down projection of dsv41_moe_down_sum (no fused shared expert) for M tokens whose h rows do not fit LDS at
+ * once: the groups are split into runs of Q = max(1, min(32 - M, ceil(n_slots / 8))) consecutive pair rows, each
+ * workgroup computes 128 output rows over one run with that run's h rows in LDS, and a second launch adds the runs'
+ * fp32 partial sums in run order before the epilogue (y, bf16(y + ys), the hyper-connection post mix). part: fp32
+ * workspace of at least S * M * N floats, S = ceil(n_slots / Q) (>= 1). N % 128 == 0, K % 128 == 0, K <= 2048.
+ * Replaces the same calls as
+ * dsv41_moe_down_sum (decode.py:324-335). */
+int dsv41_moe_down_sum_split(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled, int N, int K,
+                             const uint8_t* hc, long long ldh, const uint8_t* hs, long long ldhs, const int* grp_expert,
+                             const int* grp_start, const int* tok_sorted, int n_slots, int M, float* y, long long ldy,
+                             const uint16_t* ys, long long ldys, uint16_t* yb, long long ldyb, int shard_start, int shard_n,
+                             uint16_t* hres, const float* hpost, const float* hcomb, float* part, long long part_floats,
+                             void* stream);
+
 /* Prefill w13 + SwiGLU: for every group g of <= 256 expert-sorted pairs (moe_dispatch tables with gmax <= 256;
  * groups of more than 128 pairs run on a 256-pair tile),
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;

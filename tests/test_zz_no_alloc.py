@@ -1,6 +1,7 @@
 """The no-allocation decode entry point (dsv41_moe_experts_noalloc) through the C ABI: the same results as the
-existing entry points (dsv41_moe_decode_up + dsv41_moe_down_sum with caller-owned workspaces), bit for bit, on two
-calls in a row, the second with a smaller input, so the second runs over the scratch contents the first left."""
+existing entry points (dsv41_moe_decode_up + dsv41_moe_down_sum with caller-owned workspaces, the one-launch down
+projection also for 16 tokens), bit for bit, on two calls in a row, the second with a smaller input, so the second runs
+over the scratch contents the first left."""
 import ctypes
 
 import numpy as np
@@ -49,7 +50,7 @@ def _existing(ex, xq, k, limit, logits=None, eid=None, wt=None, ys=None):
         ws = moe.decode_up(xq, ex, limit, k, eid=eid, wt=wt, eid_out=eo, wt_out=wo)
     y = torch.empty(M, H, device=DEV)
     yb = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
-    moe.decode_down(ws, ex, ys=ys, out=yb, y32=y)
+    moe.decode_down(ws, ex, ys=ys, out=yb, y32=y, split=False)
     return y, yb, eo, wo
 
 
