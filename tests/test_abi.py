@@ -113,6 +113,31 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert down(8, Ws2=p, M=3) == -1
 
 
+def test_down_split_rejects_invalid_calls_without_launch():
+    """dsv41_moe_down_sum_split: -1 on the host, nothing launched, for a workspace smaller than its runs' partial sums,
+    an output row count not a multiple of 128, K past 2048, more than 16 tokens or a misaligned workspace."""
+    import ctypes
+    from dsv41_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    H, I = 7168, 1664
+
+    def split(M=16, N=H, K=I, part_floats=None, part=p):
+        P = M * 8
+        q = max(1, min(32 - M, (P + 7) // 8))
+        need = -(-P // q) * M * N
+        return L.dsv41_moe_down_sum_split(p, N * (K // 2), p, N * (K // 32), 1, N, K, p, K, p, K // 32, p, p, p, P, M, p, N, None, N,
+                                          None, N, 0, 384, None, None, None, part, need if part_floats is None else part_floats, None)
+    assert split(part_floats=8 * 16 * H - 1) == -1   # 8 runs of 16 rows at M = 16
+    assert split(M=8, part_floats=8 * 8 * H - 1) == -1
+    assert split(N=H - 64) == -1
+    assert split(K=2176) == -1
+    assert split(M=17) == -1
+    assert split(part=ctypes.c_void_p(24)) == -1
+
+
 def test_noalloc_rejects_calls_beyond_its_scratch():
     """dsv41_moe_experts_noalloc returns -2 (nothing launched, no GPU touched) for a call whose h rows exceed its 2 MiB
     array, and -1 for invalid arguments."""
