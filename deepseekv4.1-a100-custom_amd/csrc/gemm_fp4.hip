@@ -672,6 +672,7 @@ __global__ void __launch_bounds__(DS_WAVES * 64, H_LDS ? 4 : 2) moe_down_sum_ker
 // in run order and applies the epilogue of moe_down_sum_kernel.
 #define DX_ROWS 32
 #define DX_MAXG 32
+#define DX_RUNS 16   // runs: ceil(n_slots / Q) <= 16 for n_slots <= 256, M <= 16
 
 template <int TILED, int PF>
 __global__ void __launch_bounds__(DS_WAVES * 64, 2) moe_down_split_kernel(const DownSumArgs a, float* __restrict__ part, int Q) {
@@ -855,8 +856,15 @@ __global__ void __launch_bounds__(256) down_reduce_kernel(const DownSumArgs a, c
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= M * nq) return;
     const int col = idx / nq, row0 = (idx - col * nq) * 4;
-    v4f sum = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < S; ++s) sum += *(const v4f*)(part + ((long long)s * M + col) * N + row0);
+    // every run's partial in flight at once (S <= DX_RUNS), then summed in run order
+    v4f pv[DX_RUNS];
+#pragma unroll
+    for (int s = 0; s < DX_RUNS; ++s)
+        pv[s] = s < S ? *(const v4f*)(part + ((long long)s * M + col) * N + row0) : v4f{0.f, 0.f, 0.f, 0.f};
+    v4f sum = pv[0];
+#pragma unroll
+    for (int s = 1; s < DX_RUNS; ++s)
+        if (s < S) sum += pv[s];
     if (a.y) *(v4f*)(a.y + (long long)col * a.ldy + row0) = sum;
     if (a.yb || a.hres) {
         const float v[4] = {sum.x, sum.y, sum.z, sum.w};
@@ -1033,6 +1041,7 @@ extern "C" int dsv41_moe_down_sum_split(const uint8_t* W, long long stride_we, c
         return DSV41_EINVAL;
     // runs of Q pair rows: at least 8 runs (so the grid fills the CUs), at most 32 - M rows each (the LDS rows)
     const int Q = max(1, min(32 - M, (n_slots + 7) / 8)), runs = n_slots > 0 ? (n_slots + Q - 1) / Q : 1;
+    if (runs > DX_RUNS) return DSV41_EINVAL;
     if (part_floats < (long long)runs * M * N) return DSV41_EINVAL;
     DownSumArgs a{W, stride_we, S, stride_se, N, K, hc, ldh, hs, ldhs, n_slots, grp_expert, grp_start, tok_sorted, n_slots, M,
                   y, ldy, ys, ldys, yb, ldyb, shard_start, shard_n, nullptr, 0, nullptr, 0, 0.f, nullptr, 0, 0,
