@@ -293,7 +293,8 @@ def test_decode_down_h_rows_global(tiled, M, I):
     global memory. I <= 2048 takes the per-group scale loads (I = 640: 20 scale bytes per row, so the 16-byte h scale
     loads of a row overlap; I = 512: exactly 16); I = 2560 (20 k-chunks) the per-tile scale bytes. Checked against the
     oracle's w2 on the kernel's own h (the up projection's FP8 rounding is covered by the tests above), and bit for bit
-    against the per-tile scale path on the same h (forced by a 4-byte-misaligned h scale row stride)."""
+    against the per-tile scale path on the same h (forced by a 4-byte-misaligned h scale row stride). The one-launch
+    kernel (dsv41_moe_down_sum) throughout: at these sizes the default is the run-split form, tested below."""
     import copy
     from dsv41_amd import moe, quant
     E, H, k = 24, 1024, 8
@@ -303,7 +304,7 @@ def test_decode_down_h_rows_global(tiled, M, I):
     eid, wt = rand_routing(M, E, k, 7 * M)
     xq = quant.fake_quant_fp8(rand_x(M, H, 7 * M).to(DEV))
     ws = moe.decode_up(xq, ex, 10.0, k, eid=torch.from_numpy(eid).to(DEV), wt=torch.from_numpy(wt).to(DEV))
-    y = moe.decode_down(ws, ex).clone()
+    y = moe.decode_down(ws, ex, split=False).clone()
     ge, gs, tok = ws.grp_expert.cpu().numpy(), ws.grp_start.cpu().numpy(), ws.tok_sorted.cpu().numpy()
     h = _e4m3_values(ws.hc[:P], ws.hs[:P])
     y2 = O.grouped_gemm(h, w[2].cpu().numpy(), w[3].cpu().numpy(), ge, gs, np.arange(P, dtype=np.int32), int(np.count_nonzero(ge >= 0)))
@@ -315,8 +316,51 @@ def test_decode_down_h_rows_global(tiled, M, I):
     ws2 = copy.copy(ws)
     ws2.hs = hs_wide[:, :Ks]
     y_tile = torch.empty(M, H, dtype=torch.float32, device=DEV)
-    moe.decode_down(ws2, ex, y32=y_tile)
+    moe.decode_down(ws2, ex, y32=y_tile, split=False)
     assert torch.equal(y, y_tile), f"per-group vs per-tile scale loads differ: max {float((y - y_tile).abs().max())}"
+
+
+@pytest.mark.parametrize("M,I,tiled", [(5, 2048, True), (8, 1024, False), (16, 1024, True)])
+def test_decode_down_split_drops_ids_and_post_mix(M, I, tiled):
+    """The run-split down projection (dsv41_moe_down_sum_split; taken by default when M > 4 tokens' h rows overflow the
+    one-launch kernel's LDS) with ids outside [0, E) (the offload dummy slot E, E + 7, -1): those pairs are dropped and
+    the layer matches the oracle with their weights zeroed; it agrees with the one-launch kernel on the same h to fp32
+    rounding (its runs' partial sums add in another order); bf16(y + ys) equals the rounding of its own fp32 y bit for
+    bit, and its hyper-connection post mix equals hc_post2_ on its own bf16 output bit for bit."""
+    from dsv41_amd import fused2, moe, quant
+    E, H, k = 32, 1024, 8
+    w = make_experts(E, H, I, 880 + M)
+    ex = to_ex(*w, tiled)
+    eid, wt = rand_routing(M, E, k, 881 + M)
+    eid[0, 2], eid[M - 1, 5], eid[M // 2, 0] = E, -1, E + 7
+    xq = quant.fake_quant_fp8(rand_x(M, H, 882 + M).to(DEV))
+    ws = moe.decode_up(xq, ex, 10.0, k, eid=torch.from_numpy(eid).to(DEV), wt=torch.from_numpy(wt).to(DEV))
+    assert moe._down_split(ws, ex)
+    y = moe.decode_down(ws, ex).clone()
+    valid = (eid >= 0) & (eid < E)
+    ref = O.moe_layer_routed(bf16_vals(xq), np.where(valid, eid, 0), np.where(valid, wt, 0).astype(np.float32),
+                             *[t.cpu().numpy() for t in w], I, 10.0)
+    close(y.cpu().numpy(), ref, f"split down M={M} I={I} tiled={tiled}, dropped ids")
+    y1 = torch.empty_like(y)
+    moe.decode_down(ws, ex, y32=y1, split=False)
+    yn, y1n = y.cpu().numpy(), y1.cpu().numpy()
+    rms = float(np.sqrt(np.mean(y1n.astype(np.float64) ** 2)))
+    assert np.all(np.abs(yn - y1n) <= 1e-5 * (np.abs(y1n) + rms)), f"split vs one launch: max {np.abs(yn - y1n).max():.3e}"
+    rng = np.random.default_rng(883 + M)
+    ys = torch.from_numpy(O.f32_to_bf16_bits(rng.standard_normal((M, H)).astype(np.float32)).view(np.int16)).view(torch.bfloat16).to(DEV)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device=DEV)
+    moe.decode_down(ws, ex, ys=ys, out=out)
+    u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(u16(out), O.f32_to_bf16_bits((yn + bf16_vals(ys)).astype(np.float32)))
+    res0 = torch.from_numpy(O.f32_to_bf16_bits(rng.standard_normal((M, 1, 4, H)).astype(np.float32)).view(np.int16)).view(torch.bfloat16).to(DEV)
+    post = torch.from_numpy(rng.standard_normal((M, 4)).astype(np.float32)).to(DEV)
+    comb = torch.from_numpy(rng.standard_normal((M, 4, 4)).astype(np.float32)).to(DEV)
+    res_ref = res0.clone()
+    fused2.hc_post2_(out, res_ref, post, comb)
+    res = res0.clone()
+    moe.decode_down(ws, ex, ys=ys, hc=(res, post, comb))
+    torch.cuda.synchronize()
+    assert torch.equal(res, res_ref)
 
 
 @pytest.mark.parametrize("M,func,norm", [(1, "softmax", True), (3, "sigmoid", True), (16, "sqrtsoftplus", True), (5, "softmax", False)])
