@@ -173,6 +173,90 @@ __global__ void __launch_bounds__(256) swiglu_quant_kernel(const void* __restric
     }
 }
 
+// The same per-element arithmetic, 16 columns per lane (a 32-column group is two adjacent lanes): 16-byte loads of gate
+// and up, 16-byte stores of the codes and bf16 values. Needs 16-byte aligned rows and outputs.
+__device__ __forceinline__ void load16_f(const void* p, int bf16, long long off, float* f) {
+    if (!bf16) {
+        const v4i* src = (const v4i*)((const float*)p + off);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const v4i w = src[j];
+            f[4 * j] = __int_as_float(w.x); f[4 * j + 1] = __int_as_float(w.y);
+            f[4 * j + 2] = __int_as_float(w.z); f[4 * j + 3] = __int_as_float(w.w);
+        }
+    } else {
+        const v4i* src = (const v4i*)((const uint16_t*)p + off);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const v4i w = src[j];
+            const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f[8 * j + 2 * i] = bf16_to_f32(wd[i] & 0xFFFFu);
+                f[8 * j + 2 * i + 1] = bf16_to_f32(wd[i] >> 16);
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) swiglu_quant_vec_kernel(const void* __restrict__ gu, int gu_bf16, long long ld_gu, const float* __restrict__ wt,
+                                                               unsigned n_chunks, int inter, float limit, uint8_t* __restrict__ codes,
+                                                               uint8_t* __restrict__ scales, uint16_t* __restrict__ hb, int permute) {
+    const unsigned t = blockIdx.x * 256u + threadIdx.x;   // 16-column chunk; a 32-group's two chunks are adjacent lanes
+    if (t >= n_chunks) return;                            // n_chunks is even, so a lane pair is active together
+    const unsigned cpr = (unsigned)inter >> 4;
+    const unsigned r = t / cpr, ch = t - r * cpr;
+    const int c0 = (int)ch * 16;
+    float g[16], u[16];
+    load16_f(gu, gu_bf16, (long long)r * ld_gu + c0, g);
+    load16_f(gu, gu_bf16, (long long)r * ld_gu + inter + c0, u);
+    const float w = wt ? wt[r] : 1.f;
+    float h[16];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float gg = g[i], uu = u[i];
+        if (limit > 0.f) {
+            uu = fminf(fmaxf(uu, -limit), limit);
+            gg = fminf(gg, limit);
+        }
+        float v = gg * (1.0f / (1.0f + expf(-gg))) * uu;
+        if (wt) v = v * w;
+        v = bf16_round(v);
+        h[i] = v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
+    const int e = fq8_exponent(amax);
+    uint32_t q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = fq8_code(h[i], e);
+    if (codes) {
+        uint32_t cw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cw[j] = q[4 * j] | (q[4 * j + 1] << 8) | (q[4 * j + 2] << 16) | (q[4 * j + 3] << 24);
+        *(v4i*)(codes + (long long)r * inter + c0) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+    }
+    if (scales && (ch & 1) == 0) scales[(long long)r * (inter >> 5) + (ch >> 1)] = (uint8_t)(e + 127);
+    if (hb) {
+        // permute: column j of the chunk is stored at (j & ~7) | bitrev3(j & 7), a map that is its own inverse, so
+        // output position k holds column perm(k)
+        v4i* dst = (v4i*)(hb + (long long)r * inter + c0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t wd[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k0 = 8 * j + 2 * i, k1 = k0 + 1;
+                const int s0 = permute ? ((k0 & ~7) | ((k0 & 1) << 2) | (k0 & 2) | ((k0 >> 2) & 1)) : k0;
+                const int s1 = permute ? ((k1 & ~7) | ((k1 & 1) << 2) | (k1 & 2) | ((k1 >> 2) & 1)) : k1;
+                wd[i] = f32_to_bf16_bits(fq8_value(q[s0], e)) | (f32_to_bf16_bits(fq8_value(q[s1], e)) << 16);
+            }
+            dst[j] = v4i{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]};
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------ C ABI
 extern "C" int dsv41_dequant_fp4(const uint8_t* w, const uint8_t* s, long long rows, int K, int tiled, uint16_t* out, void* stream) {
     if (!w || !s || !out || rows < 0 || K <= 0 || (K & 31) || (tiled && ((rows & 15) || (K & 127)))) return DSV41_EINVAL;
@@ -204,6 +288,15 @@ extern "C" int dsv41_swiglu_quant(const void* gu, int gu_bf16, long long ld_gu, 
     if (!gu || rows < 0 || inter <= 0 || (inter & 31) || ld_gu < 2LL * inter || (!codes && !scales && !h_bf16)) return DSV41_EINVAL;
     const long long groups = (long long)rows * (inter / 32);
     if (groups == 0) return 0;
+    const int esz = gu_bf16 ? 2 : 4;
+    const bool vec = groups * 2 < (1ll << 31) && (((uintptr_t)gu) & 15) == 0 && ((ld_gu * esz) & 15) == 0 && (((uintptr_t)codes) & 15) == 0 &&
+                     (((uintptr_t)h_bf16) & 15) == 0;
+    if (vec) {
+        const unsigned n_chunks = (unsigned)(groups * 2);
+        swiglu_quant_vec_kernel<<<(n_chunks + 255) / 256, 256, 0, (hipStream_t)stream>>>(gu, gu_bf16, ld_gu, wt, n_chunks, inter, limit, codes,
+                                                                                          scales, h_bf16, permute);
+        return (int)hipGetLastError();
+    }
     swiglu_quant_kernel<<<(unsigned)((groups * 32 + 255) / 256), 256, 0, (hipStream_t)stream>>>(gu, gu_bf16, ld_gu, wt, rows, inter, limit, codes, scales, h_bf16, permute);
     return (int)hipGetLastError();
 }

@@ -879,6 +879,131 @@ extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, con
     return launch_prefill(a, 1, tiled, false, (hipStream_t)stream);
 }
 
+// out[row_out[p]] (+)= fl(wt[p] * y2[p]) for the pairs of every group g with an expert in [0, E) (its first P2_T pairs,
+// those the tile kernels computed), one workgroup per (1024 columns, group, SCAT_ROWS pairs), pairs in slot order. sm: 0
+// store, 1 read, add and write (the output rows are distinct, so no two workgroups touch one element), 2 fp32 atomic
+// adds.
+#define SCAT_UNROLL 8
+#define SCAT_ROWS 32
+__global__ void __launch_bounds__(256) scatter_rows_kernel(const float* __restrict__ y2, long long ldy2, const int* __restrict__ grp_expert,
+                                                           const int* __restrict__ grp_start, int E, int n_pairs,
+                                                           const int* __restrict__ row_out, const float* __restrict__ wt,
+                                                           const int* __restrict__ distinct, int accum, float* out, long long ldo,
+                                                           int out_rows, int N) {
+    const int g = blockIdx.y;
+    const int e = grp_expert[g];
+    if (e < 0 || e >= E) return;
+    const int gp0 = min(max(grp_start[g], 0), n_pairs), gp1 = min(min(grp_start[g + 1], n_pairs), gp0 + P2_T);
+    const int p0 = gp0 + (int)blockIdx.z * SCAT_ROWS, p1 = min(gp1, p0 + SCAT_ROWS);
+    const int c = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= N || p1 <= p0) return;
+    const int d = distinct ? __builtin_amdgcn_readfirstlane(*distinct) : 0;
+    const int sm = d ? (accum ? 1 : 0) : 2;
+    for (int q = p0; q < p1; q += SCAT_UNROLL) {
+        v4f v[SCAT_UNROLL];
+        int r[SCAT_UNROLL];
+        float w[SCAT_UNROLL];
+#pragma unroll
+        for (int i = 0; i < SCAT_UNROLL; ++i) {   // every load of the batch in flight before the first write
+            const int p = min(q + i, p1 - 1);
+            r[i] = q + i < p1 ? row_out[p] : -1;
+            w[i] = wt[p];
+            v[i] = *(const v4f*)(y2 + (long long)p * ldy2 + c);
+        }
+#pragma unroll
+        for (int i = 0; i < SCAT_UNROLL; ++i) {
+            if ((unsigned)r[i] >= (unsigned)out_rows) continue;
+            float* o = out + (long long)r[i] * ldo + c;
+            const v4f pv = v4f{__fmul_rn(v[i].x, w[i]), __fmul_rn(v[i].y, w[i]), __fmul_rn(v[i].z, w[i]), __fmul_rn(v[i].w, w[i])};
+            if (sm == 0) {
+                *(v4f*)o = pv;
+            } else if (sm == 1) {
+                const v4f ov = *(const v4f*)o;
+                *(v4f*)o = v4f{__fadd_rn(ov.x, pv.x), __fadd_rn(ov.y, pv.y), __fadd_rn(ov.z, pv.z), __fadd_rn(ov.w, pv.w)};
+            } else {
+                unsafeAtomicAdd(o, pv.x);
+                unsafeAtomicAdd(o + 1, pv.y);
+                unsafeAtomicAdd(o + 2, pv.z);
+                unsafeAtomicAdd(o + 3, pv.w);
+            }
+        }
+    }
+}
+
+// The reference's grouped GEMM with its weighted output-row epilogue (moe_kernels.py:29-80, 155-200): y2[p] = codes(x)
+// [row] . deq(W[e_g])^T on the mixed 128 / 256-pair tile kernel (groups of up to 256 pairs), then out[row_out[p]] +=
+// fl(wt[p] * y2[p]) in a second launch (an epilogue of that form inside the tile kernel's k-loop made its compiled loop
+// twice as slow).
+extern "C" int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                              const int* row_of_pair, const uint8_t* W, long long stride_we, const uint8_t* S,
+                                              long long stride_se, int tiled, int E, int N, int K, const int* grp_expert, const int* grp_start,
+                                              int G, int n_pairs, const int* row_out, const float* wt, const int* distinct, int accum,
+                                              float* out, long long ldo, int out_rows, float* y2, long long ldy2, void* stream) {
+    if (!xc || !xs || !W || !S || !grp_expert || !grp_start || !row_out || !wt || !out || !y2 || n_pairs < 0 || out_rows < 0 || accum < 0 ||
+        accum > 1)
+        return DSV41_EINVAL;
+    if (!row_of_pair && n_pairs > x_rows) return DSV41_EINVAL;   // without a table, pair p reads input row p
+    if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
+    if (E < 1 || N <= 0 || (N & 255) || K < 128 * PG_PF || (K & 127) || G < 0 || G > 0xFFFF || ldx < K || (ldx & 15) || (((uintptr_t)xc) & 15) ||
+        ldxs < K / 32 || (ldxs & 3) || (((uintptr_t)xs) & 3) || ldo < N || (ldo & 3) || (((uintptr_t)out) & 15) || ldy2 < N || (ldy2 & 3) ||
+        (((uintptr_t)y2) & 15))
+        return DSV41_EINVAL;
+    if (stride_we <= 0 || stride_we > 0xFFFFFFFFll || stride_se <= 0 || stride_se > 0xFFFFFFFFll || stride_we < (long long)N * (K / 2) ||
+        stride_se < (long long)N * (K / 32))
+        return DSV41_EINVAL;
+    if (G == 0 || n_pairs == 0 || out_rows == 0) return 0;
+    hipStream_t st = (hipStream_t)stream;
+    PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W, stride_we, S, stride_se, N, K, E,
+                  grp_expert, grp_start, G, row_of_pair, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy2, N / 256, 0, n_pairs};
+    const int rc = launch_prefill(a, 1, tiled, true, st);
+    if (rc != 0) return rc;
+    const dim3 grid((unsigned)((N + 1023) / 1024), (unsigned)G, P2_T / SCAT_ROWS);
+    scatter_rows_kernel<<<grid, 256, 0, st>>>(y2, ldy2, grp_expert, grp_start, E, n_pairs, row_out, wt, distinct, accum, out, ldo, out_rows, N);
+    return (int)hipGetLastError();
+}
+
+// One workgroup: a bitmap of the output rows in LDS, set by the first n_placed (or n) entries of row_out; an entry whose
+// bit was already set is a repeated row. Rows outside [0, out_rows) are never written, so they are not counted.
+// unchecked: out_rows exceeds the bitmap; the flag is 0 (the atomic form).
+__global__ void __launch_bounds__(1024) rows_distinct_kernel(const int* __restrict__ row_out, int n, const int* __restrict__ n_placed,
+                                                             int out_rows, int unchecked, int* flag) {
+    extern __shared__ unsigned bits[];
+    __shared__ int s_dup;
+    if (unchecked) {
+        if (threadIdx.x == 0) flag[0] = 0;
+        return;
+    }
+    const int nw = (out_rows + 31) >> 5;
+    for (int i = threadIdx.x; i < nw; i += blockDim.x) bits[i] = 0u;
+    if (threadIdx.x == 0) s_dup = 0;
+    __syncthreads();
+    const int cnt = n_placed ? min(max(*n_placed, 0), n) : n;
+    for (int p = threadIdx.x; p < cnt; p += blockDim.x) {
+        const int r = row_out[p];
+        if ((unsigned)r < (unsigned)out_rows) {
+            const unsigned m = 1u << (r & 31);
+            if (atomicOr(&bits[r >> 5], m) & m) s_dup = 1;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) flag[0] = s_dup ? 0 : 1;
+}
+
+#define DISTINCT_MAX_ROWS (1 << 20)   // 128 KiB of bitmap
+
+// GroupedPairs' distinct-rows flag for dsv41_fp4_grouped_gemm_scatter: *flag = 1 when no two of the first n_placed
+// (device int; NULL: n) entries of row_out inside [0, out_rows) are equal, else 0 (also for out_rows beyond the bitmap).
+extern "C" int dsv41_rows_distinct(const int* row_out, int n, const int* n_placed, int out_rows, int* flag, void* stream) {
+    if (!row_out || !flag || n < 0 || out_rows < 0) return DSV41_EINVAL;
+    hipStream_t st = (hipStream_t)stream;
+    const int unchecked = out_rows > DISTINCT_MAX_ROWS ? 1 : 0;
+    const size_t lds = unchecked ? 4 : (size_t)max((out_rows + 31) >> 5, 1) * 4;
+    const hipError_t err = hipFuncSetAttribute((const void*)rows_distinct_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (err != hipSuccess) return (int)err;
+    rows_distinct_kernel<<<1, 1024, lds, st>>>(row_out, n, n_placed, out_rows, unchecked, flag);
+    return (int)hipGetLastError();
+}
+
 extern "C" int dsv41_combine_pairs(const float* y2, long long ldy2, const int* inv, int topk, int T, int N, const uint16_t* ys, long long ldys,
                                    uint16_t* out, long long ldo, float* y32, long long ld32, void* stream) {
     if (!y2 || !inv || topk < 1 || T < 0 || N <= 0 || (N & 3) || ldy2 < N || (ldy2 & 3) || (((uintptr_t)y2) & 15) || (!out && !y32) ||

@@ -39,6 +39,8 @@ SIGNATURES = {
     "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],
     "dsv41_prefill_down": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, LL, P],
     "dsv41_fp4_grouped_gemm_t128": [P, LL, P, LL, I, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, LL, P],
+    "dsv41_rows_distinct": [P, I, P, I, P, P],
+    "dsv41_fp4_grouped_gemm_scatter": [P, LL, P, LL, I, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, P, P, I, P, LL, I, P, LL, P],
     "dsv41_combine_pairs": [P, LL, P, I, I, I, P, LL, P, LL, P, LL, P],
     "dsv41_dense_gemv_bf16": [P, LL, I, I, I, P, LL, I, P, LL, P, LL, P],
     "dsv41_residual_rmsnorm_quant": [P, LL, P, LL, P, F, I, I, P, LL, P, LL, P],

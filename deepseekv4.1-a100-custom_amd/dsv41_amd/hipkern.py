@@ -89,6 +89,42 @@ def grouped_gemm_t128(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: to
     return y
 
 
+def grouped_gemm_scatter(xc: torch.Tensor, xs: torch.Tensor, w: torch.Tensor, s: torch.Tensor, grp_expert: torch.Tensor,
+                         grp_start: torch.Tensor, row_of_pair: torch.Tensor | None, row_out: torch.Tensor, wt: torch.Tensor,
+                         distinct: torch.Tensor | None, accum: bool, out: torch.Tensor, n_pairs: int, tiled: bool,
+                         n_groups: int | None = None, y2: torch.Tensor | None = None) -> torch.Tensor:
+    """out[row_out[p]] += wt[p] * codes(x)[row_of_pair[p]] . deq(W[e_g])^T over the pairs p of the first n_groups
+    groups (<= 256 pairs each; default every table entry); distinct: device int32 scalar, non-zero when no two pairs
+    share an output row (then stores when not accum, else read-add-write; otherwise fp32 atomics); y2: fp32
+    [n_pairs, N] workspace (allocated when None); dsv41_fp4_grouped_gemm_scatter."""
+    dev = _lib.require_cuda(xc, xs, w, s, grp_expert, grp_start, row_of_pair, row_out, wt, distinct, out, y2)
+    E, N, Kh = w.shape
+    K = Kh * 2
+    assert w.stride(2) == 1 and w.stride(1) == Kh and s.stride(2) == 1 and s.stride(1) == K // 32
+    assert out.dtype == torch.float32 and out.stride(-1) == 1 and out.shape[1] >= N
+    assert row_out.dtype == torch.int32 and wt.dtype == torch.float32 and row_out.numel() >= n_pairs and wt.numel() >= n_pairs
+    assert distinct is None or (distinct.dtype == torch.int32 and distinct.numel() == 1)
+    G = grp_expert.numel() if n_groups is None else min(n_groups, grp_expert.numel())
+    if y2 is None:
+        y2 = torch.empty(max(n_pairs, 1), N, device=dev, dtype=torch.float32)
+    assert y2.dtype == torch.float32 and y2.stride(-1) == 1 and y2.shape[0] >= n_pairs and y2.shape[1] >= N
+    _lib.call("dsv41_fp4_grouped_gemm_scatter", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), xc.shape[0], _lib.ptr(row_of_pair),
+              _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 1 if tiled else 0, E, N, K, _lib.ptr(grp_expert), _lib.ptr(grp_start),
+              G, n_pairs, _lib.ptr(row_out), _lib.ptr(wt), _lib.ptr(distinct), 1 if accum else 0, _lib.ptr(out),
+              out.stride(0), out.shape[0], _lib.ptr(y2), y2.stride(0), _lib.stream(dev))
+    return out
+
+
+def rows_distinct(row_out: torch.Tensor, n: int, n_placed: torch.Tensor | None, out_rows: int) -> torch.Tensor:
+    """Device int32 [1]: 1 when no two of the first n_placed (device int32, or n) entries of row_out inside
+    [0, out_rows) are equal; dsv41_rows_distinct."""
+    dev = _lib.require_cuda(row_out, n_placed)
+    assert row_out.dtype == torch.int32 and row_out.numel() >= n and (n_placed is None or n_placed.dtype == torch.int32)
+    flag = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("dsv41_rows_distinct", _lib.ptr(row_out), n, _lib.ptr(n_placed), out_rows, _lib.ptr(flag), _lib.stream(dev))
+    return flag
+
+
 def fp4_gemv_pairs(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, row_in: torch.Tensor, expert: torch.Tensor,
                    wt: torch.Tensor, n_pairs: int, tiled: bool = False) -> torch.Tensor:
     """x: bf16 [rows_in, K]; w: uint8 [E, N, K/2]; s: uint8 [E, N, K/32]; row_in/expert: int32 [pairs];

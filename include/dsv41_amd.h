@@ -168,6 +168,27 @@ int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t*
                                 int K, const int* grp_expert, const int* grp_start, int G, int n_pairs, float* y, long long ldy,
                                 void* stream);
 
+/* moe_kernels.grouped_fp4_gemm with the reference kernel's own epilogue (moe_kernels.py:29-80, 155-200: the tile scaled
+ * by the pair weights, then tl.atomic_add into the output rows), on the prefill tile kernels for groups of up to 256
+ * pairs (128-pair tiles, 256-pair tiles for groups of more than 128): for each group g (expert in [0, E), pairs clamped
+ * to [0, n_pairs), at most the first 256 computed) and pair p: out[row_out[p]][0:N] += fl(wt[p] * (x[row] .
+ * deq(W[e])^T)), row as in dsv41_fp4_grouped_gemm_t128; output rows outside [0, out_rows) are skipped. distinct: a
+ * device int (or NULL) that is non-zero when no two pairs share an output row; then accum == 0 stores (out must hold
+ * zeros beforehand) and accum == 1 reads, adds and writes, deterministically; otherwise fp32 atomic adds (any order,
+ * as the reference's). y2: workspace fp32 [n_pairs][ldy2] (the unweighted pair rows, sorted order). G <= 65535.
+ * N % 256 == 0, K % 128 == 0, K >= 384, ldo % 4 == 0 and ldy2 % 4 == 0, out and y2 16-byte aligned. */
+int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                   const int* row_of_pair, const uint8_t* W, long long stride_we, const uint8_t* S,
+                                   long long stride_se, int tiled, int E, int N, int K, const int* grp_expert, const int* grp_start,
+                                   int G, int n_pairs, const int* row_out, const float* wt, const int* distinct, int accum,
+                                   float* out, long long ldo, int out_rows, float* y2, long long ldy2, void* stream);
+
+/* The distinct-rows flag of dsv41_fp4_grouped_gemm_scatter (no counterpart in the reference, whose kernel always adds
+ * atomically): *flag (device int) = 1 when no two of the first n_placed entries of row_out (n_placed: a device int,
+ * e.g. the dispatch's placed-pair count grp_start[n]; NULL: n) that lie in [0, out_rows) are equal, else 0; 0 without
+ * checking when out_rows > 2^20. One workgroup, no host round trip. */
+int dsv41_rows_distinct(const int* row_out, int n, const int* n_placed, int out_rows, int* flag, void* stream);
+
 /* Combine: y[t] = sum_j y2[inv[t * topk + j]] for j ascending (model.py:589, view(n, k, dim).sum(1)), fp32 into
  * y32 and/or bf16(y + ys) into out (model.py:590-591; ys NULL: no shared expert). inv: moe_dispatch's inverse
  * permutation; an entry of -1 (a dropped pair) contributes nothing. N % 4 == 0. */

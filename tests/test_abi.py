@@ -138,6 +138,36 @@ def test_down_split_rejects_invalid_calls_without_launch():
     assert split(part=ctypes.c_void_p(24)) == -1
 
 
+def test_grouped_scatter_rejects_invalid_calls_without_launch():
+    """dsv41_fp4_grouped_gemm_scatter: -1 on the host, nothing launched, for a missing output-row table, an accum flag
+    other than 0 / 1, N not a multiple of 256, K below 384, a misaligned output, a row stride below N, a missing or
+    misaligned workspace or more groups than one launch's grid rows; 0 with no pairs or no output rows."""
+    import ctypes
+    from dsv41_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)
+    N, K = 512, 768
+
+    def call(n=N, k=K, row_out=p, accum=0, out=p, ldo=N, n_pairs=8, out_rows=8, y2=p, G=4):
+        return L.dsv41_fp4_grouped_gemm_scatter(p, k, p, k // 32, 8, p, p, n * (k // 2), p, n * (k // 32), 1, 4, n, k, p, p, G, n_pairs,
+                                                row_out, p, None, accum, out, ldo, out_rows, y2, n, None)
+    assert call(row_out=None) == -1
+    assert call(accum=2) == -1
+    assert call(n=N + 128) == -1
+    assert call(k=256) == -1
+    assert call(out=ctypes.c_void_p(24)) == -1
+    assert call(ldo=N - 4) == -1
+    assert call(y2=None) == -1
+    assert call(y2=ctypes.c_void_p(20)) == -1
+    assert call(G=65536) == -1
+    assert L.dsv41_rows_distinct(None, 4, None, 4, p, None) == -1
+    assert L.dsv41_rows_distinct(p, -1, None, 4, p, None) == -1
+    assert call(n_pairs=0) == 0
+    assert call(out_rows=0) == 0
+
+
 def test_noalloc_rejects_calls_beyond_its_scratch():
     """dsv41_moe_experts_noalloc returns -2 (nothing launched, no GPU touched) for a call whose h rows exceed its 2 MiB
     array, and -1 for invalid arguments."""

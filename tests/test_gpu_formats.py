@@ -113,6 +113,29 @@ def test_swiglu_quant(limit, weighted, permute):
     assert np.array_equal(vals, got if not permute else O.unpermute_x(got))
 
 
+@pytest.mark.parametrize("bf16_in,weighted,permute", [(False, True, False), (False, False, True), (True, True, False)])
+def test_swiglu_quant_vector_equals_per_element(bf16_in, weighted, permute):
+    """The 16-column-per-lane kernel (16-byte aligned rows) and the per-element kernel (taken for a row base 4 or 8 bytes
+    off alignment) give the same bf16 values, codes and scales bit for bit."""
+    from dsv41_amd import fused
+    g = torch.Generator().manual_seed(6)
+    rows, inter = 37, 1664
+    dt = torch.bfloat16 if bf16_in else torch.float32
+    vals = (torch.randn(rows, 2 * inter, generator=g) * 5).to(dt).to(DEV)
+    wt = torch.rand(rows, generator=g).to(DEV) if weighted else None
+    buf = torch.zeros(rows, 2 * inter + 8, dtype=dt, device=DEV)
+    buf[:, :2 * inter] = vals
+    aligned = buf[:, :2 * inter]
+    buf2 = torch.zeros(rows, 2 * inter + 8, dtype=dt, device=DEV)
+    buf2[:, 2:2 * inter + 2] = vals
+    shifted = buf2[:, 2:2 * inter + 2]
+    assert aligned.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 != 0
+    assert torch.equal(fused.swiglu_quant(aligned, wt, inter, 10.0, permute=permute), fused.swiglu_quant(shifted, wt, inter, 10.0, permute=permute))
+    ca, sa = fused.swiglu_quant_codes(aligned, wt, inter, 10.0)
+    cs, ss = fused.swiglu_quant_codes(shifted, wt, inter, 10.0)
+    assert torch.equal(ca, cs) and torch.equal(sa, ss)
+
+
 def test_swiglu_quant_bf16_input():
     """bf16 gate/up (the shared expert's linear output, fused.py:294): the same values as the fp32 path on the
     bf16 values, bit for bit."""

@@ -184,6 +184,86 @@ def test_big_groups_on_the_128_pair_tile_kernel():
     close(out.cpu().numpy(), ref, "grouped_fp4_gemm block_m 64")
 
 
+def test_grouped_fp4_gemm_scatter_forms():
+    """grouped_fp4_gemm on the tile kernels' weighted epilogue (dsv41_fp4_grouped_gemm_scatter), in the reference's
+    prefill call pattern (one output row per pair, model.py:584-589) and a popular expert of more than 128 pairs (a
+    256-pair tile), ids out of range dropped: with out new the rows are stored, with out given they are read, added
+    and written; both equal fl(w_p * y_p) (+ out) bit for bit, y_p the unweighted pair rows of the 128-pair tile entry
+    on the same sorted pairs, and the oracle within tolerance. Rows shared by pairs take the atomic form, equal to the
+    oracle's sums within tolerance."""
+    from dsv41_amd import hipkern, moe_kernels, quant
+    E, N, K = 6, 512, 768
+    w, s, _, _ = make_experts(E, K, N // 2, 41)
+    wtl, stl = quant.tile_fp4(w), quant.tile_fp4_scales(s)
+    X, P, R = 120, 400, 410
+    x = quant.fake_quant_fp8(rand_x(X, K, 42, 2.0).to(DEV))
+    rng = np.random.default_rng(43)
+    eid = rng.choice(E, P, p=[0.5, 0.1, 0.1, 0.1, 0.1, 0.1]).astype(np.int32)
+    eid[[3, 250]] = [-1, E + 2]
+    rin = rng.integers(0, X, P).astype(np.int32)
+    rout = rng.permutation(R)[:P].astype(np.int32)
+    wgt = rng.random(P).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(DEV)
+    pairs = moe_kernels.GroupedPairs(t(eid), t(rin), t(rout), t(wgt), 64, n_experts=E)
+    assert int(pairs.distinct_rows(R)) == 1
+    ge, gs = pairs.tables(moe_kernels.TILE_GROUP)
+    sizes = np.diff(gs.cpu().numpy())[: int(np.count_nonzero(ge.cpu().numpy() >= 0))]
+    assert sizes.max() > 128                                                 # a 256-pair tile
+    out = moe_kernels.grouped_fp4_gemm(x, wtl, stl, pairs, R, tiled=True)   # stores
+    xc, xs = quant.quant_fp8_e8m0(x)
+    g128, s128 = pairs.tables(128)
+    y2 = torch.zeros(P, N, device=DEV)
+    hipkern.grouped_gemm_t128(xc, xs, wtl, stl, g128, s128, pairs.row_in, y2, P, True)
+    n = int(gs[-1])
+    assert n == P - 2
+    rs = pairs.row_out[:n].long()
+    exp = torch.zeros(R, N, device=DEV)
+    exp[rs] = y2[:n] * pairs.weight[:n, None]
+    assert torch.equal(out, exp)
+    out0 = torch.randn(R, N, device=DEV)
+    out1 = moe_kernels.grouped_fp4_gemm(x, wtl, stl, pairs, R, out=out0.clone(), tiled=True)   # read, add, write
+    exp1 = out0.clone()
+    exp1[rs] = out0[rs] + y2[:n] * pairs.weight[:n, None]
+    assert torch.equal(out1, exp1)
+    ref = np.zeros((R, N), np.float64)
+    xv, wn, sn = bf16_vals(x), w.cpu().numpy(), s.cpu().numpy()
+    for p in range(P):
+        if 0 <= eid[p] < E:
+            ref[rout[p]] += O.gemv_pairs(xv, wn, sn, [rin[p]], [eid[p]], [wgt[p]])[0]
+    close(out.cpu().numpy(), ref, "grouped_fp4_gemm distinct rows")
+    # shared output rows: fp32 atomics
+    rout2 = (rout % 37).astype(np.int32)
+    pairs2 = moe_kernels.GroupedPairs(t(eid), t(rin), t(rout2), t(wgt), 64, n_experts=E)
+    assert int(pairs2.distinct_rows(37)) == 0
+    out2 = moe_kernels.grouped_fp4_gemm(x, wtl, stl, pairs2, 37, tiled=True)
+    ref2 = np.zeros((37, N), np.float64)
+    for p in range(P):
+        if 0 <= eid[p] < E:
+            ref2[rout2[p]] += O.gemv_pairs(xv, wn, sn, [rin[p]], [eid[p]], [wgt[p]])[0]
+    close(out2.cpu().numpy(), ref2, "grouped_fp4_gemm shared rows (atomic)")
+
+
+def test_rows_distinct_flag():
+    """dsv41_rows_distinct: 1 exactly when no two counted entries (the first n_placed, inside [0, out_rows)) repeat a
+    row; 0 unchecked past its 2^20-row bitmap."""
+    from dsv41_amd import hipkern
+    t = lambda a: torch.tensor(np.asarray(a), dtype=torch.int32, device=DEV)
+
+    def f(rows, n_out, placed=None):
+        return int(hipkern.rows_distinct(t(rows), len(rows), None if placed is None else t([placed]), n_out))
+    assert f([3, 1, 2, 0], 4) == 1
+    assert f([3, 1, 3, 0], 4) == 0
+    assert f([3, 1, 7, 7], 4) == 1                    # the repeated row lies outside [0, out_rows): never written
+    assert f([3, 1, -1, -1], 4) == 1
+    assert f([3, 1, 0, 0], 4, placed=3) == 1          # the repeat is past the placed pairs
+    assert f([3, 1, 0, 0], 4, placed=4) == 0
+    rows = np.random.default_rng(3).permutation(300000)[:50000]
+    assert f(rows, 300000) == 1
+    rows[49999] = rows[123]
+    assert f(rows, 300000) == 0
+    assert f([0, 1], (1 << 20) + 1) == 0              # past the bitmap: unchecked, the atomic form
+
+
 def test_t128_entry_bounds():
     """dsv41_fp4_grouped_gemm_t128: group ranges are clamped to n_pairs, input rows outside [0, x_rows) read zeros (rows of
     y for them are 0), rows of pairs outside every group are left untouched; shape errors return -1 before any launch."""
