@@ -801,7 +801,7 @@ __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_mixed_kernel(const Pr
 // mixed: groups of <= 256 pairs (the prefill path's launch); otherwise <= 128 (the 128-pair tile alone)
 static int launch_prefill(PrefillArgs& a, int mode, int tiled, bool mixed, hipStream_t st) {
     a.g_pad = (a.G + 7) & ~7;
-    a.cbw = mode == 0 ? PV_CBW0 : PV_CBW1;
+    a.cbw = (mode == 0 || a.K >= 4096) ? PV_CBW0 : PV_CBW1;   // long k-loops: one column block per workgroup
     a.n_it = (a.n_cb + a.cbw - 1) / a.cbw;
     const long long items = (long long)a.n_it * a.g_pad;   // a multiple of 8
     if (items > 0x7FFFFFFFll) return DSV41_EINVAL;

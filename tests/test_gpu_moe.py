@@ -184,15 +184,17 @@ def test_big_groups_on_the_128_pair_tile_kernel():
     close(out.cpu().numpy(), ref, "grouped_fp4_gemm block_m 64")
 
 
-def test_grouped_fp4_gemm_scatter_forms():
-    """grouped_fp4_gemm on the tile kernels' weighted epilogue (dsv41_fp4_grouped_gemm_scatter), in the reference's
-    prefill call pattern (one output row per pair, model.py:584-589) and a popular expert of more than 128 pairs (a
-    256-pair tile), ids out of range dropped: with out new the rows are stored, with out given they are read, added
-    and written; both equal fl(w_p * y_p) (+ out) bit for bit, y_p the unweighted pair rows of the 128-pair tile entry
-    on the same sorted pairs, and the oracle within tolerance. Rows shared by pairs take the atomic form, equal to the
-    oracle's sums within tolerance."""
+@pytest.mark.parametrize("K", [768, 4096])
+def test_grouped_fp4_gemm_scatter_forms(K):
+    """grouped_fp4_gemm through dsv41_fp4_grouped_gemm_scatter (tile kernel into per-pair rows, then the weighted add
+    into the output rows), in the reference's prefill call pattern (one output row per pair, model.py:584-589), with a
+    popular expert of more than 128 pairs (a 256-pair tile) and ids out of range dropped: with out new the rows are
+    stored, with out given they are read, added and written; both equal fl(w_p * y_p) (+ out) bit for bit, y_p the
+    unweighted pair rows of the 128-pair tile entry on the same sorted pairs, and the oracle within tolerance. Rows
+    shared by pairs take the atomic form, equal to the oracle's sums within tolerance. K = 4096: one column block per
+    workgroup (long k-loops)."""
     from dsv41_amd import hipkern, moe_kernels, quant
-    E, N, K = 6, 512, 768
+    E, N = 6, 512
     w, s, _, _ = make_experts(E, K, N // 2, 41)
     wtl, stl = quant.tile_fp4(w), quant.tile_fp4_scales(s)
     X, P, R = 120, 400, 410
@@ -226,11 +228,13 @@ def test_grouped_fp4_gemm_scatter_forms():
     exp1[rs] = out0[rs] + y2[:n] * pairs.weight[:n, None]
     assert torch.equal(out1, exp1)
     ref = np.zeros((R, N), np.float64)
-    xv, wn, sn = bf16_vals(x), w.cpu().numpy(), s.cpu().numpy()
+    xv, wn, sn = bf16_vals(x).astype(np.float64), w.cpu().numpy(), s.cpu().numpy()
+    dense = [O.dense_weights(wn[e], sn[e]).astype(np.float64) for e in range(E)]
+    pair_row = lambda p: wgt[p] * (dense[eid[p]] @ xv[rin[p]])
     for p in range(P):
         if 0 <= eid[p] < E:
-            ref[rout[p]] += O.gemv_pairs(xv, wn, sn, [rin[p]], [eid[p]], [wgt[p]])[0]
-    close(out.cpu().numpy(), ref, "grouped_fp4_gemm distinct rows")
+            ref[rout[p]] += pair_row(p)
+    close(out.cpu().numpy(), ref, f"grouped_fp4_gemm distinct rows K={K}")
     # shared output rows: fp32 atomics
     rout2 = (rout % 37).astype(np.int32)
     pairs2 = moe_kernels.GroupedPairs(t(eid), t(rin), t(rout2), t(wgt), 64, n_experts=E)
@@ -239,8 +243,8 @@ def test_grouped_fp4_gemm_scatter_forms():
     ref2 = np.zeros((37, N), np.float64)
     for p in range(P):
         if 0 <= eid[p] < E:
-            ref2[rout2[p]] += O.gemv_pairs(xv, wn, sn, [rin[p]], [eid[p]], [wgt[p]])[0]
-    close(out2.cpu().numpy(), ref2, "grouped_fp4_gemm shared rows (atomic)")
+            ref2[rout2[p]] += pair_row(p)
+    close(out2.cpu().numpy(), ref2, f"grouped_fp4_gemm shared rows (atomic) K={K}")
 
 
 def test_rows_distinct_flag():
