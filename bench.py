@@ -54,6 +54,7 @@ def parse():
     ap.add_argument("--prefill-tokens", type=int, default=2048, help="tokens of --prefill-only (2048: configs[3]; 16384: the probe)")
     ap.add_argument("--decode-m", type=int, default=0, help="only the configs[2] decode of this many tokens (for profiling its kernels)")
     ap.add_argument("--stack-only", action="store_true", help="only the configs[4] 20-layer decode stack (for profiling its kernels)")
+    ap.add_argument("--surfaces-only", action="store_true", help="only the reference-shaped drop-in surfaces (for profiling their kernels)")
     ap.add_argument("--shared-only", choices=["bf16", "fp8"], default=None,
                     help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
     ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
@@ -691,6 +692,10 @@ def main():
         t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
         print(json.dumps({"workload": f"configs[2] decode, M = {M}", "us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
                           "TBps": round(uniq * eb / t_m / 1e12, 3), "w2_bytes_per_expert": H * (I // 2) + H * (I // 32)}))
+        return
+    if args.surfaces_only:
+        print(json.dumps({"workload": "drop-in surfaces: configs[1] fp4_gemm_tc / fp4_gemv_pairs, configs[3] GroupedPairs + grouped_fp4_gemm",
+                          **bench_surfaces(torch, dev, layers, min(K, 40), W)}))
         return
     if args.stack_only:
         t_s, b_s = bench_stack(torch, dev, layers, max(2, min(K, 10)), W)
