@@ -124,7 +124,10 @@ def test_fp4_gemv_pairs_and_gemm_tc_drop_in():
     close(got[2:6, 64:], ref2[2:6], "fp4_gemm_tc shard")
 
 
-def test_grouped_fp4_gemm_atomic_rows():
+@pytest.mark.parametrize("block_m", [16, 64])
+def test_grouped_fp4_gemm_atomic_rows(block_m):
+    """N = 64 (not a multiple of 256): the 16-pair grouped kernel, over block_m's own tables (block_m 64: built on
+    demand by a second dispatch over the same stable pair order), repeated output rows summed atomically."""
     from dsv41_amd import moe_kernels, quant
     E, N, K = 8, 64, 256
     w, s, _, _ = make_experts(E, K, N // 2, 13)
@@ -135,13 +138,13 @@ def test_grouped_fp4_gemm_atomic_rows():
     rin = torch.from_numpy(rng.integers(0, 5, P).astype(np.int32)).to(DEV)
     rout = torch.from_numpy(rng.integers(0, 3, P).astype(np.int32)).to(DEV)   # repeated rows: atomic sums
     wgt = torch.from_numpy(rng.random(P).astype(np.float32)).to(DEV)
-    pairs = moe_kernels.GroupedPairs(eid, rin, rout, wgt, 16, n_experts=E)
+    pairs = moe_kernels.GroupedPairs(eid, rin, rout, wgt, block_m, n_experts=E)
     out = moe_kernels.grouped_fp4_gemm(a, w, s, pairs, 3)
     ref = np.zeros((3, N), np.float64)
     ev = eid.cpu().numpy()
     for p in range(P):
         ref[rout[p].item()] += O.gemv_pairs(bf16_vals(a), w.cpu().numpy(), s.cpu().numpy(), [rin[p].item()], [ev[p]], [wgt[p].item()])[0]
-    close(out.cpu().numpy(), ref, "grouped_fp4_gemm atomic")
+    close(out.cpu().numpy(), ref, f"grouped_fp4_gemm atomic block_m={block_m}")
 
 
 def test_big_groups_on_the_128_pair_tile_kernel():
