@@ -57,17 +57,22 @@ def untile(w8: torch.Tensor) -> torch.Tensor:
     return w8.reshape(N // 16, K // 64, 4, 16, 16).permute(0, 3, 1, 2, 4).reshape(N, K).contiguous()
 
 
-BF16_COPY = os.environ.get("DSV41_W8_BF16_COPY", "1") == "1"  # keep a bf16 copy for steps with many rows (linear_w)
-BF16_ROWS = int(os.environ.get("DSV41_W8_BF16_ROWS", str(MAX_TC_ROWS + 1)))  # rows from which the bf16 copy is used
-BF16_RESERVE_GB = float(os.environ.get("DSV41_W8_BF16_RESERVE_GB", "4"))  # free memory to leave when keeping copies
+# Environment switches with the reference's names and defaults (w8.py:51-53). DSV41_W8_BF16_COPY: whether loaders call
+# keep_bf16(); DSV41_W8_BF16_ROWS: the row count at which linear_w / oproj_a switch from the FP8 launch to the library
+# GEMM on a kept copy (here one past the launch's row limit: the FP8 launch is faster up to it); DSV41_W8_BF16_RESERVE_GB:
+# device memory a loader leaves free when it keeps copies.
+BF16_COPY = os.environ.get("DSV41_W8_BF16_COPY", "1") == "1"
+BF16_ROWS = int(os.environ.get("DSV41_W8_BF16_ROWS", str(MAX_TC_ROWS + 1)))
+BF16_RESERVE_GB = float(os.environ.get("DSV41_W8_BF16_RESERVE_GB", "4"))
 
 
 class W8:
     __slots__ = ("w8", "s8", "shape", "device", "tiled", "bf16w")
 
     def __init__(self, w8: torch.Tensor, s8: torch.Tensor, permuted: bool = False, tiled: bool | None = None):
-        """w8: uint8 E4M3 bytes [N, K] (natural order unless permuted=True: then already in the stored order, and
-        tiled if tiled=True); s8: E8M0 [ceil(N/32), K/32]. Stored tiled when the shape allows (w8.py:57-76)."""
+        """w8: uint8 E4M3 bytes [N, K]; s8: E8M0 [ceil(N/32), K/32] (w8.py:57-76). Bytes given in natural order are
+        stored in the 1 KiB tile order when N % 16 == 0 and K % 64 == 0; permuted=True takes w8 as already stored,
+        tiled or not as `tiled` says."""
         assert w8.dtype == torch.uint8 and s8.dtype == torch.uint8 and w8.dim() == 2
         N, K = w8.shape
         if permuted:
@@ -92,7 +97,8 @@ class W8:
         return dequant_fp8_block(self.w8, self.s8, tiled=self.tiled)
 
     def keep_bf16(self) -> "W8":
-        """Materialize the bf16 copy (2x the bytes) for steps with more rows than the FP8 kernel takes (w8.py:84-89)."""
+        """Dequantise once and hold the bf16 result beside the FP8 bytes (three times the memory in all); linear_w
+        and oproj_a use it from BF16_ROWS rows on (w8.py:84-89)."""
         if self.bf16w is None:
             self.bf16w = self.bf16().contiguous()
         return self
@@ -103,13 +109,16 @@ class W8:
 
     @staticmethod
     def cat(ws: list) -> "W8":
-        """Concatenate along N (row counts multiples of 32, so scale blocks and 16-row tiles stay whole), w8.py:91-95."""
+        """One W8 whose rows are the given weights' rows in order (w8.py:91-95). Each part's row count must be a
+        multiple of 32: a 32 x 32 scale block, and so a 16-row tile, never straddles two parts."""
         assert all(w.shape[0] % 32 == 0 for w in ws) and len({w.tiled for w in ws}) == 1
         return W8(torch.cat([w.w8 for w in ws], dim=0), torch.cat([w.s8 for w in ws], dim=0), permuted=True, tiled=ws[0].tiled)
 
 
 def linear_w(x: torch.Tensor, w) -> torch.Tensor:
-    """F.linear for a bf16 tensor weight or a W8 weight (bf16 x, bf16 result), w8.py:102-113."""
+    """y = x . w^T with bf16 activations and a bf16 result, for w a plain bf16 tensor (library GEMM) or a W8
+    (w8.py:102-113): up to MAX_TC_ROWS rows the FP8 launch reads the E4M3 bytes directly, beyond that (or from
+    BF16_ROWS rows with a kept copy) the library GEMM runs on the dequantised weights."""
     if not isinstance(w, W8):
         return F.linear(x, w)
     lead = x.shape[:-1]
@@ -127,8 +136,9 @@ def linear_fp8(x: torch.Tensor, w) -> torch.Tensor:
 
 
 def oproj_a(o: torch.Tensor, wo_a, n_groups: int, rank: int) -> torch.Tensor:
-    """The block-diagonal o-projection (w8.py:116-124): o [b, s, g, d] x wo_a (rows g*rank..(g+1)*rank use only
-    group g) -> [b, s, g*rank]."""
+    """Grouped output projection (w8.py:116-124): o [b, s, g, d], wo_a [g * rank, d]; output columns
+    g' * rank .. (g' + 1) * rank - 1 are o[..., g', :] times rows g' * rank .. of wo_a, so the result is [b, s, g * rank]
+    (a block-diagonal weight applied without materialising its zero blocks)."""
     b, s, g, d = o.shape
     if isinstance(wo_a, W8) and b * s <= MAX_TC_ROWS and (wo_a.bf16w is None or b * s < BF16_ROWS):
         y = hipkern.fp8_gemm_tc(o.reshape(b * s * g, d).contiguous().to(torch.bfloat16), wo_a.w8, wo_a.s8, group_cols=rank,

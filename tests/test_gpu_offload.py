@@ -143,12 +143,12 @@ def test_hot_cache_swaps(layer_weights):
         hc.new_token()
         layer._decode_cpu(xq, eid, wt)
         hc.drain()
-    smap = layer.hot["slot"]
+    smap = layer.hot.resident()
     assert {8, 9, 10, 11} <= set(smap), f"slot map {smap}"
     ex = to_ex(*ws, True)
     for e, s in smap.items():
         for name in ("w13", "s13", "w2", "s2"):
-            assert torch.equal(getattr(layer.hot["ex"], name)[s], getattr(ex, name)[e]), f"slot {s} does not hold expert {e}"
+            assert torch.equal(getattr(layer.hot.ex, name)[s], getattr(ex, name)[e]), f"slot {s} does not hold expert {e}"
     assert hc.n_swaps >= 4 and hc.n_hits > 0
     print(hc.stats())
     w13, s13, w2, s2 = [w.cpu().numpy() for w in ws]
