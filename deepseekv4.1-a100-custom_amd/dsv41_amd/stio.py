@@ -14,7 +14,6 @@ import json
 import mmap
 import os
 import struct
-import warnings
 
 import numpy as np
 import torch
@@ -42,7 +41,9 @@ class _File:
             (n,) = struct.unpack("<Q", f.read(8))
             self.header = json.loads(f.read(n))
             self.base = 8 + n
-            self.map = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+            # copy-on-write: tensors handed out are views of the file's pages, and a caller that writes into one
+            # gets private pages (the file is never modified) instead of a fault on a read-only mapping
+            self.map = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_COPY)
         self.header.pop("__metadata__", None)
 
 
@@ -84,7 +85,9 @@ class Checkpoint:
 
     def get(self, name: str, device=None, rows: slice | None = None) -> torch.Tensor:
         """`name` as a CPU tensor viewing the mapped file (device None), or a copy on `device`. `rows` selects a range
-        of the leading dimension; only those bytes are mapped into the view."""
+        of the leading dimension; only those bytes are mapped into the view. The views of one Checkpoint share its
+        copy-on-write mapping: writing into one never changes the file, but later get()s of the same bytes from this
+        Checkpoint see the write (clone() for a tensor of its own)."""
         f = self._file(self.weight_map[name])
         m = f.header[name]
         tdtype, esize = DTYPES[m["dtype"]]
@@ -101,8 +104,6 @@ class Checkpoint:
         if end == begin:
             t = torch.empty(shape, dtype=tdtype)
         else:
-            with warnings.catch_warnings():   # the map is read-only: the view is never written
-                warnings.simplefilter("ignore", UserWarning)
-                t = torch.frombuffer(f.map, dtype=torch.uint8, count=end - begin, offset=f.base + begin)
+            t = torch.frombuffer(f.map, dtype=torch.uint8, count=end - begin, offset=f.base + begin)
             t = t.view(tdtype).view(shape)
         return t if device is None else t.to(device)

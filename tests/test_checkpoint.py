@@ -54,6 +54,20 @@ def test_reader_matches_safetensors_library_and_raw_bytes(tmp_path):
             raise
 
 
+def test_written_views_stay_private(tmp_path):
+    """A caller may write into a returned tensor: the pages become private to the process (copy-on-write), a new
+    Checkpoint of the same file reads the original bytes, and the file is unchanged."""
+    a32 = np.arange(24, dtype=np.float32).reshape(4, 6)
+    path = tmp_path / "model.safetensors"
+    write_file(str(path), {"a": ("F32", a32.shape, a32)})
+    ck = stio.Checkpoint(str(tmp_path))
+    t = ck.get("a")
+    t.mul_(2.0)
+    assert np.array_equal(t.numpy(), a32 * 2.0)
+    assert np.array_equal(stio.Checkpoint(str(tmp_path)).get("a").numpy(), a32)
+    assert a32.tobytes() in open(path, "rb").read()
+
+
 def test_sharded_checkpoint_and_expert_stacking(tmp_path):
     rng = np.random.default_rng(2)
     E, H, I = 3, 256, 128
