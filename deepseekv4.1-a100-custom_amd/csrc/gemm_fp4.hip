@@ -38,6 +38,10 @@ struct GroupedArgs {
     int shard_start, shard_n, zero_out, min_tok, max_tok, vec_store;
     int accum;                               // 0 store, 1 add (distinct rows), 2 atomic add (rows may repeat)
     int lds_rows;                            // B_LDS: activation rows staged per pass (<= 16)
+    // TERMS == 2: the second FP8 term of off-grid activations (dsv41_quant_fp8_split), same strides as xc / xs; its
+    // MFMAs run only when *lo_flag is non-zero
+    const uint8_t* xlc; const uint8_t* xls; const int* lo_flag;
+    const int* run_if;                       // optional: the launch does nothing when *run_if == 0
 };
 
 // LDS row stride for staged activation codes: +16 bytes so 16 rows fall in different banks
@@ -49,9 +53,13 @@ __device__ __forceinline__ int lds_stride(int K) { return K + 16; }
 // memory queue holds only weight tiles (PF in flight per wave); otherwise B is read from global memory
 // (L1/L2-resident) with non-divergent loads. Lanes whose column has no pair read row 0: their output
 // column is never stored.
-template <int TILED, int PF, int B_LDS, int NKC>
+// TERMS == 2 (with B_LDS): the lo term's rows are staged beside the hi rows and each weight tile takes a second MFMA
+// with them into the same accumulator, when lo_flag is set; otherwise the kernel runs exactly the one-term arithmetic.
+template <int TILED, int PF, int B_LDS, int NKC, int TERMS = 1>
 __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    static_assert(TERMS == 1 || B_LDS, "the second term is staged in LDS");
+    if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = blockIdx.x * 4 + wave;
     const int g = blockIdx.y;
@@ -82,6 +90,9 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
     const int LS = lds_stride(K);
     uint8_t* lds_s = smem + (size_t)a.lds_rows * LS;
+    // the lo term's staged rows and bytes start lo_off bytes further (16-byte aligned)
+    const int lo_off = (a.lds_rows * (LS + Ks) + 15) & ~15;
+    const bool two = TERMS == 2 && __builtin_amdgcn_readfirstlane(*a.lo_flag) != 0;
 
     const int PW = B_LDS ? a.lds_rows : 16;   // pairs per pass: never more rows than the LDS holds
     v4i A[PF];
@@ -115,9 +126,14 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
                 const v4i b0 = *(const v4i*)(xl);
                 const v4i b1 = *(const v4i*)(xl + 64);
                 const int sb = *xsl;
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
+                if (two) {
+                    const v4i l0 = *(const v4i*)(xl + lo_off);
+                    const v4i l1 = *(const v4i*)(xl + lo_off + 64);
+                    acc = mfma_fp4w_fp8x(widen(A[slot]), join(l0, l1), acc, SA[slot], (int)xsl[lo_off]);
+                }
                 xl += 128;
                 xsl += 4;
-                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
             } else {
                 acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
             }
@@ -139,6 +155,19 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
                     const int r = i / Ks, v = i - r * Ks;
                     const int t = a.pair_tok[base + r];
                     lds_s[r * Ks + v] = (t >= 0 && t < a.x_rows) ? a.xs[(long long)t * a.ldxs + v] : (uint8_t)127;
+                }
+                if (two) {
+                    for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
+                        const int r = i / vpr, v = i - r * vpr;
+                        const int t = a.pair_tok[base + r];
+                        *(v4i*)(smem + lo_off + r * LS + v * 16) =
+                            (t >= 0 && t < a.x_rows) ? *(const v4i*)(a.xlc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
+                    }
+                    for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
+                        const int r = i / Ks, v = i - r * Ks;
+                        const int t = a.pair_tok[base + r];
+                        lds_s[lo_off + r * Ks + v] = (t >= 0 && t < a.x_rows) ? a.xls[(long long)t * a.ldxs + v] : (uint8_t)127;
+                    }
                 }
             }
             __syncthreads();
@@ -907,15 +936,26 @@ __global__ void __launch_bounds__(256) down_reduce_kernel(const DownSumArgs a, c
 // ------------------------------------------------------------------------------------------ C ABI
 #define B_LDS_MAX_BYTES (48 * 1024)
 
-template <int TILED, int B_LDS>
+template <int TILED, int B_LDS, int TERMS = 1>
 static void launch_grouped(const GroupedArgs& a, int G, size_t lds, hipStream_t st) {
     dim3 grid((unsigned)((a.N / 16 + 3) / 4), (unsigned)G);
     constexpr int PF = B_LDS ? DSV41_PF_UP : 8;
-    fp4_grouped_kernel<TILED, PF, B_LDS, 0><<<grid, 256, lds, st>>>(a);
+    fp4_grouped_kernel<TILED, PF, B_LDS, 0, TERMS><<<grid, 256, lds, st>>>(a);
+}
+
+static void launch_grouped_any(const GroupedArgs& a, int G, bool use_lds, int terms, size_t lds, hipStream_t st, int tiled) {
+    if (terms == 2) {
+        if (tiled) launch_grouped<1, 1, 2>(a, G, lds, st); else launch_grouped<0, 1, 2>(a, G, lds, st);
+    } else if (tiled) {
+        if (use_lds) launch_grouped<1, 1>(a, G, lds, st); else launch_grouped<1, 0>(a, G, 0, st);
+    } else {
+        if (use_lds) launch_grouped<0, 1>(a, G, lds, st); else launch_grouped<0, 0>(a, G, 0, st);
+    }
 }
 
 extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
                                       int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                      const uint8_t* xlc, const uint8_t* xls, const int* lo_flag,
                                       const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
                                       float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
                                       int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream) {
@@ -923,21 +963,41 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || G < 0 || ldo < N || ldx < K || ldxs < K / 32 || max_tokens < 1) return DSV41_EINVAL;
     if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15) || x_rows < 0 || n_pairs < 0 || out_rows < 0 || shard_n < 0)
         return DSV41_EINVAL;
+    // the second term comes whole (codes, scales and its flag) or not at all
+    const int terms = xlc ? 2 : 1;
+    if ((xlc != nullptr) != (xls != nullptr) || (xlc != nullptr) != (lo_flag != nullptr) || (((uintptr_t)xlc) & 15)) return DSV41_EINVAL;
     // every expert W holds has N rows of K / 2 weight bytes and K / 32 scale bytes
     if (stride_we < (long long)N * (K / 2) || stride_se < (long long)N * (K / 32)) return DSV41_EINVAL;
     if (G == 0 || n_pairs == 0) return 0;
     GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, x_rows, grp_expert, grp_start, pair_tok, n_pairs, out, ldo, out_rows,
-                  out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0};
+                  out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0, xlc, xls, lo_flag, nullptr};
     a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
     const int rows = max_tokens < 16 ? max_tokens : 16;
-    const size_t lds = (size_t)rows * (K + 16) + (size_t)rows * (K / 32);
-    const bool use_lds = lds <= B_LDS_MAX_BYTES;
+    const size_t lds1 = (size_t)rows * (K + 16) + (size_t)rows * (K / 32);
+    const size_t lds2 = ((lds1 + 15) & ~(size_t)15) + lds1;
+    if (terms == 2 && lds2 <= B_LDS_MAX_BYTES) {
+        // both terms staged in LDS, one launch
+        a.lds_rows = rows;
+        launch_grouped_any(a, G, true, 2, lds2, st, tiled);
+        return (int)hipGetLastError();
+    }
+    const bool use_lds = lds1 <= B_LDS_MAX_BYTES;
     a.lds_rows = use_lds ? rows : 0;
-    if (tiled) {
-        if (use_lds) launch_grouped<1, 1>(a, G, lds, st); else launch_grouped<1, 0>(a, G, 0, st);
-    } else {
-        if (use_lds) launch_grouped<0, 1>(a, G, lds, st); else launch_grouped<0, 0>(a, G, 0, st);
+    a.xlc = a.xls = nullptr;
+    a.lo_flag = nullptr;
+    launch_grouped_any(a, G, use_lds, 1, use_lds ? lds1 : 0, st, tiled);
+    if (terms == 2) {
+        // the activation rows do not fit LDS twice: the lo term as a second pass that adds into the same outputs, which
+        // does nothing when no lo code is non-zero
+        GroupedArgs b = a;
+        b.xc = xlc;
+        b.xs = xls;
+        b.run_if = lo_flag;
+        b.accum = accum == 2 ? 2 : 1;
+        b.zero_out = 0;
+        b.vec_store = 0;
+        launch_grouped_any(b, G, use_lds, 1, use_lds ? lds1 : 0, st, tiled);
     }
     return (int)hipGetLastError();
 }

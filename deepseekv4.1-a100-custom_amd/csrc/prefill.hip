@@ -9,6 +9,8 @@
 //          turns the tile into h = fq8(bf16(w * silu(min(g, L)) * clamp(u, +-L))) for 128 columns (four FP8
 //          groups) of every pair (fused.py:284-306) -- gate/up never reach HBM;
 //   MODE 1 (w2):  rows = 256 consecutive output rows; the epilogue stores fp32 y2[pair][row].
+//   MODE 2:       MODE 1 adding into y2 instead of storing, for the second FP8 term of off-grid activations
+//          (dsv41_quant_fp8_split); the launch returns at once when that term is all zero (*run_if == 0).
 // The weight operand is the raw E2M1 nibbles + E8M0 bytes as stored; the activation operand the E4M3 codes of the
 // group's tokens, gathered by token id.
 // Workgroup order is XCD-aware: the hardware hands workgroup i to XCD i % 8. XCD x takes the groups g = x, x + 8,
@@ -39,6 +41,7 @@ struct PrefillArgs {
     int g_pad;                                // G rounded up to a multiple of 8 (XCD remap)
     int n_pairs;                              // group ranges are clamped to [0, n_pairs)
     int cbw, n_it;                            // column blocks per workgroup, workgroups per group (ceil(n_cb / cbw))
+    const int* run_if;                        // MODE 2: the launch does nothing when *run_if == 0
 };
 
 // ------------------------------------------------------------------------------------------ direct-to-LDS variant
@@ -300,7 +303,11 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
                     // rows block_of(slot_of[j], cb) * 16 + 4 kb .. = cb * 256 + 64 cg + 16 j + 4 kb ..
                     float* o = a.y + (long long)(p0 + pr) * a.ldy + cb * 256 + 64 * cg + 4 * kb;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) *(gmem_v4f*)(o + 16 * j) = acc[j][u];
+                    for (int j = 0; j < 4; ++j) {
+                        gmem_v4f* q = (gmem_v4f*)(o + 16 * j);
+                        if (MODE == 2) *q = *q + acc[j][u];   // the lo term's pass adds to the hi term's rows
+                        else *q = acc[j][u];
+                    }
                 }
             }
         }
@@ -450,6 +457,7 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
 
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
+    if (MODE == 2 && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     prefill_item128<MODE, TILED>(a, (int)blockIdx.x);
 }
 
@@ -684,7 +692,11 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
                 if (tb_on[u] && pr < m) {
                     float* o = a.y + (long long)(p0 + pr) * a.ldy + cb * 256 + 64 * cg + 4 * kb;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) *(gmem_v4f*)(o + 16 * j) = acc[j][u];
+                    for (int j = 0; j < 4; ++j) {
+                        gmem_v4f* q = (gmem_v4f*)(o + 16 * j);
+                        if (MODE == 2) *q = *q + acc[j][u];   // the lo term's pass adds to the hi term's rows
+                        else *q = acc[j][u];
+                    }
                 }
             }
         }
@@ -790,6 +802,7 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
 // The prefill path's launch: each item takes the 256-pair tile when its group holds more than 128 pairs.
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_mixed_kernel(const PrefillArgs a) {
+    if (MODE == 2 && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     const int L = (int)blockIdx.x;
     const int jx = L >> 3, g = (jx / a.n_it) * 8 + (L & 7);
     if (g >= a.G) return;
@@ -816,10 +829,12 @@ static int launch_prefill(PrefillArgs& a, int mode, int tiled, bool mixed, hipSt
     } while (0)
     if (mixed) {
         if (mode == 0) { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 0, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 0, 0); }
-        else { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 0); }
+        else if (mode == 1) { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 1, 0); }
+        else { if (tiled) PV_LAUNCH(prefill_gemm_mixed_kernel, 2, 1); else PV_LAUNCH(prefill_gemm_mixed_kernel, 2, 0); }
     } else {
         if (mode == 0) { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 0, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 0, 0); }
-        else { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 1, 0); }
+        else if (mode == 1) { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 1, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 1, 0); }
+        else { if (tiled) PV_LAUNCH(prefill_gemm_lds_kernel, 2, 1); else PV_LAUNCH(prefill_gemm_lds_kernel, 2, 0); }
     }
 #undef PV_LAUNCH
     return (int)hipGetLastError();
@@ -860,11 +875,29 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
     return launch_prefill(a, 1, tiled, true, (hipStream_t)stream);
 }
 
-extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const int* row_of_pair,
+// The second FP8 term of off-grid activations (xlc / xls / lo_flag of dsv41_quant_fp8_split, all or none): checked like
+// the first, then run as a MODE 2 pass over the same groups that adds into the rows the first pass wrote.
+static bool lo_term_bad(const uint8_t* xc, const uint8_t* xlc, const uint8_t* xls, const int* lo_flag) {
+    return (xlc != nullptr) != (xls != nullptr) || (xlc != nullptr) != (lo_flag != nullptr) || (((uintptr_t)xlc) & 15) ||
+           (((uintptr_t)xls) & 3) || (xlc && xlc == xc);
+}
+
+static int lo_pass(const PrefillArgs& a, const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, int tiled, bool mixed, hipStream_t st) {
+    if (!xlc) return 0;
+    PrefillArgs b = a;
+    b.xc = xlc;
+    b.xs = xls;
+    b.run_if = lo_flag;
+    return launch_prefill(b, 2, tiled, mixed, st);
+}
+
+extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                           const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, const int* row_of_pair,
                                            const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled, int E, int N,
                                            int K, const int* grp_expert, const int* grp_start, int G, int n_pairs, float* y, long long ldy,
                                            void* stream) {
     if (!xc || !xs || !W || !S || !grp_expert || !grp_start || !y || n_pairs < 0) return DSV41_EINVAL;
+    if (lo_term_bad(xc, xlc, xls, lo_flag)) return DSV41_EINVAL;
     if (!row_of_pair && n_pairs > x_rows) return DSV41_EINVAL;   // without a table, pair p reads input row p
     if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || N <= 0 || (N & 255) || K < 128 * PG_PF || (K & 127) || G < 0 || ldx < K || (ldx & 15) || (((uintptr_t)xc) & 15) ||
@@ -876,7 +909,8 @@ extern "C" int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, con
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W, stride_we, S, stride_se, N, K, E,
                   grp_expert, grp_start, G, row_of_pair, nullptr, 0.f, nullptr, 0, nullptr, 0, y, ldy, N / 256, 0, n_pairs};
-    return launch_prefill(a, 1, tiled, false, (hipStream_t)stream);
+    const int rc = launch_prefill(a, 1, tiled, false, (hipStream_t)stream);
+    return rc ? rc : lo_pass(a, xlc, xls, lo_flag, tiled, false, (hipStream_t)stream);
 }
 
 // out[row_out[p]] (+)= fl(wt[p] * y2[p]) for the pairs of every group g with an expert in [0, E) (its first P2_T pairs,
@@ -935,6 +969,7 @@ __global__ void __launch_bounds__(256) scatter_rows_kernel(const float* __restri
 // fl(wt[p] * y2[p]) in a second launch (an epilogue of that form inside the tile kernel's k-loop made its compiled loop
 // twice as slow).
 extern "C" int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                              const uint8_t* xlc, const uint8_t* xls, const int* lo_flag,
                                               const int* row_of_pair, const uint8_t* W, long long stride_we, const uint8_t* S,
                                               long long stride_se, int tiled, int E, int N, int K, const int* grp_expert, const int* grp_start,
                                               int G, int n_pairs, const int* row_out, const float* wt, const int* distinct, int accum,
@@ -942,6 +977,7 @@ extern "C" int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, 
     if (!xc || !xs || !W || !S || !grp_expert || !grp_start || !row_out || !wt || !out || !y2 || n_pairs < 0 || out_rows < 0 || accum < 0 ||
         accum > 1)
         return DSV41_EINVAL;
+    if (lo_term_bad(xc, xlc, xls, lo_flag)) return DSV41_EINVAL;
     if (!row_of_pair && n_pairs > x_rows) return DSV41_EINVAL;   // without a table, pair p reads input row p
     if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || N <= 0 || (N & 255) || K < 128 * PG_PF || (K & 127) || G < 0 || G > 0xFFFF || ldx < K || (ldx & 15) || (((uintptr_t)xc) & 15) ||
@@ -955,7 +991,8 @@ extern "C" int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, 
     hipStream_t st = (hipStream_t)stream;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W, stride_we, S, stride_se, N, K, E,
                   grp_expert, grp_start, G, row_of_pair, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy2, N / 256, 0, n_pairs};
-    const int rc = launch_prefill(a, 1, tiled, true, st);
+    int rc = launch_prefill(a, 1, tiled, true, st);
+    if (rc == 0) rc = lo_pass(a, xlc, xls, lo_flag, tiled, true, st);
     if (rc != 0) return rc;
     const dim3 grid((unsigned)((N + 1023) / 1024), (unsigned)G, P2_T / SCAT_ROWS);
     scatter_rows_kernel<<<grid, 256, 0, st>>>(y2, ldy2, grp_expert, grp_start, E, n_pairs, row_out, wt, distinct, accum, out, ldo, out_rows, N);

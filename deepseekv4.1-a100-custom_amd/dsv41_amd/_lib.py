@@ -28,7 +28,8 @@ SIGNATURES = {
     "dsv41_dequant_fp4": [P, P, LL, I, I, P, P],
     "dsv41_quant_fp8": [P, I, LL, I, LL, I, P, P, P, P],
     "dsv41_swiglu_quant": [P, I, LL, P, I, I, F, P, P, P, I, P],
-    "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
+    "dsv41_quant_fp8_split": [P, LL, I, LL, I, P, P, P, P, P, P],
+    "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
     "dsv41_moe_decode_up": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P,
                             P, LL, I, P, LL, P, LL, P],
     "dsv41_moe_decode_up_pairs": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P,
@@ -38,9 +39,9 @@ SIGNATURES = {
     "dsv41_moe_down_sum_split": [P, LL, P, LL, I, I, I, P, LL, P, LL, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, P, P, P, LL, P],
     "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],
     "dsv41_prefill_down": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, LL, P],
-    "dsv41_fp4_grouped_gemm_t128": [P, LL, P, LL, I, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, LL, P],
+    "dsv41_fp4_grouped_gemm_t128": [P, LL, P, LL, I, P, P, P, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, LL, P],
     "dsv41_rows_distinct": [P, I, P, I, P, P],
-    "dsv41_fp4_grouped_gemm_scatter": [P, LL, P, LL, I, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, P, P, I, P, LL, I, P, LL, P],
+    "dsv41_fp4_grouped_gemm_scatter": [P, LL, P, LL, I, P, P, P, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, P, P, I, P, LL, I, P, LL, P],
     "dsv41_combine_pairs": [P, LL, P, I, I, I, P, LL, P, LL, P, LL, P],
     "dsv41_dense_gemv_bf16": [P, LL, I, I, I, P, LL, I, P, LL, P, LL, P],
     "dsv41_residual_rmsnorm_quant": [P, LL, P, LL, P, F, I, I, P, LL, P, LL, P],

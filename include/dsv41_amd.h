@@ -32,6 +32,17 @@ int dsv41_dequant_fp4(const uint8_t* w, const uint8_t* s, long long rows, int K,
 int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, long long ldx, int permuted,
                     uint8_t* codes, uint8_t* scales, void* fq, void* stream);
 
+/* bf16 activations as two FP8 terms, so the FP4 GEMMs below honour the reference's bf16-operand contract (fp4_gemv.cu,
+ * fp4_tcw.cu and moe_kernels.py:154-200 multiply bf16 x by bf16-decoded weights; cukern.py:60-77, 238-276 and
+ * moe_kernels.py:127-151 accept any bf16 x): x = hi + lo per 32-group, hi = the codes and scales dsv41_quant_fp8 gives
+ * (bit-identical), lo = the residual x - hi rounded to E4M3 with an E8M0 scale of its own. hi + lo == x for every
+ * element whose residual is in the lo term's normal range; otherwise |x - hi - lo| < 2^-21 of the group's amax.
+ * x: bf16 [rows][ldx] (ldx % 8 == 0, 16-byte aligned), 8-k permuted when permuted = 1 (codes in natural order).
+ * Outputs: hc / lc [rows][K], hs / ls [rows][K/32], lo_flag (device int) cleared, then set to 1 when any lo code is
+ * non-zero (FP8-grid x leaves it 0). No counterpart in the reference, which has no FP8 activation operand. */
+int dsv41_quant_fp8_split(const uint16_t* x, long long rows, int K, long long ldx, int permuted, uint8_t* hc, uint8_t* hs,
+                          uint8_t* lc, uint8_t* ls, int* lo_flag, void* stream);
+
 /* h = fq8(bf16(wt * silu(min(g, L)) * clamp(u, +-L))) per 32 (fused.swiglu_quant, fused.py:283-345).
  * gu: fp32 [rows][ld_gu] (gu_bf16 = 0) or bf16 (gu_bf16 = 1, as fused.py:294 accepts), gate columns [0, inter), up
  * [inter, 2 inter); ld_gu in elements. wt: fp32 [rows] or NULL. Outputs (any
@@ -51,10 +62,12 @@ int dsv41_swiglu_quant(const void* gu, int gu_bf16, long long ld_gu, const float
  * zero_out, their rows zeroed (cukern.py:244-246); padding groups (expert < 0) and groups with fewer than min_tok
  * or more than max_tok pairs are skipped. Bounds: group ranges are clamped to [0, n_pairs); pairs whose token is
  * outside [0, x_rows) contribute zeros; output rows outside [0, out_rows) are not written. N % 16 == 0,
- * K % 128 == 0. */
+ * K % 128 == 0. xlc / xls / lo_flag (all three or none): the lo term of dsv41_quant_fp8_split, with xc / xs its hi
+ * term; x is then hi + lo, and the lo term's products are added only when *lo_flag is non-zero (FP8-grid input runs
+ * the one-term arithmetic bit for bit). */
 int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
                            int N, int K, const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
-                           const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
+                           const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
                            float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
                            int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
 
@@ -162,8 +175,11 @@ int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, lon
  * row = row_of_pair ? row_of_pair[p] : p (rows outside [0, x_rows) read zeros). x: E4M3 codes [x_rows][ldx] + E8M0
  * [x_rows][ldxs]. Rows of y for pairs outside every computed group are not written. N % 256 == 0, K % 128 == 0,
  * K >= 384. Serves moe_kernels.grouped_fp4_gemm (moe_kernels.py:127-200) and cukern.fp4_gemm_tc (cukern.py:238-276)
- * when their groups exceed 16 pairs: the weights of a group are read once for up to 128 pairs. */
-int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const int* row_of_pair,
+ * when their groups exceed 16 pairs: the weights of a group are read once for up to 128 pairs. xlc / xls / lo_flag
+ * (all or none): the lo term of dsv41_quant_fp8_split, added by a second pass over the groups that does nothing when
+ * *lo_flag is 0. */
+int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
+                                const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, const int* row_of_pair,
                                 const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled, int E, int N,
                                 int K, const int* grp_expert, const int* grp_start, int G, int n_pairs, float* y, long long ldy,
                                 void* stream);
@@ -176,9 +192,10 @@ int dsv41_fp4_grouped_gemm_t128(const uint8_t* xc, long long ldx, const uint8_t*
  * device int (or NULL) that is non-zero when no two pairs share an output row; then accum == 0 stores (out must hold
  * zeros beforehand) and accum == 1 reads, adds and writes, deterministically; otherwise fp32 atomic adds (any order,
  * as the reference's). y2: workspace fp32 [n_pairs][ldy2] (the unweighted pair rows, sorted order). G <= 65535.
- * N % 256 == 0, K % 128 == 0, K >= 384, ldo % 4 == 0 and ldy2 % 4 == 0, out and y2 16-byte aligned. */
+ * N % 256 == 0, K % 128 == 0, K >= 384, ldo % 4 == 0 and ldy2 % 4 == 0, out and y2 16-byte aligned. xlc / xls /
+ * lo_flag: the lo term, as for dsv41_fp4_grouped_gemm_t128 (its pass adds into y2 before the scatter). */
 int dsv41_fp4_grouped_gemm_scatter(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows,
-                                   const int* row_of_pair, const uint8_t* W, long long stride_we, const uint8_t* S,
+                                   const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, const int* row_of_pair, const uint8_t* W, long long stride_we, const uint8_t* S,
                                    long long stride_se, int tiled, int E, int N, int K, const int* grp_expert, const int* grp_start,
                                    int G, int n_pairs, const int* row_out, const float* wt, const int* distinct, int accum,
                                    float* out, long long ldo, int out_rows, float* y2, long long ldy2, void* stream);

@@ -29,6 +29,11 @@ PINS = {
     "round_e4m3": "torch float8_e4m3fn cast on 2^20 samples (test_fused.py:17 twin) + exhaustive code grid",
     "fake_quant_fp8": "golden fq8 (bf16 and fp32 inputs, edge groups)",
     "quant_fp8": "golden qfp8 codes and scales",
+    "lo_exponent": "brute force: the smallest e >= -126 with a <= 448 2^e by scanning e, on random, power-of-two and "
+                   "448 2^k boundary amax values",
+    "fp8_split": "hi = the golden-pinned quant_fp8 codes/scales; hi + lo reconstructs bf16 x exactly wherever the residual "
+                 "is in lo's normal range and within 2^-21 of the block amax elsewhere (closed form); lo codes = torch "
+                 "float8_e4m3fn cast of residual / 2^e2; FP8-grid x gives lo = 0",
     "permute_x": "closed form: inverse permutation round trip",
     "swiglu_quant": "compiled reference CPU library (oracle/_ref) layer output + closed form",
     "gate_topk": "brute force (sort) on random and tied inputs",
@@ -220,6 +225,46 @@ def quant_fp8_e8m0(x, block: int = 32):
     codes = e4m3_encode(q).reshape(shape)
     scales = (e + 127).astype(np.uint8).reshape(*shape[:-1], shape[-1] // block)
     return codes, scales
+
+
+def lo_exponent(amax) -> np.ndarray:
+    """Smallest integer e >= -126 with amax / 2^e <= 448 (no 1e-4 floor): the scale exponent of the split's second
+    term. This build's own rule (the reference has no FP8 activation operand); brute-force pinned."""
+    a = np.asarray(amax, dtype=np.float64)
+    e = np.full(a.shape, -126, dtype=np.int32)
+    pos = a > 0
+    m, ex = np.frexp(a[pos])                      # a = m 2^ex, m in [0.5, 1)
+    need = np.ceil(np.log2(a[pos] / 448.0)).astype(np.int32)
+    # log2 can be off by an ulp at exact powers of two: settle the integer with the exact comparison a <= 448 2^e
+    need = np.where(np.ldexp(448.0, need - 1) >= a[pos], need - 1, need)
+    need = np.where(np.ldexp(448.0, need) < a[pos], need + 1, need)
+    e[pos] = np.maximum(need, -126)
+    return e
+
+
+def fp8_split(x, block: int = 32):
+    """bf16-valued x [..., K] as two FP8 operand terms (dsv41_quant_fp8_split): (hi codes, hi scales, lo codes, lo
+    scales). hi = quant_fp8_e8m0(x) (quant.py:57-64); lo = the residual x - hi (exact in fp32), quantised per block
+    with 2^lo_exponent(amax of the residual) and E4M3 round-to-nearest-even. The reference multiplies bf16 x directly
+    (fp4_gemv.cu:15-66, moe_kernels.py:154-200); hi + lo is that x to within 2^-21 of the block's amax."""
+    shape = np.shape(x)
+    xg = _groups(x, block)
+    hc, hs = quant_fp8_e8m0(xg, block)
+    hv = e4m3_decode(hc).astype(np.float64) * np.ldexp(1.0, hs.astype(np.int32) - 127)
+    r = (xg.astype(np.float64) - hv).astype(F32)            # exact: both are short fp32 values within 24 bits
+    e2 = lo_exponent(np.abs(r).max(axis=-1, keepdims=True))
+    q2 = round_e4m3(np.clip(r / np.ldexp(F32(1.0), e2).astype(F32), -FP8_MAX, FP8_MAX))
+    lc = e4m3_encode(q2)
+    ls = (e2 + 127).astype(np.uint8)
+    return hc.reshape(shape), hs.reshape(*shape[:-1], shape[-1] // block), lc.reshape(shape), ls.reshape(*shape[:-1], shape[-1] // block)
+
+
+def fp8_split_values(hc, hs, lc, ls, block: int = 32) -> np.ndarray:
+    """float64 value of hi + lo, per element."""
+    shape = np.shape(hc)
+    v = lambda c, s: e4m3_decode(np.asarray(c).reshape(-1, block)).astype(np.float64) * \
+        np.ldexp(1.0, np.asarray(s).reshape(-1, 1).astype(np.int32) - 127)
+    return (v(hc, hs) + v(lc, ls)).reshape(shape)
 
 
 def quant_fp8(x, block: int = 32):

@@ -73,9 +73,9 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     N, K = 3328, 7168
     we, se = N * K // 2, N * K // 32
 
-    def grouped(n, k, stride_we, stride_se, x_rows=1, n_pairs=8, out_rows=8, shard_n=384):
-        return L.dsv41_fp4_grouped_gemm(p, stride_we, p, stride_se, 1, n, k, p, k, p, k // 32, x_rows, p, p, 8, p, n_pairs, p, n, out_rows,
-                                        None, None, 0, 1, 0, shard_n, 0, 0, 1 << 30, None)
+    def grouped(n, k, stride_we, stride_se, x_rows=1, n_pairs=8, out_rows=8, shard_n=384, lo=(None, None, None)):
+        return L.dsv41_fp4_grouped_gemm(p, stride_we, p, stride_se, 1, n, k, p, k, p, k // 32, x_rows, *lo, p, p, 8, p, n_pairs, p, n,
+                                        out_rows, None, None, 0, 1, 0, shard_n, 0, 0, 1 << 30, None)
     assert grouped(2 * N, K, we, se) == -1           # N rows past one expert's weight bytes
     assert grouped(N, 2 * K, we, 2 * se) == -1       # K past the weight bytes
     assert grouped(N, K, we, se - 1) == -1           # scales shorter than N K / 32
@@ -84,6 +84,19 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert grouped(N, K, we, se, out_rows=-1) == -1
     assert grouped(N, K, we, se, shard_n=-1) == -1
     assert grouped(N, K, we, se, n_pairs=0) == 0     # nothing to do: returns before any launch
+    # the second FP8 term comes whole (codes, scales, flag) and 16-byte aligned, or not at all
+    assert grouped(N, K, we, se, lo=(p, None, p)) == -1
+    assert grouped(N, K, we, se, lo=(p, p, None)) == -1
+    assert grouped(N, K, we, se, lo=(None, p, p)) == -1
+    assert grouped(N, K, we, se, lo=(ctypes.c_void_p(24), p, p)) == -1
+    assert grouped(N, K, we, se, lo=(p, p, p), n_pairs=0) == 0
+    # the split quantiser: K % 32, row stride % 8, alignment of x and of the code outputs, every output given
+    q = ctypes.c_void_p(32)
+    assert L.dsv41_quant_fp8_split(q, 4, 48, 48, 0, q, q, q, q, q, None) == -1
+    assert L.dsv41_quant_fp8_split(q, 4, 64, 68, 0, q, q, q, q, q, None) == -1
+    assert L.dsv41_quant_fp8_split(ctypes.c_void_p(40), 4, 64, 64, 0, q, q, q, q, q, None) == -1
+    assert L.dsv41_quant_fp8_split(q, 4, 64, 64, 0, q, q, ctypes.c_void_p(40), q, q, None) == -1
+    assert L.dsv41_quant_fp8_split(q, 4, 64, 64, 0, q, q, q, q, None, None) == -1
 
     H, I = 7168, 1664
 
@@ -150,9 +163,9 @@ def test_grouped_scatter_rejects_invalid_calls_without_launch():
     p = ctypes.c_void_p(16)
     N, K = 512, 768
 
-    def call(n=N, k=K, row_out=p, accum=0, out=p, ldo=N, n_pairs=8, out_rows=8, y2=p, G=4):
-        return L.dsv41_fp4_grouped_gemm_scatter(p, k, p, k // 32, 8, p, p, n * (k // 2), p, n * (k // 32), 1, 4, n, k, p, p, G, n_pairs,
-                                                row_out, p, None, accum, out, ldo, out_rows, y2, n, None)
+    def call(n=N, k=K, row_out=p, accum=0, out=p, ldo=N, n_pairs=8, out_rows=8, y2=p, G=4, lo=(None, None, None)):
+        return L.dsv41_fp4_grouped_gemm_scatter(p, k, p, k // 32, 8, *lo, p, p, n * (k // 2), p, n * (k // 32), 1, 4, n, k, p, p, G,
+                                                n_pairs, row_out, p, None, accum, out, ldo, out_rows, y2, n, None)
     assert call(row_out=None) == -1
     assert call(accum=2) == -1
     assert call(n=N + 128) == -1
@@ -162,6 +175,12 @@ def test_grouped_scatter_rejects_invalid_calls_without_launch():
     assert call(y2=None) == -1
     assert call(y2=ctypes.c_void_p(20)) == -1
     assert call(G=65536) == -1
+    assert call(lo=(p, p, None)) == -1
+    assert call(lo=(p, None, p)) == -1
+    assert call(lo=(ctypes.c_void_p(24), p, p)) == -1
+    assert call(lo=(ctypes.c_void_p(48), ctypes.c_void_p(50), p)) == -1   # lo scales not 4-byte aligned
+    assert L.dsv41_fp4_grouped_gemm_t128(p, K, p, K // 32, 8, p, None, p, p, p, N * (K // 2), p, N * (K // 32), 1, 4, N, K, p, p, 4, 8,
+                                         p, N, None) == -1
     assert L.dsv41_rows_distinct(None, 4, None, 4, p, None) == -1
     assert L.dsv41_rows_distinct(p, -1, None, 4, p, None) == -1
     assert call(n_pairs=0) == 0

@@ -1,0 +1,318 @@
+"""The drop-in FP4 GEMM surfaces on bf16 activations that are not on the FP8 grid, as the reference's kernels take them
+(fp4_gemv.cu:15-66, fp4_tcw.cu, moe_kernels.py:154-200 multiply bf16 x by bf16-decoded weights), at the reference's own
+test cases:
+  * test_moe.py:14-29 -- GroupedPairs + grouped_fp4_gemm, E 32, N 2304, K 5120, M 1 / 5 / 64 / 512 tokens x top-6, raw
+    randn activations, scale bytes 110..134, block_m 16 / 64, row-major weights;
+  * test_fp4_tcw.py:10-45 -- fp4_gemm_tc, E 48, N 4608, K 5120, tiled weights, scale bytes 112..127, its seven group
+    mixes (groups split at 64 pairs), FP8-grid activations as that test uses, and raw ones;
+  * test_fp4_tc.py:34-46 -- fp4_gemm_tc and fp4_gemv_pairs, E 8, N 4608, K 5120, G experts x M tokens.
+The reference value is the textbook sum in float64 over the dequantised weights (dsv41_dequant_fp4, bit-exact with the
+reference's quant.dequant_fp4 over every code and scale byte, tests/test_gpu_formats.py; checked against the numpy
+oracle's dense_weights here too), the same computation the reference's tests make. Tolerances: the reference tests'
+own metric max|y - ref| / max|ref| < 2e-3, and BASELINE's rel L2 <= 2e-3, max-abs <= 1e-2 x RMS.
+Also: the split quantiser equals the oracle's fp8_split bit for bit, and FP8-grid input runs the one-term arithmetic
+bit for bit (its lo flag stays 0)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as O
+from test_gpu_moe import DEV, bf16_vals, close
+
+pytestmark = pytest.mark.gpu
+
+
+def ref_max_rel(got: torch.Tensor, ref: torch.Tensor) -> float:
+    """The reference tests' metric (test_moe.py:28, test_fp4_tcw.py:67)."""
+    return float((got.double() - ref).abs().max() / ref.abs().max())
+
+
+def check(got: torch.Tensor, ref: torch.Tensor, what: str):
+    e = ref_max_rel(got, ref)
+    print(f"{what}: max|err| / max|ref| {e:.2e}")
+    assert e < 2e-3, f"{what}: {e:.3e}"
+    close(got.float().cpu().numpy(), ref.float().cpu().numpy(), what)
+
+
+class Dense:
+    """Per-expert float64 weights, dequantised on the GPU once per expert and kept as bf16 (the dequant is exact in bf16)."""
+
+    def __init__(self, w, s, tiled):
+        from dsv41_amd import quant
+        self.w, self.s, self.tiled = w, s, tiled
+        self.cache = {}
+        self.quant = quant
+
+    def __getitem__(self, e):
+        e = int(e)
+        if e not in self.cache:
+            self.cache[e] = self.quant.dequant_fp4(self.w[e], self.s[e], tiled=self.tiled)
+        return self.cache[e].double()
+
+
+def pairs_ref(a, dense, eid, row_in, row_out, wt, n_out, N):
+    """out[row_out[p]] += wt[p] * a[row_in[p]] . W[eid[p]]^T in float64 (test_moe.py:15-19)."""
+    out = torch.zeros(n_out, N, dtype=torch.float64, device=DEV)
+    for e in torch.unique(eid).tolist():
+        sel = torch.nonzero(eid == e).flatten()
+        contrib = wt[sel].double()[:, None] * (a[row_in[sel].long()].double() @ dense[e].T)
+        out.index_add_(0, row_out[sel].long(), contrib)
+    return out
+
+
+def test_split_quantiser_equals_oracle():
+    """dsv41_quant_fp8_split against the oracle's fp8_split, bit for bit, on raw bf16 rows of several magnitudes (zero
+    and sub-1e-4 groups included), in natural and 8-k permuted input order; the lo flag is set. On FP8-grid rows the hi
+    term equals quant_fp8_e8m0, the lo codes are all zero and the flag is 0."""
+    from dsv41_amd import hipkern, quant
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(40, 1024, generator=g)
+    x[:10] *= 1e-3
+    x[10:20] *= 300.0
+    x[20, :64] = 0.0
+    x[21, :32] = 3e-6
+    x = x.to(torch.bfloat16)
+    want = O.fp8_split(bf16_vals(x))
+    got = quant.quant_fp8_split(x.to(DEV))
+    for w_, g_, name in zip(want, got[:4], ("hi codes", "hi scales", "lo codes", "lo scales")):
+        assert np.array_equal(w_, g_.cpu().numpy()), name
+    assert int(got[4]) == 1
+    gp = quant.quant_fp8_split(hipkern.permute_x(x.to(DEV)), permuted=True)
+    for w_, g_, name in zip(want, gp[:4], ("hi codes", "hi scales", "lo codes", "lo scales")):
+        assert np.array_equal(w_, g_.cpu().numpy()), f"permuted input: {name}"
+    fq = quant.fake_quant_fp8(x.to(DEV))
+    hc, hs, lc, ls, flag = quant.quant_fp8_split(fq)
+    qc, qs = quant.quant_fp8_e8m0(fq)
+    assert torch.equal(hc, qc) and torch.equal(hs, qs)
+    assert int((lc & 0x7F).max()) == 0 and int(flag) == 0
+
+
+MECHANISMS = {"two-term LDS kernel": [4, 2, 3], "rows from global memory + lo pass": [16, 3, 9], "128-pair tile + MODE 2 pass": [64, 40, 17]}
+
+
+def _mechanism_setup(seed):
+    from dsv41_amd import quant
+    from test_gpu_moe import make_experts
+    E, N, K = 6, 512, 3072      # K = 3072: 16 staged rows (50 KB) exceed the LDS budget, 4 rows twice (25 KB) do not
+    w, s, _, _ = make_experts(E, K, N // 2, seed)
+    return w, s, quant.tile_fp4(w), quant.tile_fp4_scales(s), E, N, K
+
+
+def _groups(rng, sizes, E, X):
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)
+    ge = t(rng.choice(E, len(sizes), replace=False))
+    gs = t(np.concatenate([[0], np.cumsum(sizes)]))
+    P = int(sum(sizes))
+    return ge, gs, t(rng.integers(0, X, P)), P
+
+
+def test_fp8_grid_input_is_bit_identical_to_one_term():
+    """FP8-grid x through the bf16-capable surfaces equals the one-term launches bit for bit, on each way the lo term
+    runs: fp4_gemv_pairs and 4-pair groups (both terms staged in LDS, one launch), 16-pair groups at K = 3072 (rows
+    from global memory; the lo pass launches and returns at once) and 64-pair groups (the 128-pair tile kernel and its
+    MODE 2 pass)."""
+    from dsv41_amd import hipkern, quant
+    from test_gpu_moe import rand_x
+    w, s, wt_, st_, E, N, K = _mechanism_setup(81)
+    X = 96
+    x = quant.fake_quant_fp8(rand_x(X, K, 82, 2.0).to(DEV))
+    xc, xs = quant.quant_fp8_e8m0(x)
+    rng = np.random.default_rng(83)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)
+    P = 7
+    row_in, expert = t(rng.integers(0, X, P)), t(rng.integers(0, E, P))
+    wt = torch.from_numpy(rng.random(P).astype(np.float32)).to(DEV)
+    got = hipkern.fp4_gemv_pairs(x, w, s, row_in, expert, wt, P)
+    one = torch.empty(P, N, device=DEV)
+    hipkern.grouped_gemm_codes(xc, xs, w, s, expert, torch.arange(P + 1, dtype=torch.int32, device=DEV), row_in, one, 1, False, pair_wt=wt)
+    assert torch.equal(got, one), "fp4_gemv_pairs"
+    for name, sizes in MECHANISMS.items():
+        ge, gs, tok, P = _groups(rng, sizes, E, X)
+        got = hipkern.fp4_gemm_tc(hipkern.permute_x(x), wt_, st_, ge, gs, tok, P, max(sizes))
+        one = torch.empty(P, N, device=DEV)
+        if max(sizes) > 16:
+            hipkern.grouped_gemm_t128(xc, xs, wt_, st_, ge, gs, tok, one, P, True)
+        else:
+            hipkern.grouped_gemm_codes(xc, xs, wt_, st_, ge, gs, tok, one, max(sizes), True, n_pairs=P)
+        assert torch.equal(got, one), name
+
+
+def test_off_grid_input_on_each_mechanism():
+    """Raw bf16 x (off the FP8 grid) through fp4_gemv_pairs and fp4_gemm_tc on each way the lo term runs, against the
+    float64 textbook sum (and the numpy oracle's grouped_gemm for the tile-kernel groups); the one-term encoding of the
+    same x misses the bar, so the second term is what closes it."""
+    from dsv41_amd import hipkern, quant
+    w, s, wt_, st_, E, N, K = _mechanism_setup(91)
+    X = 96
+    g = torch.Generator(device=DEV).manual_seed(92)
+    x = torch.randn(X, K, generator=g, device=DEV).to(torch.bfloat16)
+    dense = Dense(w, s, False)
+    rng = np.random.default_rng(93)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)
+    P = 7
+    row_in, expert = t(rng.integers(0, X, P)), t(rng.integers(0, E, P))
+    wt = torch.from_numpy(rng.random(P).astype(np.float32)).to(DEV)
+    got = hipkern.fp4_gemv_pairs(x, w, s, row_in, expert, wt, P)
+    ref = torch.stack([wt[p].double() * (x[int(row_in[p])].double() @ dense[int(expert[p])].T) for p in range(P)])
+    check(got, ref, "fp4_gemv_pairs raw")
+    for name, sizes in MECHANISMS.items():
+        ge, gs, tok, P = _groups(rng, sizes, E, X)
+        got = hipkern.fp4_gemm_tc(hipkern.permute_x(x), wt_, st_, ge, gs, tok, P, max(sizes))
+        ref = torch.empty(P, N, dtype=torch.float64, device=DEV)
+        for i in range(len(sizes)):
+            a, b = int(gs[i]), int(gs[i + 1])
+            ref[a:b] = x[tok[a:b].long()].double() @ dense[int(ge[i])].T
+        check(got, ref, f"fp4_gemm_tc raw, {name}")
+        xc, xs = quant.quant_fp8_e8m0(x)
+        one = torch.empty(P, N, device=DEV)
+        hipkern.grouped_gemm_codes(xc, xs, wt_, st_, ge, gs, tok, one, max(sizes), True, n_pairs=P)
+        assert ref_max_rel(one, ref) > 5e-3, "the one-term encoding alone should miss the bar"
+        if max(sizes) > 16:
+            onp = O.grouped_gemm(bf16_vals(x), w.cpu().numpy(), s.cpu().numpy(), ge.cpu().numpy(), gs.cpu().numpy(), tok.cpu().numpy(),
+                                 len(sizes))
+            close(got.cpu().numpy(), onp, f"fp4_gemm_tc raw, {name}, vs numpy oracle")
+
+
+@pytest.fixture(scope="module")
+def moe_test_weights():
+    """test_moe.py:10-11: E 32, N 2304, K 5120, random bytes, scale bytes 110..134, row-major."""
+    g = torch.Generator(device=DEV).manual_seed(0)
+    E, N, K = 32, 2304, 5120
+    w = torch.randint(0, 256, (E, N, K // 2), generator=g, dtype=torch.uint8, device=DEV)
+    s = torch.randint(110, 135, (E, N, K // 32), generator=g, dtype=torch.uint8, device=DEV)
+    return w, s, Dense(w, s, False)
+
+
+@pytest.mark.parametrize("M", [1, 5, 64, 512])
+def test_reference_test_moe_cases(moe_test_weights, M):
+    """test_moe.py:21-29: raw randn bf16 activations (off the FP8 grid), top-6 of 32 experts per token, GroupedPairs
+    with block_m 16 (M <= 16) or 64, then grouped_fp4_gemm; every token's output row sums its 6 pairs. M = 5 is also
+    checked against the numpy oracle's gemv_pairs."""
+    from dsv41_amd import moe_kernels
+    w, s, dense = moe_test_weights
+    E, N, K = w.shape[0], w.shape[1], w.shape[2] * 2
+    g = torch.Generator(device=DEV).manual_seed(100 + M)
+    topk = 6
+    a = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    eid = torch.randint(0, E, (M, topk), generator=g, device=DEV)
+    wt = torch.rand(M, topk, generator=g, device=DEV)
+    row_in = torch.arange(M, device=DEV).repeat_interleave(topk)
+    pairs = moe_kernels.GroupedPairs(eid.flatten(), row_in, row_in.clone(), wt.flatten(), block_m=16 if M <= 16 else 64)
+    out = moe_kernels.grouped_fp4_gemm(a, w, s, pairs, M)
+    ref = pairs_ref(a, dense, eid.flatten(), row_in, row_in, wt.flatten(), M, N)
+    check(out, ref, f"test_moe.py M={M} raw randn")
+    if M == 5:
+        onp = O.gemv_pairs(bf16_vals(a), w.cpu().numpy(), s.cpu().numpy(), row_in.cpu().numpy(), eid.flatten().cpu().numpy(),
+                           wt.flatten().cpu().numpy())
+        per_tok = onp.reshape(M, topk, N).sum(1)
+        close(out.cpu().numpy(), per_tok, "test_moe.py M=5 vs numpy oracle")
+        # the same pairs with FP8-rounded activations, the old contract: an error far past the bar
+        from dsv41_amd import quant
+        old = moe_kernels.grouped_fp4_gemm(quant.fake_quant_fp8(a), w, s, pairs, M)
+        assert ref_max_rel(old, ref) > 5e-3
+
+
+def test_grouped_pairs_attributes_follow_the_reference():
+    """GroupedPairs (moe_kernels.py:87-124): up to 64 pairs keep their order with one tile per pair (tile_start = 0..n-1,
+    tile_count = 1); more pairs are sorted by expert (stable) with ceil(count / block_m) tiles of consecutive pairs per
+    expert, tables sized to the tile count."""
+    from dsv41_amd import moe_kernels
+    rng = np.random.default_rng(5)
+    t = lambda a: torch.from_numpy(np.asarray(a)).to(DEV)
+    eid = rng.integers(0, 8, 30).astype(np.int32)
+    p = moe_kernels.GroupedPairs(t(eid), t(np.arange(30, dtype=np.int32)), t(np.arange(30, dtype=np.int32)[::-1].copy()),
+                                 t(rng.random(30).astype(np.float32)), 16)
+    assert torch.equal(p.expert.cpu(), torch.from_numpy(eid))
+    assert torch.equal(p.tile_expert.cpu(), torch.from_numpy(eid))
+    assert p.tile_start.tolist() == list(range(30)) and p.tile_count.tolist() == [1] * 30
+    assert p.row_out.tolist() == list(range(29, -1, -1))
+    n, bm = 300, 64
+    eid = rng.choice(6, n, p=[0.5, 0.1, 0.1, 0.1, 0.1, 0.1]).astype(np.int32)
+    rin = rng.integers(0, 90, n).astype(np.int32)
+    p = moe_kernels.GroupedPairs(t(eid), t(rin), t(rin), t(rng.random(n).astype(np.float32)), bm, n_experts=6)
+    order = np.argsort(eid, kind="stable")
+    assert p.expert.tolist() == eid[order].tolist() and p.row_in.tolist() == rin[order].tolist()
+    te, ts, tc = [], [], []
+    counts = np.bincount(eid, minlength=6)
+    starts = np.cumsum(counts) - counts
+    for e in range(6):
+        for k in range(0, counts[e], bm):
+            te.append(e)
+            ts.append(starts[e] + k)
+            tc.append(min(bm, counts[e] - k))
+    assert p.tile_expert.tolist() == te and p.tile_start.tolist() == ts and p.tile_count.tolist() == tc
+
+
+TCW_CASES = {"uniform 1": [1] * 48, "uniform 8": [8] * 48, "uniform 16": [16] * 24, "uniform 32": [32] * 12, "uniform 64": [64] * 6,
+             "decode B=32 mix": [1] * 24 + [2] * 12 + [3] * 6 + [6] * 3 + [12, 20, 40],
+             "verify 192 rows mix": [2] * 16 + [4] * 12 + [8] * 8 + [16] * 6 + [32] * 4 + [64] * 2}
+
+
+@pytest.fixture(scope="module")
+def tcw_weights():
+    """test_fp4_tcw.py:11-16: E 48, N 4608, K 5120, scale bytes 112..127, stored tiled."""
+    from dsv41_amd import quant
+    g = torch.Generator(device=DEV).manual_seed(1)
+    E, N, K = 48, 4608, 5120
+    w = torch.randint(0, 256, (E, N, K // 2), generator=g, dtype=torch.uint8, device=DEV)
+    s = torch.randint(112, 128, (E, N, K // 32), generator=g, dtype=torch.uint8, device=DEV)
+    return quant.tile_fp4(w), quant.tile_fp4_scales(s), Dense(w, s, False)
+
+
+@pytest.mark.parametrize("grid", ["fp8", "raw"])
+@pytest.mark.parametrize("case", list(TCW_CASES))
+def test_reference_test_fp4_tcw_mixes(tcw_weights, case, grid):
+    """test_fp4_tcw.py:38-67: expert e takes the next sizes[e] token rows, groups split at 64 pairs; fp4_gemm_tc on the
+    permuted x with max_tokens = min(max size, 64): groups up to 16 pairs on the generic kernel, larger on the 128-pair
+    tile kernel. grid 'fp8': the test's fake_quant_fp8 activations; 'raw': plain bf16 randn."""
+    from dsv41_amd import hipkern, quant
+    wt_, st_, dense = tcw_weights
+    sizes = TCW_CASES[case]
+    K = wt_.shape[2] * 2
+    ge, gs, tok = [], [0], []
+    T = 0
+    for e, m in enumerate(sizes):
+        toks = list(range(T, T + m))
+        T += m
+        for i in range(0, m, 64):
+            ge.append(e)
+            tok += toks[i:i + 64]
+            gs.append(len(tok))
+    ti = lambda v: torch.tensor(v, device=DEV, dtype=torch.int32)
+    ge, gs, tok = ti(ge), ti(gs), ti(tok)
+    g = torch.Generator(device=DEV).manual_seed(7 + len(sizes))
+    x = torch.randn(T, K, generator=g, device=DEV).to(torch.bfloat16)
+    if grid == "fp8":
+        x = quant.fake_quant_fp8(x)
+    y = hipkern.fp4_gemm_tc(hipkern.permute_x(x), wt_, st_, ge, gs, tok, T, min(max(sizes), 64))
+    ref = torch.empty(T, wt_.shape[1], dtype=torch.float64, device=DEV)
+    for i in range(ge.numel()):
+        a, b = int(gs[i]), int(gs[i + 1])
+        ref[a:b] = x[tok[a:b].long()].double() @ dense[int(ge[i])].T
+    check(y, ref, f"test_fp4_tcw.py {case} ({grid})")
+
+
+@pytest.mark.parametrize("grid", ["fp8", "raw"])
+def test_reference_test_fp4_tc_cases(tcw_weights, grid):
+    """test_fp4_tc.py:34-46 on the first 8 experts: G experts each seeing all M tokens through fp4_gemm_tc, and the
+    same pairs through fp4_gemv_pairs (one pair per program row). The dequantised weights equal the numpy oracle's."""
+    from dsv41_amd import hipkern, quant
+    wt_, st_, dense = tcw_weights
+    K = wt_.shape[2] * 2
+    N = wt_.shape[1]
+    w8, s8 = quant.untile_fp4(wt_[:8]), quant.untile_fp4_scales(st_[:8])
+    assert np.array_equal(dense[3].float().cpu().numpy(), O.dense_weights(w8[3].cpu().numpy(), s8[3].cpu().numpy()))
+    for G, M in [(1, 1), (1, 2), (1, 4), (1, 8), (1, 16), (6, 1), (6, 2), (6, 4), (6, 6)]:
+        g = torch.Generator(device=DEV).manual_seed(G * 100 + M)
+        x = (torch.randn(M, K, generator=g, device=DEV) * 2).to(torch.bfloat16)
+        if grid == "fp8":
+            x = quant.fake_quant_fp8(x)
+        experts = torch.arange(G, device=DEV, dtype=torch.int32)
+        grp_start = torch.arange(0, G * M + 1, M, device=DEV, dtype=torch.int32)
+        pair_tok = torch.arange(M, device=DEV, dtype=torch.int32).repeat(G)
+        P = G * M
+        ref = torch.stack([x.double() @ dense[e].T for e in range(G)]).view(P, N)
+        y = hipkern.fp4_gemm_tc(hipkern.permute_x(x), wt_, st_, experts, grp_start, pair_tok, P, M)
+        check(y, ref, f"test_fp4_tc.py fp4_gemm_tc G={G} M={M} ({grid})")
+        y2 = hipkern.fp4_gemv_pairs(x, w8, s8, pair_tok, experts.repeat_interleave(M), torch.ones(P, device=DEV), P)
+        check(y2, ref, f"test_fp4_tc.py fp4_gemv_pairs G={G} M={M} ({grid})")

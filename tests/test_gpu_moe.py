@@ -218,17 +218,17 @@ def test_grouped_fp4_gemm_scatter_forms(K):
     xc, xs = quant.quant_fp8_e8m0(x)
     g128, s128 = pairs.tables(128)
     y2 = torch.zeros(P, N, device=DEV)
-    hipkern.grouped_gemm_t128(xc, xs, wtl, stl, g128, s128, pairs.row_in, y2, P, True)
+    hipkern.grouped_gemm_t128(xc, xs, wtl, stl, g128, s128, pairs.s_row_in, y2, P, True)
     n = int(gs[-1])
     assert n == P - 2
-    rs = pairs.row_out[:n].long()
+    rs = pairs.s_row_out[:n].long()
     exp = torch.zeros(R, N, device=DEV)
-    exp[rs] = y2[:n] * pairs.weight[:n, None]
+    exp[rs] = y2[:n] * pairs.s_weight[:n, None]
     assert torch.equal(out, exp)
     out0 = torch.randn(R, N, device=DEV)
     out1 = moe_kernels.grouped_fp4_gemm(x, wtl, stl, pairs, R, out=out0.clone(), tiled=True)   # read, add, write
     exp1 = out0.clone()
-    exp1[rs] = out0[rs] + y2[:n] * pairs.weight[:n, None]
+    exp1[rs] = out0[rs] + y2[:n] * pairs.s_weight[:n, None]
     assert torch.equal(out1, exp1)
     ref = np.zeros((R, N), np.float64)
     xv, wn, sn = bf16_vals(x).astype(np.float64), w.cpu().numpy(), s.cpu().numpy()
@@ -283,19 +283,25 @@ def test_t128_entry_bounds():
     gs = torch.tensor([0, 5, 400], dtype=torch.int32, device=DEV)            # the second range runs past n_pairs
     rows = torch.tensor([0, 3, -4, 8, 7, 1, 2, 100000], dtype=torch.int32, device=DEV)
     y = torch.full((9, N), 5.0, device=DEV)
-    _lib.call("dsv41_fp4_grouped_gemm_t128", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), 8, _lib.ptr(rows), _lib.ptr(w),
-              w.stride(0), _lib.ptr(s), s.stride(0), 0, E, N, K, _lib.ptr(ge), _lib.ptr(gs), 2, 8, _lib.ptr(y), N, _lib.stream(DEV))
-    got = y.cpu().numpy()
-    xv, wn, sn = bf16_vals(x), w.cpu().numpy(), s.cpu().numpy()
-    for p in range(8):
-        e = 1 if p < 5 else 2
-        r = int(rows[p])
-        if 0 <= r < 8:
-            close(got[p], O.gemv_pairs(xv, wn, sn, [r], [e], [1.0])[0], f"t128 pair {p}")
-        else:
-            assert np.all(got[p] == 0.0), f"pair {p}: row {r} outside the input must read zeros"
-    assert np.all(got[8] == 5.0), "a row past n_pairs is not written"
-    bad = lambda **kw: _lib.lib().dsv41_fp4_grouped_gemm_t128(_lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), 8, _lib.ptr(rows),
+    # the one-term call, then a raw (off-grid) x with its second term: the MODE 2 pass keeps the same bounds
+    xr = rand_x(8, K, 33).to(DEV)
+    hc, hs, lc, ls, flag = quant.quant_fp8_split(xr)
+    for xv, (c, sc, lo) in ((bf16_vals(x), (xc, xs, (None, None, None))), (bf16_vals(xr), (hc, hs, (_lib.ptr(lc), _lib.ptr(ls), _lib.ptr(flag))))):
+        y = torch.full((9, N), 5.0, device=DEV)
+        _lib.call("dsv41_fp4_grouped_gemm_t128", _lib.ptr(c), c.stride(0), _lib.ptr(sc), sc.stride(0), 8, *lo, _lib.ptr(rows), _lib.ptr(w),
+                  w.stride(0), _lib.ptr(s), s.stride(0), 0, E, N, K, _lib.ptr(ge), _lib.ptr(gs), 2, 8, _lib.ptr(y), N, _lib.stream(DEV))
+        got = y.cpu().numpy()
+        wn, sn = w.cpu().numpy(), s.cpu().numpy()
+        for p in range(8):
+            e = 1 if p < 5 else 2
+            r = int(rows[p])
+            if 0 <= r < 8:
+                close(got[p], O.gemv_pairs(xv, wn, sn, [r], [e], [1.0])[0], f"t128 pair {p}")
+            else:
+                assert np.all(got[p] == 0.0), f"pair {p}: row {r} outside the input must read zeros"
+        assert np.all(got[8] == 5.0), "a row past n_pairs is not written"
+    bad = lambda **kw: _lib.lib().dsv41_fp4_grouped_gemm_t128(_lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), 8, None, None, None,
+                                                              _lib.ptr(rows),
                                                               _lib.ptr(w), w.stride(0), _lib.ptr(s), s.stride(0), 0, E, kw.get("N", N),
                                                               kw.get("K", K), _lib.ptr(ge), _lib.ptr(gs), 2, 8, _lib.ptr(y), N, _lib.stream(DEV))
     assert bad(N=128) == -1 and bad(K=256) == -1

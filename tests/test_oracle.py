@@ -324,7 +324,7 @@ def test_every_oracle_function_has_a_pin():
     import inspect
     helpers = {"f32_bits", "bits_f32", "f32_to_bf16_bits", "bf16_bits_to_f32", "bf16_round", "e4m3_encode", "e4m3_decode", "unpack_fp4",
                "dequant_fp4_f32", "dequant_fp4_values", "untile_fp4", "untile_fp4_scales", "quant_fp8_e8m0", "pow2_scale", "unpermute_x",
-               "sigmoid_f32", "dense_weights", "expert_pair", "deq64", "rel_l2", "max_abs_over_rms"}
+               "sigmoid_f32", "dense_weights", "expert_pair", "deq64", "rel_l2", "max_abs_over_rms", "fp8_split_values"}
     fns = {n for n, f in inspect.getmembers(O, inspect.isfunction) if f.__module__ == O.__name__ and not n.startswith("_")}
     missing = fns - helpers - set(O.PINS)
     assert not missing, f"oracle functions without a pin: {sorted(missing)}"
@@ -451,3 +451,47 @@ def test_linear_fp8w_pins():
         for n in range(N):
             v = float(np.dot(xg[b * G + n // gc].astype(np.float64), d[n]))
             assert got[b, n] == np.float32(v)
+
+
+def test_lo_exponent_brute_force():
+    """lo_exponent(a) is the smallest e >= -126 with a <= 448 * 2^e, found by scanning e; on random magnitudes over the
+    whole fp32 range, on powers of two and on the 448 * 2^k boundaries and their fp32 neighbours."""
+    rng = np.random.default_rng(7)
+    a = np.concatenate([np.exp(rng.uniform(-100, 88, 3000)).astype(np.float32),
+                        np.ldexp(np.float32(1.0), np.arange(-149, 127)).astype(np.float32),
+                        np.ldexp(np.float32(448.0), np.arange(-140, 118)).astype(np.float32)])
+    a = np.concatenate([a, np.nextafter(a, np.float32(np.inf)), np.nextafter(a, np.float32(0)), [0.0, 1e-45]]).astype(np.float32)
+    got = O.lo_exponent(a)
+    for ai, g in zip(a.astype(np.float64), got):
+        e = -126
+        while ai > 448.0 * 2.0 ** e:
+            e += 1
+        assert g == e, (ai, g, e)
+
+
+def test_fp8_split_pins():
+    """hi is the golden-pinned quant_fp8 encoding; lo is torch's float8_e4m3fn cast of the residual at its scale; hi + lo
+    reconstructs bf16 x exactly except residuals below lo's normal range (then within 2^-21 of the block amax); an
+    FP8-grid x gives all-zero lo codes."""
+    import torch
+    rng = np.random.default_rng(11)
+    for scale in (1.0, 1e-3, 300.0):
+        x = torch.from_numpy((rng.standard_normal((64, 256)) * scale).astype(np.float32)).to(torch.bfloat16).float().numpy()
+        x[0, :32] = 0.0
+        x[1, :32] = torch.tensor(1e-6).to(torch.bfloat16).float().item()   # a block under the hi rule's 1e-4 floor
+        hc, hs, lc, ls = O.fp8_split(x)
+        qc, qs = O.quant_fp8_e8m0(x)
+        assert np.array_equal(hc, qc) and np.array_equal(hs, qs)
+        hv = O.e4m3_decode(hc).astype(np.float64) * np.ldexp(1.0, np.repeat(hs.astype(np.int32) - 127, 32, axis=-1))
+        r = (x.astype(np.float64) - hv).astype(np.float32)
+        e2 = ls.astype(np.int32) - 127
+        want = torch.from_numpy((r / np.ldexp(1.0, np.repeat(e2, 32, axis=-1))).astype(np.float32)).to(torch.float8_e4m3fn)
+        assert np.array_equal(lc, want.view(torch.uint8).numpy())
+        v = O.fp8_split_values(hc, hs, lc, ls)
+        amax = np.repeat(np.abs(x.reshape(-1, 32)).max(-1), 32).reshape(x.shape).astype(np.float64)
+        err = np.abs(v - x)
+        assert np.all(err <= amax * 2.0 ** -21)
+        assert np.mean(err == 0) > 0.9999
+    fq = O.fake_quant_fp8(x)
+    _, _, lc0, _ = O.fp8_split(fq)
+    assert not np.any(lc0 & 0x7F)
