@@ -82,8 +82,13 @@ def make_layers(torch, dev, n, seed):
     return layers
 
 
-def graph_time(torch, fn_steps, steps, warmup):
-    """Capture `steps` calls (fn_steps(i) for i in range(steps)) in one graph; replay warmup then timed."""
+REPLAYS = 50   # timed replays of each captured graph; the median is reported (p10 / p90 kept in graph_time.stats)
+
+
+def graph_time(torch, fn_steps, steps, warmup, replays=None):
+    """Capture `steps` calls (fn_steps(i) for i in range(steps)) in one graph; replay it for warm-up, then REPLAYS times
+    back to back with one HIP event pair around each replay (one synchronisation before and after the set). Returns
+    (median seconds per step, graph); graph_time.stats holds the p10 / median / p90 per step and the replay count."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())   # inputs were produced on the current stream
     with torch.cuda.stream(s):
@@ -96,16 +101,18 @@ def graph_time(torch, fn_steps, steps, warmup):
             fn_steps(i)
     for _ in range(max(1, warmup // max(1, steps) + 1)):
         g.replay()
+    n = replays or REPLAYS
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     torch.cuda.synchronize()
-    times = []
-    for _ in range(3):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
+    for e0, e1 in ev:
         e0.record()
         g.replay()
         e1.record()
-        torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1) / 1e3 / steps)
+    torch.cuda.synchronize()
+    times = sorted(e0.elapsed_time(e1) / 1e3 / steps for e0, e1 in ev)
+    q = lambda f: times[min(n - 1, int(round(f * (n - 1))))]
+    graph_time.stats = {"replays": n, "steps_per_replay": steps, "p10_us": round(q(0.1) * 1e6, 3), "median_us": round(statistics.median(times) * 1e6, 3),
+                        "p90_us": round(q(0.9) * 1e6, 3)}
     return statistics.median(times), g
 
 
@@ -195,7 +202,7 @@ def zipf_routing(T, seed, s=1.1):
     return eid, wt
 
 
-def bench_prefill(torch, dev, ex, T, iters=5, seed=31):
+def bench_prefill(torch, dev, ex, T, iters=20, seed=31):
     """prefill of T tokens (x bf16 ~N(0,1) -> FP8 fake-quant -> codes; Zipf routing) through the
     expert path: quantise + dispatch, w13 GEMM + SwiGLU, w2 GEMM, combine. Times each stage with HIP events
     (median over iters) and returns a dict."""
@@ -308,6 +315,23 @@ def _time_layer_calls(L, bufs, Es, steps_cap, budget_s, it0=0):
     return statistics.median(times[1:] if len(times) > 1 else times), len(times)
 
 
+def llc_bytes() -> int:
+    """The largest cache of cpu0 from sysfs (the last-level cache), in bytes; 0 when unreadable."""
+    best = 0
+    base = "/sys/devices/system/cpu/cpu0/cache"
+    try:
+        for d in os.listdir(base):
+            try:
+                v = open(os.path.join(base, d, "size")).read().strip()
+            except OSError:
+                continue
+            mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(v[-1:].upper(), 1)
+            best = max(best, int(v.rstrip("KkMmGg")) * mult)
+    except OSError:
+        pass
+    return best
+
+
 def cpu_baselines(steps_cap=80):
     """CPU numbers, all on the same host buffers and the same worker CPUs (this process's CPUs minus one core
     per NUMA node, as cpumoe.default_cpu_list):
@@ -332,13 +356,26 @@ def cpu_baselines(steps_cap=80):
     M.cpumoe_set_int8(2)
     res["host"]["worker_cpus"] = len(lst)
     res["host"]["workers_pinned"] = M.cpumoe_threads_pinned()
+    # the host's DRAM read rate with every worker: a 1 GiB stream (32x the 32 MiB L3 and more) read with plain loads and
+    # with the expert kernels' 8 KB software prefetch; probed before, between and after the timed blocks (the host's
+    # clocks settle during the first calls), the best reading reported
     bw_bytes = 1 << 30
     pbw = M.cpumoe_alloc(bw_bytes)
     np.frombuffer((ctypes.c_uint8 * bw_bytes).from_address(pbw), dtype=np.uint8)[:] = 1
-    res["host"]["dram_read_GBps"] = round(M.cpumoe_bw_test(pbw, bw_bytes, 5, -1), 1)
-    M.cpumoe_free(pbw, bw_bytes)
+    probes = []
 
-    Es = 48
+    def probe(when):
+        for pf in (0, 8192):
+            M.cpumoe_set_prefetch(pf)
+            probes.append({"when": when, "prefetch_bytes": pf, "GBps": round(M.cpumoe_bw_test(pbw, bw_bytes, 5, -1), 1)})
+        M.cpumoe_set_prefetch(int(os.environ.get("DSV41_CPU_PF", "8192")))   # the kernels' setting again
+    probe("before warm-up")
+
+    # the expert subset: at least 48 experts (0.91 GB) and at least 4x the last-level cache, so no call finds its
+    # experts cache-resident (rotating ids; 8 of the subset per call)
+    llc = llc_bytes()
+    Es = min(E, max(48, -(-4 * llc // expert_bytes())))
+    res["host"]["llc_bytes"] = llc
     b13, bs13, b2, bs2 = 2 * I * (H // 2), 2 * I * (H // 32), H * (I // 2), H * (I // 32)
     rng = np.random.default_rng(3)
     sizes = (Es * b13, Es * bs13, Es * b2, Es * bs2)
@@ -348,8 +385,8 @@ def cpu_baselines(steps_cap=80):
         np.frombuffer((ctypes.c_uint8 * nbytes).from_address(p), dtype=np.uint8)[:] = rng.integers(lo, hi, nbytes, dtype=np.uint8)
         bufs.append(p)
     sel = TOPK * expert_bytes()
-    sample = (f"configs[1] layer shapes, 48-expert subset (0.91 GB), top-8 per call with rotating ids, int8 W4A8 mode, "
-              f"{len(lst)} pinned worker CPUs")
+    sample = (f"configs[1] layer shapes, {Es}-expert subset ({Es * expert_bytes() / 1e9:.2f} GB, {Es * expert_bytes() / max(llc, 1):.0f}x the "
+              f"last-level cache), top-8 per call with rotating ids, int8 W4A8 mode, {len(lst)} pinned worker CPUs")
     baseline = {"value": None, "note": "oracle/_ref not built or host lacks its ISA"}
     R = _ref_lib()
     libs = [M]
@@ -361,14 +398,25 @@ def cpu_baselines(steps_cap=80):
     # they are timed in alternating blocks of 10 calls, so neither gains from running later
     for L in libs:
         _time_layer_calls(L, bufs, Es, 1 << 20, 1.5)
+    probe("after warm-up")
     meds = {id(L): [] for L in libs}
-    for blk in range(max(1, steps_cap // 10)):
+    n_blk = max(1, steps_cap // 10)
+    for blk in range(n_blk):
         for L in libs:
             meds[id(L)].append(_time_layer_calls(L, bufs, Es, 11, 5.0, it0=11 * blk)[0])
+        if blk == n_blk // 2:
+            probe("between timing blocks")
+    probe("after the timed blocks")
+    M.cpumoe_free(pbw, bw_bytes)
+    best_bw = max(p["GBps"] for p in probes)
+    res["host"]["dram_read_GBps"] = best_bw
+    res["host"]["dram_read_probes"] = probes
     if R is not None:
         med = statistics.median(meds[id(R)])
         baseline = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
                     "kind": "reference", "sample": sample + f", median of {len(meds[id(R)])} blocks of 10 calls, alternating with cpu_port"}
+    rates = [sel / statistics.median(meds[id(L)]) / 1e9 for L in libs]
+    res["host"]["layer_rate_within_dram_read"] = bool(max(rates) <= best_bw)
     med = statistics.median(meds[id(M)])
     res["cpu_port"] = {"value": round(med * 1e6, 1), "unit": "us/layer", "gbps": round(sel / med / 1e9, 1), "cores": len(lst),
                        "kind": "port", "sample": sample + f", median of {len(meds[id(M)])} blocks of 10 calls, alternating with cpu_baseline",
@@ -597,7 +645,7 @@ def mfma_rate(torch, dev, iters=2000):
 
 def plain_read_us(torch, dev, buf, nbytes, blocks, waves, sync=0, steps=20):
     """Seconds per launch of a plain read of nbytes (dsv41_selftest_stream) in one launch shape, graph-timed (steps launches
-    per graph, median of 3 replays) over rotating regions of buf: 160 MiB regions (4 of them, 640 MiB > the 256 MB
+    per graph, median of the replays) over rotating regions of buf: 160 MiB regions (4 of them, 640 MiB > the 256 MB
     Infinity Cache) below 1 GiB, else two regions of nbytes."""
     from dsv41_amd import _lib
     out = torch.zeros(4, dtype=torch.int32, device=dev)
@@ -719,6 +767,7 @@ def main():
 
     progress("layers resident")
     t_routed, _ = bench_decode(torch, dev, layers, K, W, 1)
+    timing = {"layer": dict(graph_time.stats)}
     progress(f"configs[1] decode layer {t_routed * 1e6:.2f} us")
     value = sel_bytes / t_routed / 1e12
     extra = {}
@@ -726,6 +775,7 @@ def main():
     # logits and activations it also reads are < 0.03 % of that and not counted)
     w13_bytes = TOPK * (2 * I * (H // 2) + 2 * I * (H // 32))
     t_up = bench_up_kernel(torch, dev, layers, K, W)
+    timing["up_kernel"] = dict(graph_time.stats)
     roof = {"bound": "hbm", "kernel": "moe_decode_up_kernel<1,8,6,1> (routing + w13 + SwiGLU, M=1)", "achieved": round(w13_bytes / t_up / 1e9, 1),
             "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(w13_bytes / t_up / HBM_PEAK, 4), "traffic": UP_TRAFFIC_BYTES,
             "traffic_over_algorithmic": round(UP_TRAFFIC_BYTES / w13_bytes, 4), "avg_launch_us": round(t_up * 1e6, 2),
@@ -780,11 +830,12 @@ def main():
         for M in (4, 8, 16):
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
-                                     "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4)}
+                                     "TBps": round(uniq * eb / t_m / 1e12, 3), "frac_hbm": round(uniq * eb / t_m / HBM_PEAK, 4),
+                                     "p10_us": graph_time.stats["p10_us"], "p90_us": graph_time.stats["p90_us"]}
         progress("decode M = 4 / 8 / 16")
         extra["prefill_2048"] = dict(bench_prefill(torch, dev, layers[0], 2048),
                                      workload="configs[3]: 2048 tokens x top-8, Zipf(1.1) routing, full expert path")
-        extra["prefill_16384_probe"] = dict(bench_prefill(torch, dev, layers[1], 16384, iters=3),
+        extra["prefill_16384_probe"] = dict(bench_prefill(torch, dev, layers[1], 16384, iters=10),
                                             workload="16,384-token probe (~341 pairs per expert)")
         ks = max(2, min(K, 10))
         t_s, b_s = bench_stack(torch, dev, layers, ks, 1)
@@ -832,6 +883,8 @@ def main():
         "frac_hbm_peak": round(value * 1e12 / HBM_PEAK, 4),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "timing": dict(timing, protocol=f"each figure: one graph of `steps` calls, replayed {REPLAYS} times back to back with an "
+                                        "event pair per replay, median per step (p10 / p90 beside it)"),
     }
     result.update(extra)
     print(json.dumps(result))

@@ -679,7 +679,16 @@ void bw_job(void* q, int t) {
     const uint8_t* a = B.p + b0 + tin * per;
     __m512i s0 = _mm512_setzero_si512(), s1 = s0, s2 = s0, s3 = s0;
     size_t i = 0;
+    // the same software prefetch distance as the expert kernels' weight streams (g_pf bytes ahead), so the probe
+    // measures what a core's stream can draw, not the hardware prefetcher's reach alone
+    const size_t pf = (size_t)g_pf;
     for (; i + 256 <= per; i += 256) {
+        if (pf && i + pf + 256 <= per) {
+            _mm_prefetch((const char*)(a + i + pf), _MM_HINT_T0);
+            _mm_prefetch((const char*)(a + i + pf + 64), _MM_HINT_T0);
+            _mm_prefetch((const char*)(a + i + pf + 128), _MM_HINT_T0);
+            _mm_prefetch((const char*)(a + i + pf + 192), _MM_HINT_T0);
+        }
         s0 = _mm512_add_epi64(s0, _mm512_loadu_si512(a + i));
         s1 = _mm512_add_epi64(s1, _mm512_loadu_si512(a + i + 64));
         s2 = _mm512_add_epi64(s2, _mm512_loadu_si512(a + i + 128));
