@@ -100,6 +100,62 @@ __device__ __forceinline__ float fq8_value(uint32_t code, int e) {
     return e4m3_decode(code) * __uint_as_float((uint32_t)(127 + e) << 23);
 }
 
+// ------------------------------------------------------------------------------------------ two-term FP8 split
+// bf16 activations off the FP8 grid as two E4M3 x E8M0 terms per 32-group: hi = the per-32 rounding above, lo = the
+// residual x - hi (exact in fp32: x has 8 significant bits, hi 4, within 24 bits of each other) rounded the same way
+// with a scale of its own. hi + lo == x unless a residual falls below lo's normal range (then within 2^-21 of the
+// group's amax). lo's exponent: the smallest e >= -126 with amax / 2^e <= 448, no floor (residuals may be tiny):
+// amax = m 2^ea, m in [1, 2), needs 2^e >= m / 1.75 * 2^(ea - 8), i.e. e = ea - 8 when m <= 1.75, else ea - 7.
+__device__ __forceinline__ int lo_exponent(float amax) {
+    const uint32_t u = __float_as_uint(amax);
+    const int ea = (int)((u >> 23) & 0xFFu) - 127;
+    if (ea < -126) return -126;                           // zero or subnormal: 448 * 2^-126 exceeds it
+    const int e = ea - 8 + ((u & 0x7FFFFFu) > 0x600000u ? 1 : 0);
+    return e < -126 ? -126 : e;
+}
+
+// One lane's 16 consecutive bf16 values (two 16-byte vectors) of a 32-group whose other half sits on the adjacent
+// lane (lane ^ 1, which must run the same call): their hi and lo codes as 16 bytes each, in natural k order when the
+// input is 8-k permuted (position j holds input position (j & ~7) | bitrev3(j & 7)), and the two exponents (E8M0
+// bytes e + 127). Returns whether a lo code of this lane is non-zero.
+__device__ __forceinline__ bool fp8_split16(const v4i w0, const v4i w1, int permuted, v4i& hi, v4i& lo, int& e, int& e2) {
+    const uint32_t wd[8] = {(uint32_t)w0.x, (uint32_t)w0.y, (uint32_t)w0.z, (uint32_t)w0.w,
+                            (uint32_t)w1.x, (uint32_t)w1.y, (uint32_t)w1.z, (uint32_t)w1.w};
+    // value at input position i (bf16 -> fp32 is a shift)
+    auto val = [&](int i) { return __uint_as_float((i & 1) ? (wd[i >> 1] & 0xFFFF0000u) : (wd[i >> 1] << 16)); };
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(val(i)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
+    e = fq8_exponent(amax);
+    // codes are packed as they are made, in output (natural k) order: position j holds input position (j & ~7) |
+    // bitrev3(j & 7) when permuted; the residuals are kept in output order (only their amax depends on all of them)
+    float r[16];
+    uint32_t cw[4] = {0, 0, 0, 0}, cw2[4] = {0, 0, 0, 0};
+    float rmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int sj = (j & ~7) | ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1);
+        const float v = permuted ? val(sj) : val(j);
+        const uint32_t q = fq8_code(v, e);
+        cw[j >> 2] |= q << (8 * (j & 3));
+        r[j] = __fsub_rn(v, fq8_value(q, e));   // the residual, exact
+        rmax = fmaxf(rmax, fabsf(r[j]));
+    }
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 2));
+    e2 = lo_exponent(rmax);
+    uint32_t nz = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t q2 = fq8_code(r[j], e2);
+        nz |= q2 & 0x7Fu;
+        cw2[j >> 2] |= q2 << (8 * (j & 3));
+    }
+    hi = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
+    lo = v4i{(int)cw2[0], (int)cw2[1], (int)cw2[2], (int)cw2[3]};
+    return nz != 0;
+}
+
 // ------------------------------------------------------------------------------------------ waves
 __device__ __forceinline__ float wave_max32(float v) {  // max over each 32-lane half of the wave
 #pragma unroll
@@ -305,15 +361,22 @@ __device__ __forceinline__ void pipeline_start(int n, LoadF&& load) {
     }
 }
 
-template <int PF, typename LoadF, typename UseF>
+// UNCOND: load(slot, it) is safe for it >= n (a buffer load past its descriptor's range returns 0 without a memory
+// access), so the drain and the short path issue their loads unconditionally: each slot register is then written on
+// every path and the compiler keeps no copies of the old value (a conditional load makes the slot a phi).
+// DRAIN_BARRIER: a scheduling barrier after each consume of the drain and the short path too, so the compiler does not
+// hoist every remaining slot's operand reads (LDS) ahead of the first MFMA and keeps them live together.
+template <int PF, bool DRAIN_BARRIER = false, bool UNCOND = false, typename LoadF, typename UseF>
 __device__ __forceinline__ void pipeline_finish(int n, LoadF&& load, UseF&& use) {
     if (n < PF) {  // short: issue every load, then consume in order (one memory latency, not n)
 #pragma unroll
         for (int i = 0; i < PF; ++i)
-            if (i < n) load(i, i);
+            if (UNCOND || i < n) load(i, i);
 #pragma unroll
-        for (int i = 0; i < PF; ++i)
+        for (int i = 0; i < PF; ++i) {
             if (i < n) use(i);
+            if (DRAIN_BARRIER) __builtin_amdgcn_sched_barrier(0);
+        }
         return;
     }
     int it = 0;
@@ -328,13 +391,15 @@ __device__ __forceinline__ void pipeline_finish(int n, LoadF&& load, UseF&& use)
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
         use(i);
-        if (it + PF + i < n) load(i, it + PF + i);
+        if (UNCOND || it + PF + i < n) load(i, it + PF + i);
         __builtin_amdgcn_sched_barrier(0);
     }
     it += PF;
 #pragma unroll
-    for (int i = 0; i < PF; ++i)
+    for (int i = 0; i < PF; ++i) {
         if (it + i < n) use(i);
+        if (DRAIN_BARRIER) __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
 template <int PF, typename LoadF, typename UseF>

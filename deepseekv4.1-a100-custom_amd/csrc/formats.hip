@@ -139,23 +139,9 @@ __global__ void __launch_bounds__(256) quant_fp8_vec_kernel(const void* __restri
 
 // ------------------------------------------------------------------------------------------ two-term FP8 split
 // Activations that are not on the FP8 grid (any bf16 row, as the reference's bf16-operand GEMMs accept) as the sum of
-// two E4M3 x E8M0 terms per 32-group: hi = the per-32 FP8 rounding above (bit-identical codes and scales), lo = the
-// residual x - hi (exact in fp32: x has 8 significant bits, hi 4, and they are within 24 bits of each other) rounded
-// the same way with a scale of its own. A bf16 value takes 8 significant bits, two E4M3 terms 4 + 4, so hi + lo equals
-// x exactly unless its residual falls below the lo term's normal range; then the error is under 2^-17 of the lo
-// term's amax, itself at most 2^-4 of the group's amax. lo_flag (int32, cleared by the entry first) is set when some
-// lo code of any group is not zero, so kernels can skip the second term of FP8-grid input.
-
-// smallest e >= -126 with amax / 2^e <= 448 (no floor: residuals can be far below 1e-4): amax = m 2^ea, m in [1, 2),
-// needs 2^e >= m / 1.75 * 2^(ea - 8), i.e. e = ea - 8 when m <= 1.75, else ea - 7
-__device__ __forceinline__ int lo_exponent(float amax) {
-    const uint32_t u = __float_as_uint(amax);
-    const int ea = (int)((u >> 23) & 0xFFu) - 127;
-    if (ea < -126) return -126;                           // zero or subnormal: 448 * 2^-126 exceeds it
-    const int e = ea - 8 + ((u & 0x7FFFFFu) > 0x600000u ? 1 : 0);
-    return e < -126 ? -126 : e;
-}
-
+// two E4M3 x E8M0 terms per 32-group (fp8_split16): hi = the per-32 FP8 rounding above (bit-identical codes and
+// scales), lo = the residual rounded with a scale of its own. lo_flag (int32, optional; cleared by the entry first) is
+// set when some lo code of any group is not zero, so kernels can skip the second term of FP8-grid input.
 __global__ void __launch_bounds__(256) quant_fp8_split_kernel(const uint16_t* __restrict__ x, unsigned n_chunks, int K, long long ldx,
                                                               int permuted, uint8_t* __restrict__ hc, uint8_t* __restrict__ hs,
                                                               uint8_t* __restrict__ lc, uint8_t* __restrict__ ls, int* lo_flag) {
@@ -165,53 +151,12 @@ __global__ void __launch_bounds__(256) quant_fp8_split_kernel(const uint16_t* __
         const unsigned cpr = (unsigned)K >> 4;
         const unsigned r = t / cpr, c = t - r * cpr;
         const int k0 = (int)c * 16;
-        float f[16];
         const v4i* src = (const v4i*)(x + (long long)r * ldx + k0);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const v4i w = src[j];
-            const uint32_t wd[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f[8 * j + 2 * i] = bf16_to_f32(wd[i] & 0xFFFFu);
-                f[8 * j + 2 * i + 1] = bf16_to_f32(wd[i] >> 16);
-            }
-        }
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(f[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
-        const int e = fq8_exponent(amax);
-        uint32_t q[16], q2[16];
-        float rmax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            q[i] = fq8_code(f[i], e);
-            f[i] = __fsub_rn(f[i], fq8_value(q[i], e));   // the residual, exact
-            rmax = fmaxf(rmax, fabsf(f[i]));
-        }
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 2));
-        const int e2 = lo_exponent(rmax);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            q2[i] = fq8_code(f[i], e2);
-            nz |= (q2[i] & 0x7Fu) != 0u;
-        }
-        // natural position j holds input position (j & ~7) | bitrev3(j & 7) when the input is 8-k permuted
-        uint32_t cw[4], cw2[4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            cw[w] = cw2[w] = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int j = 4 * w + b;
-                const int s = permuted ? ((j & ~7) | ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1)) : j;
-                cw[w] |= q[s] << (8 * b);
-                cw2[w] |= q2[s] << (8 * b);
-            }
-        }
-        *(v4i*)(hc + (long long)r * K + k0) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
-        *(v4i*)(lc + (long long)r * K + k0) = v4i{(int)cw2[0], (int)cw2[1], (int)cw2[2], (int)cw2[3]};
+        v4i hi, lo;
+        int e, e2;
+        nz = fp8_split16(src[0], src[1], permuted, hi, lo, e, e2);
+        *(v4i*)(hc + (long long)r * K + k0) = hi;
+        *(v4i*)(lc + (long long)r * K + k0) = lo;
         if ((c & 1) == 0) {
             hs[(long long)r * (K >> 5) + (c >> 1)] = (uint8_t)(e + 127);
             ls[(long long)r * (K >> 5) + (c >> 1)] = (uint8_t)(e2 + 127);
@@ -219,7 +164,7 @@ __global__ void __launch_bounds__(256) quant_fp8_split_kernel(const uint16_t* __
     }
     // one vector store of 1 per wave that saw a non-zero lo code (every writer stores the same value)
     const unsigned long long any = __ballot(nz);
-    if (any && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(any)) *(volatile int*)lo_flag = 1;
+    if (lo_flag && any && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(any)) *(volatile int*)lo_flag = 1;
 }
 
 __global__ void clear_flag_kernel(int* flag) {
@@ -374,13 +319,13 @@ extern "C" int dsv41_quant_fp8(const void* x, int x_f32, long long rows, int K, 
 
 extern "C" int dsv41_quant_fp8_split(const uint16_t* x, long long rows, int K, long long ldx, int permuted, uint8_t* hc, uint8_t* hs,
                                      uint8_t* lc, uint8_t* ls, int* lo_flag, void* stream) {
-    if (!x || !hc || !hs || !lc || !ls || !lo_flag || rows < 0 || K <= 0 || (K & 31) || ldx < K || (ldx & 7) || (((uintptr_t)x) & 15) ||
+    if (!x || !hc || !hs || !lc || !ls || rows < 0 || K <= 0 || (K & 31) || ldx < K || (ldx & 7) || (((uintptr_t)x) & 15) ||
         (((uintptr_t)hc) & 15) || (((uintptr_t)lc) & 15))
         return DSV41_EINVAL;
     const long long n = rows * (K / 16);
     if (n >= (1ll << 31)) return DSV41_EINVAL;
     hipStream_t st = (hipStream_t)stream;
-    clear_flag_kernel<<<1, 64, 0, st>>>(lo_flag);
+    if (lo_flag) clear_flag_kernel<<<1, 64, 0, st>>>(lo_flag);
     if (n > 0)
         quant_fp8_split_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(x, (unsigned)n, K, ldx, permuted, hc, hs, lc, ls, lo_flag);
     return (int)hipGetLastError();

@@ -38,14 +38,16 @@ struct GroupedArgs {
     int shard_start, shard_n, zero_out, min_tok, max_tok, vec_store;
     int accum;                               // 0 store, 1 add (distinct rows), 2 atomic add (rows may repeat)
     int lds_rows;                            // B_LDS: activation rows staged per pass (<= 16)
-    // TERMS == 2: the second FP8 term of off-grid activations (dsv41_quant_fp8_split), same strides as xc / xs; its
-    // MFMAs run only when *lo_flag is non-zero
-    const uint8_t* xlc; const uint8_t* xls; const int* lo_flag;
+    // TERMS == 2: the second FP8 term of off-grid activations (dsv41_quant_fp8_split), same strides as xc / xs
+    const uint8_t* xlc; const uint8_t* xls;
     const int* run_if;                       // optional: the launch does nothing when *run_if == 0
 };
 
 // LDS row stride for staged activation codes: +16 bytes so 16 rows fall in different banks
 __device__ __forceinline__ int lds_stride(int K) { return K + 16; }
+
+// A lane offset past every buffer this file's descriptors cover (the entries keep their byte counts below it)
+#define OOB 0xFFFFFFF0u
 
 // One wave = one (group, 16-row block); 4 waves per workgroup on consecutive row blocks of one group. A pass
 // covers up to 16 pairs of the group (one MFMA column each); larger groups take several passes.
@@ -53,8 +55,10 @@ __device__ __forceinline__ int lds_stride(int K) { return K + 16; }
 // memory queue holds only weight tiles (PF in flight per wave); otherwise B is read from global memory
 // (L1/L2-resident) with non-divergent loads. Lanes whose column has no pair read row 0: their output
 // column is never stored.
-// TERMS == 2 (with B_LDS): the lo term's rows are staged beside the hi rows and each weight tile takes a second MFMA
-// with them into the same accumulator, when lo_flag is set; otherwise the kernel runs exactly the one-term arithmetic.
+// TERMS == 2 (with B_LDS): the lo term's rows are staged beside the hi rows, and a pass covers up to 8 pairs: MFMA column
+// c < 8 is pair c's hi row, column c + 8 its lo row, so one MFMA per weight tile computes both terms and the epilogue
+// adds lane c + 8's accumulator to lane c's. For FP8-grid activations the lo codes are +0, so column c + 8 holds signed
+// zeros and the sum is the one-term result bit for bit; no flag is read.
 template <int TILED, int PF, int B_LDS, int NKC, int TERMS = 1>
 __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -85,39 +89,53 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
         return;
     }
     const int K = a.K, nk = K >> 7, Kh = K >> 1, Ks = K >> 5;
-    const uint8_t* wl = a.W + (long long)e * a.stride_we + wtile_off<TILED>(nb, 0, nk, Kh, lane);
-    const uint8_t* sl = a.S + (long long)e * a.stride_se + stile_off<TILED>(nb, 0, nk, Ks, lane);
+    // the expert's weights and scales through buffer descriptors (base and byte count in scalar registers, a 32-bit
+    // lane offset, the k step as a scalar offset): 4 VGPRs per tile in flight instead of 64-bit addresses per slot
+    const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.W + (long long)e * a.stride_we, (uint32_t)a.stride_we);
+    const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(a.S + (long long)e * a.stride_se, (uint32_t)a.stride_se);
+
+    const uint32_t wvo = (uint32_t)wtile_off<TILED>(nb, 0, nk, Kh, lane), svo = (uint32_t)stile_off<TILED>(nb, 0, nk, Ks, lane);
     const int ws = TILED ? 1024 : 64, ss = TILED ? 64 : 4;
     const int LS = lds_stride(K);
     uint8_t* lds_s = smem + (size_t)a.lds_rows * LS;
     // the lo term's staged rows and bytes start lo_off bytes further (16-byte aligned)
     const int lo_off = (a.lds_rows * (LS + Ks) + 15) & ~15;
-    const bool two = TERMS == 2 && __builtin_amdgcn_readfirstlane(*a.lo_flag) != 0;
 
-    const int PW = B_LDS ? a.lds_rows : 16;   // pairs per pass: never more rows than the LDS holds
+    const int PW = B_LDS ? a.lds_rows : 16;   // pairs per pass: never more rows than the LDS holds (TERMS == 2: <= 8)
+    const int pc = TERMS == 2 ? (col & 7) : col;         // the lane's pair column in the pass
+    const int term_off = TERMS == 2 && col >= 8 ? lo_off : 0;   // and its term (TERMS == 2: columns 8-15 read the lo rows)
     v4i A[PF];
     int SA[PF];
     v4i B0[B_LDS ? 1 : PF], B1[B_LDS ? 1 : PF];
     int SB[B_LDS ? 1 : PF];
     for (int base = p0; base < p1; base += PW) {
         const int mp = min(PW, p1 - base);
-        const int brow = col < mp ? col : 0;
+        const int brow = pc < mp ? pc : 0;
         // a pair whose token row is outside [0, x_rows) reads row 0 here and stores zeros below (global B path);
         // the LDS path stages a zero row for it
         const int tk = a.pair_tok[base + brow];
         const bool tok_ok = tk >= 0 && tk < a.x_rows;
-        const uint8_t* xg = a.xc + (long long)(tok_ok ? tk : 0) * a.ldx + kb * 16;
-        const uint8_t* xsg = a.xs + (long long)(tok_ok ? tk : 0) * a.ldxs + kb;
-        const uint8_t* xl = smem + brow * LS + kb * 16;
-        const uint8_t* xsl = lds_s + brow * Ks + kb;
+        // the global path's activation rows through buffer descriptors too (x_rows * ldx < 2^32 - 16, checked by the entry)
+        const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.xc, B_LDS ? 0u : (uint32_t)((long long)a.x_rows * a.ldx));
+        const __amdgpu_buffer_rsrc_t xsr = buffer_rsrc(a.xs, B_LDS ? 0u : (uint32_t)((long long)a.x_rows * a.ldxs));
+        const uint32_t xvo = (uint32_t)((long long)(tok_ok ? tk : 0) * a.ldx + kb * 16);
+        const uint32_t xsvo = (uint32_t)((long long)(tok_ok ? tk : 0) * a.ldxs + kb);
+        const uint8_t* xl = smem + term_off + brow * LS + kb * 16;
+        const uint8_t* xsl = lds_s + term_off + brow * Ks + kb;
         v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
         auto load = [&](int slot, int kc) {
-            A[slot] = load_weight_tile(wl + (long long)kc * ws);
-            SA[slot] = sl[(long long)kc * ss];
+            // the pipeline issues up to PF loads past the last k-chunk (unconditionally, so no slot register is a phi):
+            // they take the lane offset OOB with no scalar offset, past every descriptor's byte count (the entry bounds
+            // those below OOB), so they return zeros without a memory access; they are never consumed
+            const bool in = kc < nk;
+            const uint32_t k = in ? (uint32_t)kc : 0u;
+            A[slot] = buffer_load_tile(wr, in ? wvo : OOB, k * ws);
+            SA[slot] = buffer_load_byte(sr, in ? svo : OOB, k * ss);
             if (!B_LDS) {
-                B0[slot] = *(const v4i*)(xg + kc * 128);
-                B1[slot] = *(const v4i*)(xg + kc * 128 + 64);
-                SB[slot] = xsg[kc * 4];
+                const uint32_t xo = in ? xvo : OOB;
+                B0[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, k * 128, 0));
+                B1[slot] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, xo, k * 128 + 64, 0));
+                SB[slot] = buffer_load_byte(xsr, in ? xsvo : OOB, k * 4);
             }
         };
         auto use = [&](int slot) {
@@ -126,14 +144,9 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
                 const v4i b0 = *(const v4i*)(xl);
                 const v4i b1 = *(const v4i*)(xl + 64);
                 const int sb = *xsl;
-                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
-                if (two) {
-                    const v4i l0 = *(const v4i*)(xl + lo_off);
-                    const v4i l1 = *(const v4i*)(xl + lo_off + 64);
-                    acc = mfma_fp4w_fp8x(widen(A[slot]), join(l0, l1), acc, SA[slot], (int)xsl[lo_off]);
-                }
                 xl += 128;
                 xsl += 4;
+                acc = mfma_fp4w_fp8x(widen(A[slot]), join(b0, b1), acc, SA[slot], sb);
             } else {
                 acc = mfma_fp4w_fp8x(widen(A[slot]), join(B0[slot], B1[slot]), acc, SA[slot], SB[slot]);
             }
@@ -143,40 +156,57 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
         if (B_LDS) {
             __syncthreads();
             {
-                // stage rows base .. base+mp-1: codes as 16-byte vectors, then the E8M0 bytes
-                const int vpr = K >> 4;
-                for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
-                    const int r = i / vpr, v = i - r * vpr;
-                    const int t = a.pair_tok[base + r];
-                    *(v4i*)(smem + r * LS + v * 16) =
-                        (t >= 0 && t < a.x_rows) ? *(const v4i*)(a.xc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
-                }
-                for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
-                    const int r = i / Ks, v = i - r * Ks;
-                    const int t = a.pair_tok[base + r];
-                    lds_s[r * Ks + v] = (t >= 0 && t < a.x_rows) ? a.xs[(long long)t * a.ldxs + v] : (uint8_t)127;
-                }
-                if (two) {
-                    for (int i = threadIdx.x; i < mp * vpr; i += blockDim.x) {
+                // stage rows base .. base+mp-1, both terms: each thread issues all loads of a round (16-byte code vectors,
+                // 4-byte E8M0 words) before its first LDS store, so staging costs one memory round trip per round rather
+                // than one per array
+                const int vpr = K >> 4, wpr = K >> 7;   // code vectors and scale words per row (wpr <= vpr)
+                constexpr int U = 2;                     // items per thread per round
+                for (int i0 = threadIdx.x; i0 < mp * vpr; i0 += U * (int)blockDim.x) {
+                    v4i hv[U], lv[U];
+                    uint32_t hw[U], lw[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int i = i0 + u * (int)blockDim.x;
                         const int r = i / vpr, v = i - r * vpr;
-                        const int t = a.pair_tok[base + r];
-                        *(v4i*)(smem + lo_off + r * LS + v * 16) =
-                            (t >= 0 && t < a.x_rows) ? *(const v4i*)(a.xlc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
+                        const int t = i < mp * vpr ? a.pair_tok[base + r] : -1;
+                        const bool ok = t >= 0 && t < a.x_rows;
+                        hv[u] = ok ? *(const v4i*)(a.xc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
+                        if (TERMS == 2) lv[u] = ok ? *(const v4i*)(a.xlc + (long long)t * a.ldx + v * 16) : v4i{0, 0, 0, 0};
+                        const int rs = i / wpr, ws_ = i - rs * wpr;
+                        const int ts = i < mp * wpr ? a.pair_tok[base + rs] : -1;
+                        const bool oks = ts >= 0 && ts < a.x_rows;
+                        hw[u] = oks ? *(const uint32_t*)(a.xs + (long long)ts * a.ldxs + 4 * ws_) : 0x7F7F7F7Fu;
+                        if (TERMS == 2) lw[u] = oks ? *(const uint32_t*)(a.xls + (long long)ts * a.ldxs + 4 * ws_) : 0x7F7F7F7Fu;
                     }
-                    for (int i = threadIdx.x; i < mp * Ks; i += blockDim.x) {
-                        const int r = i / Ks, v = i - r * Ks;
-                        const int t = a.pair_tok[base + r];
-                        lds_s[lo_off + r * Ks + v] = (t >= 0 && t < a.x_rows) ? a.xls[(long long)t * a.ldxs + v] : (uint8_t)127;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int i = i0 + u * (int)blockDim.x;
+                        if (i < mp * vpr) {
+                            const int r = i / vpr, v = i - r * vpr;
+                            *(v4i*)(smem + r * LS + v * 16) = hv[u];
+                            if (TERMS == 2) *(v4i*)(smem + lo_off + r * LS + v * 16) = lv[u];
+                        }
+                        if (i < mp * wpr) {
+                            const int rs = i / wpr, ws_ = i - rs * wpr;
+                            *(uint32_t*)(lds_s + rs * Ks + 4 * ws_) = hw[u];
+                            if (TERMS == 2) *(uint32_t*)(lds_s + lo_off + rs * Ks + 4 * ws_) = lw[u];
+                        }
                     }
                 }
             }
             __syncthreads();
         }
         if (!active) continue;
-        pipeline_finish<PF>(nk, load, use);
+        pipeline_finish<PF, B_LDS != 0, true>(nk, load, use);
+        if (TERMS == 2) {   // pair column pc: its hi sum (lane pc) plus its lo sum (lane pc + 8)
+            acc.x += __shfl_xor(acc.x, 8);
+            acc.y += __shfl_xor(acc.y, 8);
+            acc.z += __shfl_xor(acc.z, 8);
+            acc.w += __shfl_xor(acc.w, 8);
+        }
         const long long orow = a.out_row ? (long long)a.out_row[base + brow] : (long long)(base + brow);
-        if (col < mp && orow >= 0 && orow < a.out_rows) {
-            const int q = base + col;
+        if ((TERMS == 1 || col < 8) && pc < mp && orow >= 0 && orow < a.out_rows) {
+            const int q = base + pc;
             const float f = a.pair_wt ? a.pair_wt[q] : 1.f;
             float* o = a.out + orow * a.ldo + row0;
             const v4f v = (B_LDS || tok_ok) ? acc * f : v4f{0.f, 0.f, 0.f, 0.f};
@@ -963,33 +993,37 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
     if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || G < 0 || ldo < N || ldx < K || ldxs < K / 32 || max_tokens < 1) return DSV41_EINVAL;
     if (accum < 0 || accum > 2 || (ldx & 15) || (((uintptr_t)xc) & 15) || x_rows < 0 || n_pairs < 0 || out_rows < 0 || shard_n < 0)
         return DSV41_EINVAL;
-    // the second term comes whole (codes, scales and its flag) or not at all
+    if ((long long)x_rows * ldx >= OOB || (long long)x_rows * ldxs >= OOB) return DSV41_EINVAL;   // 32-bit offsets, below OOB
+    if ((ldxs & 3) || (((uintptr_t)xs) & 3) || (((uintptr_t)xls) & 3)) return DSV41_EINVAL;         // scale rows read as words
+    // the second term comes whole (codes and scales; its flag optional) or not at all
     const int terms = xlc ? 2 : 1;
-    if ((xlc != nullptr) != (xls != nullptr) || (xlc != nullptr) != (lo_flag != nullptr) || (((uintptr_t)xlc) & 15)) return DSV41_EINVAL;
-    // every expert W holds has N rows of K / 2 weight bytes and K / 32 scale bytes
-    if (stride_we < (long long)N * (K / 2) || stride_se < (long long)N * (K / 32)) return DSV41_EINVAL;
+    if ((xlc != nullptr) != (xls != nullptr) || (lo_flag && !xlc) || (((uintptr_t)xlc) & 15)) return DSV41_EINVAL;
+    // every expert W holds has N rows of K / 2 weight bytes and K / 32 scale bytes, within 32-bit buffer offsets
+    if (stride_we < (long long)N * (K / 2) || stride_se < (long long)N * (K / 32) || stride_we >= OOB || stride_se >= OOB)
+        return DSV41_EINVAL;
     if (G == 0 || n_pairs == 0) return 0;
     GroupedArgs a{W, stride_we, S, stride_se, N, K, xc, ldx, xs, ldxs, x_rows, grp_expert, grp_start, pair_tok, n_pairs, out, ldo, out_rows,
-                  out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0, xlc, xls, lo_flag, nullptr};
+                  out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, 0, xlc, xls, nullptr};
     a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
     hipStream_t st = (hipStream_t)stream;
     const int rows = max_tokens < 16 ? max_tokens : 16;
     const size_t lds1 = (size_t)rows * (K + 16) + (size_t)rows * (K / 32);
-    const size_t lds2 = ((lds1 + 15) & ~(size_t)15) + lds1;
+    const int rows2 = rows < 8 ? rows : 8;   // two terms: passes of up to 8 pairs (hi and lo in one MFMA's 16 columns)
+    const size_t one2 = (size_t)rows2 * (K + 16) + (size_t)rows2 * (K / 32);
+    const size_t lds2 = ((one2 + 15) & ~(size_t)15) + one2;
     if (terms == 2 && lds2 <= B_LDS_MAX_BYTES) {
-        // both terms staged in LDS, one launch
-        a.lds_rows = rows;
+        // both terms staged in LDS, one launch (lo_flag is not needed)
+        a.lds_rows = rows2;
         launch_grouped_any(a, G, true, 2, lds2, st, tiled);
         return (int)hipGetLastError();
     }
     const bool use_lds = lds1 <= B_LDS_MAX_BYTES;
     a.lds_rows = use_lds ? rows : 0;
     a.xlc = a.xls = nullptr;
-    a.lo_flag = nullptr;
     launch_grouped_any(a, G, use_lds, 1, use_lds ? lds1 : 0, st, tiled);
     if (terms == 2) {
-        // the activation rows do not fit LDS twice: the lo term as a second pass that adds into the same outputs, which
-        // does nothing when no lo code is non-zero
+        // the activation rows do not fit LDS twice: the lo term as a second pass that adds into the same outputs; with
+        // lo_flag it does nothing when no lo code is non-zero
         GroupedArgs b = a;
         b.xc = xlc;
         b.xs = xls;

@@ -41,7 +41,7 @@ struct PrefillArgs {
     int g_pad;                                // G rounded up to a multiple of 8 (XCD remap)
     int n_pairs;                              // group ranges are clamped to [0, n_pairs)
     int cbw, n_it;                            // column blocks per workgroup, workgroups per group (ceil(n_cb / cbw))
-    const int* run_if;                        // MODE 2: the launch does nothing when *run_if == 0
+    const int* run_if;                        // MODE 2, optional: the launch does nothing when *run_if == 0
 };
 
 // ------------------------------------------------------------------------------------------ direct-to-LDS variant
@@ -457,7 +457,7 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
 
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_lds_kernel(const PrefillArgs a) {
-    if (MODE == 2 && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
+    if (MODE == 2 && a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     prefill_item128<MODE, TILED>(a, (int)blockIdx.x);
 }
 
@@ -802,7 +802,7 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
 // The prefill path's launch: each item takes the 256-pair tile when its group holds more than 128 pairs.
 template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_mixed_kernel(const PrefillArgs a) {
-    if (MODE == 2 && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
+    if (MODE == 2 && a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     const int L = (int)blockIdx.x;
     const int jx = L >> 3, g = (jx / a.n_it) * 8 + (L & 7);
     if (g >= a.G) return;
@@ -878,8 +878,8 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
 // The second FP8 term of off-grid activations (xlc / xls / lo_flag of dsv41_quant_fp8_split, all or none): checked like
 // the first, then run as a MODE 2 pass over the same groups that adds into the rows the first pass wrote.
 static bool lo_term_bad(const uint8_t* xc, const uint8_t* xlc, const uint8_t* xls, const int* lo_flag) {
-    return (xlc != nullptr) != (xls != nullptr) || (xlc != nullptr) != (lo_flag != nullptr) || (((uintptr_t)xlc) & 15) ||
-           (((uintptr_t)xls) & 3) || (xlc && xlc == xc);
+    return (xlc != nullptr) != (xls != nullptr) || (lo_flag && !xlc) || (((uintptr_t)xlc) & 15) || (((uintptr_t)xls) & 3) ||
+           (xlc && xlc == xc);
 }
 
 static int lo_pass(const PrefillArgs& a, const uint8_t* xlc, const uint8_t* xls, const int* lo_flag, int tiled, bool mixed, hipStream_t st) {

@@ -84,10 +84,11 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert grouped(N, K, we, se, out_rows=-1) == -1
     assert grouped(N, K, we, se, shard_n=-1) == -1
     assert grouped(N, K, we, se, n_pairs=0) == 0     # nothing to do: returns before any launch
-    # the second FP8 term comes whole (codes, scales, flag) and 16-byte aligned, or not at all
+    # the second FP8 term: codes and scales together (its flag optional, not without them), 16-byte aligned
     assert grouped(N, K, we, se, lo=(p, None, p)) == -1
-    assert grouped(N, K, we, se, lo=(p, p, None)) == -1
+    assert grouped(N, K, we, se, lo=(p, None, None)) == -1
     assert grouped(N, K, we, se, lo=(None, p, p)) == -1
+    assert grouped(N, K, we, se, lo=(None, None, p)) == -1
     assert grouped(N, K, we, se, lo=(ctypes.c_void_p(24), p, p)) == -1
     assert grouped(N, K, we, se, lo=(p, p, p), n_pairs=0) == 0
     # the split quantiser: K % 32, row stride % 8, alignment of x and of the code outputs, every output given
@@ -96,7 +97,6 @@ def test_bound_checks_reject_oversized_shapes_without_launch():
     assert L.dsv41_quant_fp8_split(q, 4, 64, 68, 0, q, q, q, q, q, None) == -1
     assert L.dsv41_quant_fp8_split(ctypes.c_void_p(40), 4, 64, 64, 0, q, q, q, q, q, None) == -1
     assert L.dsv41_quant_fp8_split(q, 4, 64, 64, 0, q, q, ctypes.c_void_p(40), q, q, None) == -1
-    assert L.dsv41_quant_fp8_split(q, 4, 64, 64, 0, q, q, q, q, None, None) == -1
 
     H, I = 7168, 1664
 
@@ -175,7 +175,7 @@ def test_grouped_scatter_rejects_invalid_calls_without_launch():
     assert call(y2=None) == -1
     assert call(y2=ctypes.c_void_p(20)) == -1
     assert call(G=65536) == -1
-    assert call(lo=(p, p, None)) == -1
+    assert call(lo=(None, None, p)) == -1
     assert call(lo=(p, None, p)) == -1
     assert call(lo=(ctypes.c_void_p(24), p, p)) == -1
     assert call(lo=(ctypes.c_void_p(48), ctypes.c_void_p(50), p)) == -1   # lo scales not 4-byte aligned
