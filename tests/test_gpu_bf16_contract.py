@@ -22,6 +22,12 @@ from test_gpu_moe import DEV, bf16_vals, close
 pytestmark = pytest.mark.gpu
 
 
+def fp8_operand_values(codes: torch.Tensor, scales: torch.Tensor) -> np.ndarray:
+    """The values an FP8 operand (E4M3 codes [rows, K], E8M0 bytes [rows, K/32]) stands for, fp32 (exact)."""
+    v = O.e4m3_decode(codes.cpu().numpy()).astype(np.float64) * np.repeat(O.e8m0_to_f32(scales.cpu().numpy()), 32, axis=1)
+    return v.astype(np.float32)
+
+
 def ref_max_rel(got: torch.Tensor, ref: torch.Tensor) -> float:
     """The reference tests' metric (test_moe.py:28, test_fp4_tcw.py:67)."""
     return float((got.double() - ref).abs().max() / ref.abs().max())
@@ -135,6 +141,58 @@ def test_fp8_grid_input_is_bit_identical_to_one_term():
         else:
             hipkern.grouped_gemm_codes(xc, xs, wt_, st_, ge, gs, tok, one, max(sizes), True, n_pairs=P)
         assert torch.equal(got, one), name
+
+
+def test_swiglu_result_carries_its_fp8_operand():
+    """fused.swiglu_quant writes the FP8 codes and E8M0 bytes of its result in the same launch and records them on the
+    result: they equal the split quantiser's hi term of the result (lo codes all zero, flag 0) in both store orders.
+    The surfaces given the result -- fp4_gemm_tc on the permuted one (one group per pair, and each mechanism's groups),
+    fp4_gemv_pairs and grouped_fp4_gemm on the natural one -- return bit for bit what they return for an unrecorded
+    copy (which they quantise). An in-place change drops the record, and the surfaces follow the new values."""
+    from dsv41_amd import fused, hipkern, moe_kernels, quant
+    w, s, wt_, st_, E, N, K = _mechanism_setup(91)
+    P = 128
+    g = torch.Generator(device=DEV).manual_seed(92)
+    gu = torch.randn(P, 2 * K, generator=g, device=DEV) * 2
+    wts = torch.rand(P, generator=g, device=DEV)
+    rng = np.random.default_rng(93)
+    t = lambda a: torch.from_numpy(np.asarray(a, np.int32)).to(DEV)
+    h = {}
+    for permute in (True, False):
+        h[permute] = fused.swiglu_quant(gu, wts, K, 7.0, permute=permute)
+        rec = quant.attached_codes(h[permute], permute)
+        assert rec is not None and quant.attached_codes(h[permute], not permute) is None
+        hv = bf16_vals(h[permute])
+        if permute:
+            hv = O.unpermute_x(hv)
+        for c_, s_ in (rec, quant.quant_fp8_split(h[permute], permuted=permute)[:2]):
+            assert np.array_equal(fp8_operand_values(c_, s_), hv), f"permute={permute}"
+        # (the codes themselves may differ from the quantiser's: where fq8 rounded a group's amax down to
+        # 448 x 2^(e-1), quantising the result again picks the scale one lower -- same values, other codes)
+        _, _, lc, ls, f = quant.quant_fp8_split(h[permute], permuted=permute)
+        assert int(f) == 0 and not bool(lc.any())
+    hp, hn = h[True], h[False]
+    # decode form: one group per pair, pair p reads row p
+    ex = t(rng.integers(0, E, 8))
+    rows, starts = t(np.arange(8)), t(np.arange(9))
+    assert torch.equal(hipkern.fp4_gemm_tc(hp, wt_, st_, ex, starts, rows, 8, 1, zero_out=True),
+                       hipkern.fp4_gemm_tc(hp.clone(), wt_, st_, ex, starts, rows, 8, 1, zero_out=True)), "fp4_gemm_tc decode"
+    for name, sizes in MECHANISMS.items():
+        ge, gs, tok, n = _groups(rng, sizes, E, P)
+        assert torch.equal(hipkern.fp4_gemm_tc(hp, wt_, st_, ge, gs, tok, n, max(sizes)),
+                           hipkern.fp4_gemm_tc(hp.clone(), wt_, st_, ge, gs, tok, n, max(sizes))), name
+    ones = torch.ones(P, device=DEV)
+    eid = t(rng.integers(0, E, P))
+    pr = t(np.arange(P))
+    assert torch.equal(hipkern.fp4_gemv_pairs(hn, w, s, pr, eid, ones, P), hipkern.fp4_gemv_pairs(hn.clone(), w, s, pr, eid, ones, P))
+    for block_m in (16, 64):
+        got = moe_kernels.grouped_fp4_gemm(hn, wt_, st_, moe_kernels.GroupedPairs(eid, pr, pr, wts, block_m, n_experts=E), P, tiled=True)
+        want = moe_kernels.grouped_fp4_gemm(hn.clone(), wt_, st_, moe_kernels.GroupedPairs(eid, pr, pr, wts, block_m, n_experts=E), P,
+                                            tiled=True)
+        assert torch.equal(got, want), f"grouped_fp4_gemm block_m={block_m}"
+    hn.mul_(1.5)                                  # off the FP8 grid in places: the surfaces quantise it again
+    assert quant.attached_codes(hn, False) is None
+    assert torch.equal(hipkern.fp4_gemv_pairs(hn, w, s, pr, eid, ones, P), hipkern.fp4_gemv_pairs(hn.clone(), w, s, pr, eid, ones, P))
 
 
 def test_off_grid_input_on_each_mechanism():

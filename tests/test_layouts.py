@@ -18,3 +18,23 @@ def test_tile_bf16_index_formula_and_round_trip():
         assert flat[off] == src[n, k]
     assert torch.equal(quant.untile_bf16(t).view(torch.int16), src)
     assert torch.equal(quant.untile_bf16(quant.tile_bf16(w)), w)
+
+
+def test_attached_codes_follow_the_tensor_version():
+    """The FP8 operand recorded on a tensor (quant.attach_codes) is returned for the recorded k order only, and is
+    dropped by any in-place change of the tensor, through itself or through a view; views and copies carry none."""
+    x = torch.randn(4, 64).to(torch.bfloat16)
+    codes = torch.zeros(4, 64, dtype=torch.uint8)
+    scales = torch.zeros(4, 2, dtype=torch.uint8)
+    assert quant.attached_codes(x, False) is None
+    quant.attach_codes(x, codes, scales, permuted=True)
+    got = quant.attached_codes(x, True)
+    assert got is not None and got[0] is codes and got[1] is scales
+    assert quant.attached_codes(x, False) is None
+    assert quant.attached_codes(x[1:], True) is None and quant.attached_codes(x.clone(), True) is None
+    x[1:].mul_(2)
+    assert quant.attached_codes(x, True) is None
+    quant.attach_codes(x, codes, scales)
+    assert quant.attached_codes(x, False) is not None
+    x.add_(1)
+    assert quant.attached_codes(x, False) is None
