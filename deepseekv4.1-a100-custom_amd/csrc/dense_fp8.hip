@@ -276,27 +276,43 @@ extern "C" int dsv41_fp8_gemm(const uint8_t* W, long long ldw, int tiled, const 
     const long long G = group_cols ? N / group_cols : 1;
     Fp8Args a{W, ldw, S, lds, N, K, K / 64, x, ldx, ldx * G, M, group_cols, out, ldo, outb, ldob};
     hipStream_t st = (hipStream_t)stream;
-    // up to 4 tokens whose activations fit 64 KiB of LDS per workgroup: the LDS-staged kernel, with 4 waves per
-    // workgroup when there are enough row blocks (measured fastest: 32768 x 1280 in 10.7 us against 19.0 us with 8),
-    // 8 when 4 waves would need too much LDS, and 16 for few row blocks with long rows
+    // up to 4 tokens whose activations fit 64 KiB of LDS per workgroup: the LDS-staged kernel. Launch shapes, measured
+    // at one token over resident copies larger than the 256 MB last-level cache (median of 50 graph replays):
+    //  * >= 256 row blocks: 4 waves per workgroup, 4 weight tiles in flight per wave (5120 x 8192: 9.5 us; 12 in flight
+    //    10.9, 24 12.1, 8 waves 10.7-11.0, 16 waves 12.2-13.1); rows of <= 24 chunks (K <= 1536) 2 waves, each with
+    //    more of the row (32768 x 1280: 9.2 us against 10.1 with 4 waves);
+    //  * fewer row blocks: 4 waves with 10 tiles in flight (1280 x 5120: 5.0 us against 5.9 with 16 waves).
+    // Deeper prefetch was slower for every shape with more row blocks than CUs.
     const int nb = (N + 15) / 16;
-    const int cand[2] = {nb < 256 && a.nk >= 64 ? 16 : 4, nb < 256 && a.nk >= 64 ? 16 : 8};
-    for (int c = 0; c < 2 && M <= 4; ++c) {
-        const int wpg = cand[c];
-        const int cpw = (a.nk + wpg - 1) / wpg;
-        const long long lds_bytes = (long long)wpg * fp8_lds_region(M, cpw);
-        // every wave owns >= 1 chunk; activation pieces and scale bytes fit the per-lane staging registers
-        if (a.nk < wpg || M * cpw > 64 || 2 * cpw > 128 || lds_bytes > 65536) continue;
+    const int wpg = nb >= 256 && a.nk <= 24 ? 2 : 4;
+    const int cpw = (a.nk + wpg - 1) / wpg;
+    const long long lds_bytes = (long long)wpg * fp8_lds_region(M, cpw);
+    // every wave owns >= 1 chunk; activation pieces and scale bytes fit the per-lane staging registers
+    if (M <= 4 && a.nk >= wpg && M * cpw <= 64 && 2 * cpw <= 128 && lds_bytes <= 65536) {
         const dim3 grid(nb);
-        if (wpg == 16) {
-            if (tiled) fp8_gemv_lds_kernel<16, 12, 1><<<grid, 1024, lds_bytes, st>>>(a, cpw);
-            else fp8_gemv_lds_kernel<16, 12, 0><<<grid, 1024, lds_bytes, st>>>(a, cpw);
-        } else if (wpg == 8) {
-            if (tiled) fp8_gemv_lds_kernel<8, 12, 1><<<grid, 512, lds_bytes, st>>>(a, cpw);
-            else fp8_gemv_lds_kernel<8, 12, 0><<<grid, 512, lds_bytes, st>>>(a, cpw);
+        if (wpg == 2) {
+            if (tiled) fp8_gemv_lds_kernel<2, 4, 1><<<grid, 128, lds_bytes, st>>>(a, cpw);
+            else fp8_gemv_lds_kernel<2, 4, 0><<<grid, 128, lds_bytes, st>>>(a, cpw);
+        } else if (nb >= 256) {
+            if (tiled) fp8_gemv_lds_kernel<4, 4, 1><<<grid, 256, lds_bytes, st>>>(a, cpw);
+            else fp8_gemv_lds_kernel<4, 4, 0><<<grid, 256, lds_bytes, st>>>(a, cpw);
         } else {
-            if (tiled) fp8_gemv_lds_kernel<4, 12, 1><<<grid, 256, lds_bytes, st>>>(a, cpw);
-            else fp8_gemv_lds_kernel<4, 12, 0><<<grid, 256, lds_bytes, st>>>(a, cpw);
+            if (tiled) fp8_gemv_lds_kernel<4, 10, 1><<<grid, 256, lds_bytes, st>>>(a, cpw);
+            else fp8_gemv_lds_kernel<4, 10, 0><<<grid, 256, lds_bytes, st>>>(a, cpw);
+        }
+        return (int)hipGetLastError();
+    }
+    // more tokens x chunks than 4 waves can stage: 8 waves (16 for few row blocks with long rows), 12 tiles in flight
+    const int wpg2 = nb < 256 && a.nk >= 64 ? 16 : 8, cpw2 = (a.nk + wpg2 - 1) / wpg2;
+    const long long lds2 = (long long)wpg2 * fp8_lds_region(M, cpw2);
+    if (M <= 4 && a.nk >= wpg2 && M * cpw2 <= 64 && 2 * cpw2 <= 128 && lds2 <= 65536) {
+        const dim3 grid(nb);
+        if (wpg2 == 16) {
+            if (tiled) fp8_gemv_lds_kernel<16, 12, 1><<<grid, 1024, lds2, st>>>(a, cpw2);
+            else fp8_gemv_lds_kernel<16, 12, 0><<<grid, 1024, lds2, st>>>(a, cpw2);
+        } else {
+            if (tiled) fp8_gemv_lds_kernel<8, 12, 1><<<grid, 512, lds2, st>>>(a, cpw2);
+            else fp8_gemv_lds_kernel<8, 12, 0><<<grid, 512, lds2, st>>>(a, cpw2);
         }
         return (int)hipGetLastError();
     }

@@ -261,7 +261,7 @@ struct DownSumArgs {
 #define DS_SHC8 5        // SH == 2 (FP8): its 64-k chunks per wave (K / 64 <= 8 DS_SHC8)
 #define DS_HS_SH 2
 #ifndef DS_PF_SH
-#define DS_PF_SH 12      // SH: weight tiles in flight per wave
+#define DS_PF_SH 4       // SH: weight tiles in flight per wave (12: the bf16 shared-expert layer 2.2 us slower, FP8 1.9)
 #endif
 #define DS_SCG 2         // SCL: groups per wave whose weight scales are staged in LDS
 #define DS_SCW 2048      // SCL: LDS bytes per wave for them (<= 32 k-chunks of 64 bytes)
@@ -1103,7 +1103,9 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
         return (int)hipGetLastError();
     }
 #undef DS_LAUNCH_SH
-    if (scl) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 1); else DS_LAUNCH(0, 12, 0, 1, 1); }
+    // weight tiles in flight per wave, measured at configs[1] (one token, 8 groups): 4 -> down launch 11.5 us, 12 -> 12.0,
+    // 2 -> 12.2; M = 4 (h rows in LDS, 32 groups) keeps 12 (4 in flight: 103.1 against 101.3 us per layer)
+    if (scl) { if (tiled) DS_LAUNCH(1, 4, 0, 1, 1); else DS_LAUNCH(0, 4, 0, 1, 1); }
     else if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 0); else DS_LAUNCH(0, 12, 0, 1, 0); }
     else if (gs) { if (tiled) DS_LAUNCH(1, 6, 0, 0, 2); else DS_LAUNCH(0, 6, 0, 0, 2); }
     else { if (tiled) DS_LAUNCH(1, 8, 0, 0, 0); else DS_LAUNCH(0, 8, 0, 0, 0); }
