@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--surfaces-only", action="store_true", help="only the reference-shaped drop-in surfaces (for profiling their kernels)")
     ap.add_argument("--shared-only", choices=["bf16", "fp8"], default=None,
                     help="only the configs[1] layer with its shared expert fused into the decode launches (for profiling them)")
+    ap.add_argument("--fp8-only", action="store_true", help="only the FP8 dense GEMV at the reference's test shapes (for profiling it)")
+    ap.add_argument("--fp8-rows", type=int, default=1, help="token rows of --fp8-only (1: the GEMV; 5..64: fp8_gemm_kernel)")
     ap.add_argument("--mfma-rate", action="store_true", help="only the MFMA issue-rate probe (block-scaled 16x16x128, three operand "
                     "mixes): the attainable matrix rate the prefill kernels are measured against")
     ap.add_argument("--stream-probe", action="store_true", help="only the HBM stream-rate probe: the decode byte volumes read in "
@@ -472,10 +474,10 @@ def bench_gemv_gpu(torch, dev, steps, warmup):
 FP8_SHAPES = [(5120, 8192), (4608, 5120), (32768, 1280), (1280, 5120), (5120, 2304)]   # test_fp8_tc.py:19 (V4.1 dims)
 
 
-def bench_fp8_dense(torch, dev, steps, warmup):
-    """The FP8 dense-weight GEMV (w8.linear_w on a W8 weight, one token) at the reference's own test shapes, each over
-    enough resident copies to exceed the 256 MB Infinity Cache, against torch's bf16 F.linear (hipBLASLt) on bf16
-    copies of the same shape. Bytes: the FP8 weights plus their E8M0 scales."""
+def bench_fp8_dense(torch, dev, steps, warmup, rows=1, with_bf16=True):
+    """The FP8 dense-weight GEMV (w8.linear_w on a W8 weight, `rows` tokens, one by default) at the reference's own
+    test shapes, each over enough resident copies to exceed the 256 MB Infinity Cache, against torch's bf16 F.linear
+    (hipBLASLt) on bf16 copies of the same shape. Bytes: the FP8 weights plus their E8M0 scales."""
     from dsv41_amd import w8
     out = {}
     g = torch.Generator(device=dev).manual_seed(17)
@@ -483,13 +485,16 @@ def bench_fp8_dense(torch, dev, steps, warmup):
         copies = max(2, int(600e6 // (N * Kd)) + 1)
         Ws = [w8.W8(torch.randint(0, 256, (N, Kd), generator=g, dtype=torch.uint8, device=dev) & 0x7E,
                     torch.randint(115, 130, (N // 32, Kd // 32), generator=g, dtype=torch.uint8, device=dev)) for _ in range(copies)]
-        x = torch.randn(1, Kd, generator=g, device=dev).to(torch.bfloat16)
+        x = torch.randn(rows, Kd, generator=g, device=dev).to(torch.bfloat16)
         t8, _ = graph_time(torch, lambda i: w8.linear_w(x, Ws[i % copies]), max(steps, copies), warmup)
         del Ws
+        nbytes = N * Kd + (N // 32) * (Kd // 32)
+        if not with_bf16:
+            out[f"{N}x{Kd}"] = {"us": round(t8 * 1e6, 2), "GBps": round(nbytes / t8 / 1e9, 1)}
+            continue
         Wb = [torch.randn(N, Kd, generator=g, device=dev).to(torch.bfloat16) for _ in range(max(2, copies // 2))]
         tb, _ = graph_time(torch, lambda i: torch.nn.functional.linear(x, Wb[i % len(Wb)]), max(steps, len(Wb)), warmup)
         del Wb
-        nbytes = N * Kd + (N // 32) * (Kd // 32)
         out[f"{N}x{Kd}"] = {"us": round(t8 * 1e6, 2), "GBps": round(nbytes / t8 / 1e9, 1),
                             "bf16_linear_us": round(tb * 1e6, 2), "speedup_vs_bf16": round(tb / t8, 2)}
         torch.cuda.empty_cache()
@@ -726,6 +731,10 @@ def main():
         return
     if args.stream_probe:
         print(json.dumps({"stream_probe": stream_probe(torch, dev)}))
+        return
+    if args.fp8_only:
+        print(json.dumps({"workload": f"FP8 dense weights x {args.fp8_rows} bf16 row(s), the reference's test shapes",
+                          "fp8_dense": bench_fp8_dense(torch, dev, K, W, rows=args.fp8_rows, with_bf16=False)}))
         return
     if args.prefill_only:
         layers = make_layers(torch, dev, 1, 1000)
