@@ -193,6 +193,11 @@ def test_swiglu_result_carries_its_fp8_operand():
     hn.mul_(1.5)                                  # off the FP8 grid in places: the surfaces quantise it again
     assert quant.attached_codes(hn, False) is None
     assert torch.equal(hipkern.fp4_gemv_pairs(hn, w, s, pr, eid, ones, P), hipkern.fp4_gemv_pairs(hn.clone(), w, s, pr, eid, ones, P))
+    with torch.inference_mode():                  # no version counter: no record, the surfaces quantise as usual
+        hi = fused.swiglu_quant(gu, wts, K, 7.0)
+        assert quant.attached_codes(hi, False) is None
+        got = hipkern.fp4_gemv_pairs(hi, w, s, pr, eid, ones, P)
+    assert torch.equal(got, hipkern.fp4_gemv_pairs(fused.swiglu_quant(gu, wts, K, 7.0), w, s, pr, eid, ones, P))
 
 
 def test_off_grid_input_on_each_mechanism():

@@ -38,3 +38,15 @@ def test_attached_codes_follow_the_tensor_version():
     assert quant.attached_codes(x, False) is not None
     x.add_(1)
     assert quant.attached_codes(x, False) is None
+
+
+def test_inference_tensors_carry_no_record():
+    """Tensors made in inference mode keep no version counter: attach_codes leaves them unrecorded (the surfaces then
+    quantise them as any input) instead of failing."""
+    codes = torch.zeros(2, 64, dtype=torch.uint8)
+    scales = torch.zeros(2, 2, dtype=torch.uint8)
+    with torch.inference_mode():
+        x = torch.randn(2, 64).to(torch.bfloat16)
+        assert quant.attach_codes(x, codes, scales) is x
+        assert quant.attached_codes(x, False) is None
+    assert quant.attached_codes(x, False) is None
