@@ -167,6 +167,77 @@ __global__ void __launch_bounds__(256) quant_fp8_split_kernel(const uint16_t* __
     if (lo_flag && any && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(any)) *(volatile int*)lo_flag = 1;
 }
 
+// inputs of at most this many 16-value chunks (262,144 values: 36 rows of 7168) take the 4-value-per-lane kernels
+#define SMALL_CHUNKS 16384
+
+// Small inputs (decode rows): the same split with 4 values per lane and a 32-group on 8 adjacent lanes. At one row of
+// 7168 values the 16-value form runs 448 lanes through a serial chain of 16 encodings (two terms); this one runs 1792
+// lanes through 4, which is what the launch's latency is made of at that size. Bit-identical to the 16-value form.
+// permuted: the input holds 8-k permuted positions; lane pair (2m, 2m + 1) holds positions 8 m' .. 8 m' + 7 of one
+// 8-block, and natural column j of the block sits at position (j & ~7) | bitrev3(j & 7), so each lane takes two of its
+// values from the other lane of the pair.
+__device__ __forceinline__ void unpermute_quad(float (&v)[4], bool odd) {
+    // even lane: columns 0..3 = positions 0, 4, 2, 6 (own 0, pair 0, own 2, pair 2); odd lane: columns 4..7 =
+    // positions 1, 5, 3, 7 (pair 1, own 1, pair 3, own 3)
+    const float r0 = __shfl_xor(odd ? v[0] : v[1], 1), r1 = __shfl_xor(odd ? v[2] : v[3], 1);
+    if (odd) {
+        v[0] = r0;
+        v[2] = r1;
+    } else {
+        v[1] = r0;
+        v[3] = r1;
+    }
+}
+
+__global__ void __launch_bounds__(256) quant_fp8_split_q4_kernel(const uint16_t* __restrict__ x, unsigned n_quads, int K, long long ldx,
+                                                                 int permuted, uint8_t* __restrict__ hc, uint8_t* __restrict__ hs,
+                                                                 uint8_t* __restrict__ lc, uint8_t* __restrict__ ls, int* lo_flag) {
+    const unsigned t = blockIdx.x * 256u + threadIdx.x;   // 4-value quad; a 32-group's 8 quads are 8 aligned lanes
+    bool nz = false;
+    if (t < n_quads) {                                    // n_quads is a multiple of 8: a group's lanes are active together
+        const unsigned qpr = (unsigned)K >> 2;
+        const unsigned r = t / qpr, q = t - r * qpr;
+        const int k0 = (int)q * 4;
+        const uint2 w = *(const uint2*)(x + (long long)r * ldx + k0);
+        float v[4] = {bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xFFFFu), bf16_to_f32(w.y >> 16)};
+        if (permuted) unpermute_quad(v, (q & 1) != 0);
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+        const int e = fq8_exponent(amax);
+        uint32_t cw = 0, cw2 = 0;
+        float rr[4], rmax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = fq8_code(v[j], e);
+            cw |= c << (8 * j);
+            rr[j] = __fsub_rn(v[j], fq8_value(c, e));   // the residual, exact
+            rmax = fmaxf(rmax, fabsf(rr[j]));
+        }
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 8));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 8));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 8));
+        const int e2 = lo_exponent(rmax);
+        uint32_t any = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c2 = fq8_code(rr[j], e2);
+            any |= c2 & 0x7Fu;
+            cw2 |= c2 << (8 * j);
+        }
+        nz = any != 0;
+        *(uint32_t*)(hc + (long long)r * K + k0) = cw;
+        *(uint32_t*)(lc + (long long)r * K + k0) = cw2;
+        if ((q & 7) == 0) {
+            hs[(long long)r * (K >> 5) + (q >> 3)] = (uint8_t)(e + 127);
+            ls[(long long)r * (K >> 5) + (q >> 3)] = (uint8_t)(e2 + 127);
+        }
+    }
+    const unsigned long long any = __ballot(nz);
+    if (lo_flag && any && (threadIdx.x & 63) == (unsigned)__builtin_ctzll(any)) *(volatile int*)lo_flag = 1;
+}
+
 __global__ void clear_flag_kernel(int* flag) {
     if (threadIdx.x == 0) *(volatile int*)flag = 0;
 }
@@ -291,6 +362,62 @@ __global__ void __launch_bounds__(256) swiglu_quant_vec_kernel(const void* __res
     }
 }
 
+// Small inputs (decode rows): the same SwiGLU epilogue with 4 columns per lane and a 32-column group on 8 adjacent
+// lanes (a serial chain of 4 exp / divide / encode steps per lane instead of 16). Bit-identical to the 16-column form.
+// permute: the bf16 values go out 8-k permuted; the column <-> position map is its own inverse, so the lane pair
+// exchanges values as unpermute_quad does.
+__global__ void __launch_bounds__(256) swiglu_quant_q4_kernel(const void* __restrict__ gu, int gu_bf16, long long ld_gu, const float* __restrict__ wt,
+                                                              unsigned n_quads, int inter, float limit, uint8_t* __restrict__ codes,
+                                                              uint8_t* __restrict__ scales, uint16_t* __restrict__ hb, int permute) {
+    const unsigned t = blockIdx.x * 256u + threadIdx.x;   // 4-column quad; a 32-group's 8 quads are 8 aligned lanes
+    if (t >= n_quads) return;                             // n_quads is a multiple of 8: whole groups leave together
+    const unsigned qpr = (unsigned)inter >> 2;
+    const unsigned r = t / qpr, q = t - r * qpr;
+    const int c0 = (int)q * 4;
+    float g[4], u[4];
+    const long long og = (long long)r * ld_gu + c0, ou = og + inter;
+    if (!gu_bf16) {
+        const v4f a = *(const v4f*)((const float*)gu + og), b = *(const v4f*)((const float*)gu + ou);
+        g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+        u[0] = b.x; u[1] = b.y; u[2] = b.z; u[3] = b.w;
+    } else {
+        const uint2 a = *(const uint2*)((const uint16_t*)gu + og), b = *(const uint2*)((const uint16_t*)gu + ou);
+        g[0] = bf16_to_f32(a.x & 0xFFFFu); g[1] = bf16_to_f32(a.x >> 16); g[2] = bf16_to_f32(a.y & 0xFFFFu); g[3] = bf16_to_f32(a.y >> 16);
+        u[0] = bf16_to_f32(b.x & 0xFFFFu); u[1] = bf16_to_f32(b.x >> 16); u[2] = bf16_to_f32(b.y & 0xFFFFu); u[3] = bf16_to_f32(b.y >> 16);
+    }
+    const float w = wt ? wt[r] : 1.f;
+    float h[4];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float gg = g[i], uu = u[i];
+        if (limit > 0.f) {
+            uu = fminf(fmaxf(uu, -limit), limit);
+            gg = fminf(gg, limit);
+        }
+        float v = gg * (1.0f / (1.0f + expf(-gg))) * uu;
+        if (wt) v = v * w;
+        v = bf16_round(v);
+        h[i] = v;
+        amax = fmaxf(amax, fabsf(v));
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+    const int e = fq8_exponent(amax);
+    uint32_t qc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qc[i] = fq8_code(h[i], e);
+    if (codes) *(uint32_t*)(codes + (long long)r * inter + c0) = qc[0] | (qc[1] << 8) | (qc[2] << 16) | (qc[3] << 24);
+    if (scales && (q & 7) == 0) scales[(long long)r * (inter >> 5) + (q >> 3)] = (uint8_t)(e + 127);
+    if (hb) {
+        float o[4] = {fq8_value(qc[0], e), fq8_value(qc[1], e), fq8_value(qc[2], e), fq8_value(qc[3], e)};
+        if (permute) unpermute_quad(o, (q & 1) != 0);
+        *(uint2*)(hb + (long long)r * inter + c0) = uint2{f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16),
+                                                          f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16)};
+    }
+}
+
 // ------------------------------------------------------------------------------------------ C ABI
 extern "C" int dsv41_dequant_fp4(const uint8_t* w, const uint8_t* s, long long rows, int K, int tiled, uint16_t* out, void* stream) {
     if (!w || !s || !out || rows < 0 || K <= 0 || (K & 31) || (tiled && ((rows & 15) || (K & 127)))) return DSV41_EINVAL;
@@ -326,8 +453,12 @@ extern "C" int dsv41_quant_fp8_split(const uint16_t* x, long long rows, int K, l
     if (n >= (1ll << 31)) return DSV41_EINVAL;
     hipStream_t st = (hipStream_t)stream;
     if (lo_flag) clear_flag_kernel<<<1, 64, 0, st>>>(lo_flag);
-    if (n > 0)
+    if (n > 0 && n <= SMALL_CHUNKS) {   // decode rows: 4 values per lane
+        const unsigned nq = (unsigned)(4 * n);
+        quant_fp8_split_q4_kernel<<<(nq + 255) / 256, 256, 0, st>>>(x, nq, K, ldx, permuted, hc, hs, lc, ls, lo_flag);
+    } else if (n > 0) {
         quant_fp8_split_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(x, (unsigned)n, K, ldx, permuted, hc, hs, lc, ls, lo_flag);
+    }
     return (int)hipGetLastError();
 }
 
@@ -337,6 +468,13 @@ extern "C" int dsv41_swiglu_quant(const void* gu, int gu_bf16, long long ld_gu, 
     const long long groups = (long long)rows * (inter / 32);
     if (groups == 0) return 0;
     const int esz = gu_bf16 ? 2 : 4;
+    if (groups * 2 <= SMALL_CHUNKS && (((uintptr_t)gu) & 15) == 0 && (ld_gu & 3) == 0 && (((uintptr_t)codes) & 3) == 0 &&
+        (((uintptr_t)h_bf16) & 7) == 0) {   // decode rows: 4 columns per lane
+        const unsigned nq = (unsigned)(groups * 8);
+        swiglu_quant_q4_kernel<<<(nq + 255) / 256, 256, 0, (hipStream_t)stream>>>(gu, gu_bf16, ld_gu, wt, nq, inter, limit, codes, scales,
+                                                                                  h_bf16, permute);
+        return (int)hipGetLastError();
+    }
     const bool vec = groups * 2 < (1ll << 31) && (((uintptr_t)gu) & 15) == 0 && ((ld_gu * esz) & 15) == 0 && (((uintptr_t)codes) & 15) == 0 &&
                      (((uintptr_t)h_bf16) & 15) == 0;
     if (vec) {

@@ -96,6 +96,29 @@ def test_split_quantiser_equals_oracle():
 MECHANISMS = {"two-term LDS kernel": [4, 2, 3], "rows from global memory + lo pass": [16, 3, 9], "128-pair tile + MODE 2 pass": [64, 40, 17]}
 
 
+@pytest.mark.parametrize("permuted", [False, True])
+def test_split_quantiser_small_and_large_kernels_agree(permuted):
+    """The 4-value-per-lane split kernel (inputs of <= 262,144 values) and the 16-value one give the same four outputs
+    bit for bit (40 rows x 8192 on the 16-value kernel against its first 32 rows on the 4-value kernel), and the large
+    input equals the oracle too."""
+    from dsv41_amd import hipkern, quant
+    g = torch.Generator().manual_seed(73)
+    x = torch.randn(40, 8192, generator=g)
+    x[:8] *= 1e-3
+    x[8:16] *= 500.0
+    x = x.to(torch.bfloat16)
+    xd = x.to(DEV)
+    if permuted:
+        xd = hipkern.permute_x(xd)
+    big = quant.quant_fp8_split(xd, permuted=permuted)
+    small = quant.quant_fp8_split(xd[:32], permuted=permuted)
+    for b_, s_, name in zip(big[:4], small[:4], ("hi codes", "hi scales", "lo codes", "lo scales")):
+        assert torch.equal(b_[:32], s_), name
+    assert int(big[4]) == 1 and int(small[4]) == 1
+    for w_, g_, name in zip(O.fp8_split(bf16_vals(x)), big[:4], ("hi codes", "hi scales", "lo codes", "lo scales")):
+        assert np.array_equal(w_, g_.cpu().numpy()), name
+
+
 def _mechanism_setup(seed):
     from dsv41_amd import quant
     from test_gpu_moe import make_experts

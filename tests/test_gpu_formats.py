@@ -136,6 +136,30 @@ def test_swiglu_quant_vector_equals_per_element(bf16_in, weighted, permute):
     assert torch.equal(ca, cs) and torch.equal(sa, ss)
 
 
+@pytest.mark.parametrize("bf16_in,weighted,permute", [(False, True, False), (False, False, True), (True, True, True)])
+def test_swiglu_quant_three_kernels_agree(bf16_in, weighted, permute):
+    """The three SwiGLU kernels -- 4 columns per lane (inputs of <= 262,144 values: decode rows), 16 columns per lane
+    (larger aligned inputs) and one column per thread (misaligned rows) -- give the same bf16 values, codes and scales
+    bit for bit: 200 rows x 1664 on the 16-column kernel against its first 36 rows on the 4-column one and against a
+    misaligned copy on the per-element one."""
+    from dsv41_amd import fused
+    g = torch.Generator().manual_seed(8)
+    rows, inter, small = 200, 1664, 36
+    dt = torch.bfloat16 if bf16_in else torch.float32
+    vals = (torch.randn(rows, 2 * inter, generator=g) * 5).to(dt).to(DEV)
+    wt = torch.rand(rows, generator=g).to(DEV) if weighted else None
+    buf2 = torch.zeros(rows, 2 * inter + 8, dtype=dt, device=DEV)
+    buf2[:, 2:2 * inter + 2] = vals
+    shifted = buf2[:, 2:2 * inter + 2]
+    big = fused.swiglu_quant(vals, wt, inter, 10.0, permute=permute)
+    part = fused.swiglu_quant(vals[:small], wt[:small] if weighted else None, inter, 10.0, permute=permute)
+    assert torch.equal(big[:small], part)
+    assert torch.equal(big, fused.swiglu_quant(shifted, wt, inter, 10.0, permute=permute))
+    cb, sb = fused.swiglu_quant_codes(vals, wt, inter, 10.0)
+    cp, sp = fused.swiglu_quant_codes(vals[:small], wt[:small] if weighted else None, inter, 10.0)
+    assert torch.equal(cb[:small], cp) and torch.equal(sb[:small], sp)
+
+
 def test_swiglu_quant_bf16_input():
     """bf16 gate/up (the shared expert's linear output, fused.py:294): the same values as the fp32 path on the
     bf16 values, bit for bit."""
