@@ -666,7 +666,8 @@ def plain_read_us(torch, dev, buf, nbytes, blocks, waves, sync=0, steps=20):
 
 def stream_probe(torch, dev):
     """What a plain read of the decode byte volumes attains: the down projection's 50.7 MB, the up projection's 101.4 MB,
-    the layer's 152.1 MB and 1 GiB, each in several launch shapes (workgroups x waves), plain_read_us each. sync: a
+    the layer's 152.1 MB and 1 GiB, each in several launch shapes (workgroups x waves), plain_read_us each; and 96 MiB
+    read by 16 .. 512 workgroups (how fast part of the chip streams). sync: a
     workgroup barrier after every second tile, as the prefill kernels synchronise each k-step. fit: t = F + bytes / R by
     least squares over the four volumes for one shape."""
     import numpy as np
@@ -681,6 +682,12 @@ def stream_probe(torch, dev):
             key = f"{vname}_{blocks}x{waves}" + ("_sync" if sync else "")
             res["us"][key] = round(t * 1e6, 2)
             res["TBps"][key] = round(nb / t / 1e12, 3)
+    # part of the chip streaming: 96 MiB over 16 .. 512 workgroups of 8 waves (one per CU up to 256), the per-CU rate
+    # a kernel reaches when other CUs are busy with something else
+    for blocks in (16, 32, 64, 128, 192, 256, 512):
+        t = plain_read_us(torch, dev, buf, 96 << 20, blocks, 8, 0)
+        res["us"][f"cus_96MiB_{blocks}x8"] = round(t * 1e6, 2)
+        res["TBps"][f"cus_96MiB_{blocks}x8"] = round((96 << 20) / t / 1e12, 3)
     for blocks, waves in ((416, 8), (512, 8)):
         xs = np.array([float(v) for v in vols.values()])
         ys = np.array([res["us"][f"{k}_{blocks}x{waves}"] * 1e-6 for k in vols])
