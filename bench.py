@@ -123,7 +123,7 @@ def routing_stream(torch, dev, steps, M, seed):
     return torch.randn(steps, M, E, generator=g, device=dev)
 
 
-def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode="fused", seed=7):
+def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode="fused", seed=7, limit=LIMIT):
     """One decode layer per step over the rotating layer copies; shared: list of SharedExpert copies (bf16 or FP8),
     rotated with the layers, computed inside the two decode launches ("fused") or, bf16, as its own launches first
     ("separate"), or of (w8.W8 w13, w8.W8 w2) FP8 copies run as two FP8 GEMMs and a SwiGLU first ("fp8"). Returns
@@ -140,7 +140,7 @@ def bench_decode(torch, dev, layers, steps, warmup, M, shared=None, shared_mode=
 
     def step(i):
         ex = layers[i % len(layers)]
-        route = (xq, logits[i], None, 1.0, TOPK, 1.0, "softmax", True, ex, LIMIT)
+        route = (xq, logits[i], None, 1.0, TOPK, 1.0, "softmax", True, ex, limit)
         if shared is None:
             moe.moe_route_experts(*route, out=out, eid_out=eid[i], wt_out=wt[i])
         elif shared_mode == "fused":
@@ -814,6 +814,9 @@ def main():
                                          "the MFMAs and the reductions to two such reads"}
     progress(f"plain reads of the two volumes {(r_up + r_dn) * 1e6:.2f} us")
     if not args.quick:
+        # the same layer with the SwiGLU clamp disabled (swiglu_limit 0: the second setting configs[1] is run at)
+        t_nolim, _ = bench_decode(torch, dev, layers, K, W, 1, limit=0.0)
+        extra["layer_us_swiglu_limit_0"] = round(t_nolim * 1e6, 2)
         # the bf16 shared expert, one copy per layer copy (4 x 71.6 MB: with the routed bytes between two uses of a copy,
         # more than the 256 MB Infinity Cache holds)
         from dsv41_amd import moe
