@@ -250,20 +250,29 @@ __global__ void dequant_fp8_kernel(const uint8_t* __restrict__ W, long long ldw,
 }
 
 // ------------------------------------------------------------------------------------------ entry points
-template <int MT>
-static void fp8_launch(const Fp8Args& a, int tiled, hipStream_t st) {
-    constexpr int PF = MT == 1 ? 6 : MT == 2 ? 4 : 2;   // <= 128 VGPRs: two 8-wave workgroups per CU
-    const int nb = (a.N + 15) / 16;
-    const dim3 grid(nb);
-    // few row blocks: 16 waves per workgroup so the K split still fills the CUs (not for 4 token tiles, whose
-    // registers do not fit 16 waves per CU)
-    if (MT <= 2 && nb < 256 && a.nk >= 64) {
+template <int MT, int PF>
+static void fp8_launch_pf(const Fp8Args& a, int tiled, bool wide, hipStream_t st) {
+    const dim3 grid((a.N + 15) / 16);
+    if (wide) {
         if (tiled) fp8_gemm_kernel<16, PF, MT, 1><<<grid, 1024, 0, st>>>(a);
         else fp8_gemm_kernel<16, PF, MT, 0><<<grid, 1024, 0, st>>>(a);
     } else {
         if (tiled) fp8_gemm_kernel<8, PF, MT, 1><<<grid, 512, 0, st>>>(a);
         else fp8_gemm_kernel<8, PF, MT, 0><<<grid, 512, 0, st>>>(a);
     }
+}
+
+template <int MT>
+static void fp8_launch(const Fp8Args& a, int tiled, hipStream_t st) {
+    const int nb = (a.N + 15) / 16;
+    // few row blocks: 16 waves per workgroup so the K split still fills the CUs (not for 4 token tiles, whose
+    // registers do not fit 16 waves per CU)
+    const bool wide = MT <= 2 && nb < 256 && a.nk >= 64;
+    // <= 128 VGPRs: two 8-wave workgroups per CU. One token tile: 6 tiles in flight per wave, 3 when a wave has fewer
+    // than 6 chunks (measured at 16 / 8 rows: 32768 x 1280 17.9 -> 15.1 / 14.8 -> 11.0 us; the other reference shapes
+    // within 1 %, and 2 / 4 / 8 in flight no better)
+    if (MT == 1 && a.nk < 6 * (wide ? 16 : 8)) fp8_launch_pf<MT, 3>(a, tiled, wide, st);
+    else fp8_launch_pf<MT, MT == 1 ? 6 : MT == 2 ? 4 : 2>(a, tiled, wide, st);
 }
 
 extern "C" int dsv41_fp8_gemm(const uint8_t* W, long long ldw, int tiled, const uint8_t* S, long long lds, int N, int K,

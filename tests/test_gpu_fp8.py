@@ -100,6 +100,8 @@ SHAPES = [(1, 512, 5120, 0), (1, 1280, 5120, 0), (1, 32768, 1280, 0), (6, 5120, 
 # every launch shape of the <= 4-token LDS kernel: 2 waves (>= 256 row blocks, K <= 1536), 4 waves with 4 tiles in
 # flight (>= 256 row blocks), 4 waves with 10 (fewer), and the 8- and 16-wave fallbacks for 4 tokens at K = 8192
 SHAPES += [(2, 32768, 1280, 0), (1, 4608, 5120, 0), (3, 512, 5120, 0), (4, 5120, 8192, 0), (4, 1280, 8192, 0)]
+# and of the 5-16-row kernel with 3 tiles in flight (fewer than 6 chunks per wave): 8 and 16 waves per workgroup
+SHAPES += [(12, 32768, 1280, 0), (16, 5120, 2304, 0), (16, 1280, 5120, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,gc", SHAPES)
