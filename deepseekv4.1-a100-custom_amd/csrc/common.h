@@ -3,7 +3,8 @@
 // Formats (the reference's quant.py:6-110):
 //   E2M1 weights, two per byte along k, low nibble = even k; one E8M0 byte per (row, 32 k), value 2^(b-127).
 //   FP8 activations: E4M3 (float8_e4m3fn) codes with one E8M0 byte per 32 k (power-of-two scale).
-// Every rounding helper here is integer/bit based so results do not depend on the FP mode (denormal flush).
+// The rounding helpers are integer/bit based, or (FP8 encode and decode) the gfx950 conversion instructions checked
+// bit for bit against them, so results do not depend on the FP mode (denormal flush).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -90,14 +91,38 @@ __device__ __forceinline__ int fq8_exponent(float amax) {
     return (int)((u >> 23) & 0xFFu) - 127 + ((u & 0x7FFFFFu) != 0u ? 1 : 0);
 }
 
-// code of v at scale 2^e: RNE_e4m3(clamp(v / 2^e, +-448)); the division by a power of two is exact
-__device__ __forceinline__ uint32_t fq8_code(float v, int e) {
-    const float x = v * __uint_as_float((uint32_t)(127 - e) << 23);
-    return e4m3_encode(round_e4m3(fminf(fmaxf(x, -448.0f), 448.0f)));
+// v / 2^e clamped to +-448 (the division by a power of two is exact; a NaN v becomes -448, as fmaxf drops it)
+__device__ __forceinline__ float fq8_scaled(float v, int e) {
+    return fminf(fmaxf(v * __uint_as_float((uint32_t)(127 - e) << 23), -448.0f), 448.0f);
 }
+
+// code of v at scale 2^e: RNE_e4m3(clamp(v / 2^e, +-448)), by arithmetic on the bits
+__device__ __forceinline__ uint32_t fq8_code_sw(float v, int e) { return e4m3_encode(round_e4m3(fq8_scaled(v, e))); }
+
+// The same codes from the hardware conversion: v_cvt_pk_fp8_f32 rounds two fp32 values to nearest even on the
+// float8_e4m3fn grid (subnormals included) and packs them into bits 0-15 of a word (or 16-31 with hi). Every input
+// is clamped to +-448 first, so no conversion leaves the grid. Bit-identical with fq8_code_sw: the self-test entry
+// dsv41_selftest_fp8_cvt compares the two over every bf16 value, every rounding midpoint and random fp32 inputs.
+__device__ __forceinline__ uint32_t fq8_code2_hw(float a, float b, int e) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fq8_scaled(a, e), fq8_scaled(b, e), 0, false) & 0xFFFFu;
+}
+__device__ __forceinline__ uint32_t fq8_code4_hw(float a, float b, float c, float d, int e) {
+    const int w = __builtin_amdgcn_cvt_pk_fp8_f32(fq8_scaled(a, e), fq8_scaled(b, e), 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fq8_scaled(c, e), fq8_scaled(d, e), w, true);
+}
+__device__ __forceinline__ uint32_t fq8_code_hw(float v, int e) { return fq8_code2_hw(v, v, e) & 0xFFu; }
+
+__device__ __forceinline__ uint32_t fq8_code(float v, int e) { return fq8_code_hw(v, e); }
 
 __device__ __forceinline__ float fq8_value(uint32_t code, int e) {
     return e4m3_decode(code) * __uint_as_float((uint32_t)(127 + e) << 23);
+}
+
+// byte B of a word of E4M3 codes (a code fq8 produces: never the NaN codes 0x7F / 0xFF) as fp32, by the hardware
+// conversion (v_cvt_f32_fp8), times 2^e
+template <int B>
+__device__ __forceinline__ float fq8_value_hw(uint32_t word, int e) {
+    return __builtin_amdgcn_cvt_f32_fp8((int)word, B) * __uint_as_float((uint32_t)(127 + e) << 23);
 }
 
 // ------------------------------------------------------------------------------------------ two-term FP8 split
@@ -128,28 +153,33 @@ __device__ __forceinline__ bool fp8_split16(const v4i w0, const v4i w1, int perm
     for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(val(i)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 2));
     e = fq8_exponent(amax);
-    // codes are packed as they are made, in output (natural k) order: position j holds input position (j & ~7) |
-    // bitrev3(j & 7) when permuted; the residuals are kept in output order (only their amax depends on all of them)
-    float r[16];
-    uint32_t cw[4] = {0, 0, 0, 0}, cw2[4] = {0, 0, 0, 0};
-    float rmax = 0.f;
+    // codes in output (natural k) order: position j holds input position (j & ~7) | bitrev3(j & 7) when permuted; four
+    // codes per conversion pair, the residuals from the codes' decoded values (only their amax depends on all of them)
+    float v[16], r[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int sj = (j & ~7) | ((j & 1) << 2) | (j & 2) | ((j >> 2) & 1);
-        const float v = permuted ? val(sj) : val(j);
-        const uint32_t q = fq8_code(v, e);
-        cw[j >> 2] |= q << (8 * (j & 3));
-        r[j] = __fsub_rn(v, fq8_value(q, e));   // the residual, exact
-        rmax = fmaxf(rmax, fabsf(r[j]));
+        v[j] = permuted ? val(sj) : val(j);
+    }
+    uint32_t cw[4], cw2[4];
+    float rmax = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        cw[q] = fq8_code4_hw(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], e);
+        r[4 * q + 0] = __fsub_rn(v[4 * q + 0], fq8_value_hw<0>(cw[q], e));   // the residuals, exact
+        r[4 * q + 1] = __fsub_rn(v[4 * q + 1], fq8_value_hw<1>(cw[q], e));
+        r[4 * q + 2] = __fsub_rn(v[4 * q + 2], fq8_value_hw<2>(cw[q], e));
+        r[4 * q + 3] = __fsub_rn(v[4 * q + 3], fq8_value_hw<3>(cw[q], e));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rmax = fmaxf(rmax, fabsf(r[4 * q + i]));
     }
     rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 2));
     e2 = lo_exponent(rmax);
     uint32_t nz = 0;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const uint32_t q2 = fq8_code(r[j], e2);
-        nz |= q2 & 0x7Fu;
-        cw2[j >> 2] |= q2 << (8 * (j & 3));
+    for (int q = 0; q < 4; ++q) {
+        cw2[q] = fq8_code4_hw(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3], e2);
+        nz |= cw2[q] & 0x7F7F7F7Fu;
     }
     hi = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
     lo = v4i{(int)cw2[0], (int)cw2[1], (int)cw2[2], (int)cw2[3]};

@@ -184,11 +184,7 @@ __global__ void __launch_bounds__(UP_WAVES * 64, 4) moe_decode_up_kernel(const D
         const int e = fq8_exponent(amax);
         uint32_t cw[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            cw[j] = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) cw[j] |= fq8_code(f[4 * j + b], e) << (8 * b);
-        }
+        for (int j = 0; j < 4; ++j) cw[j] = fq8_code4_hw(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3], e);
         *(v4i*)(smem + row * LS + q * 16) = v4i{(int)cw[0], (int)cw[1], (int)cw[2], (int)cw[3]};
         if ((q & 1) == 0) lds_s[row * Ks + (q >> 1)] = (uint8_t)(e + 127);
     };

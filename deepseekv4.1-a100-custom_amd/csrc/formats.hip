@@ -206,27 +206,16 @@ __global__ void __launch_bounds__(256) quant_fp8_split_q4_kernel(const uint16_t*
         amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
         amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
         const int e = fq8_exponent(amax);
-        uint32_t cw = 0, cw2 = 0;
-        float rr[4], rmax = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = fq8_code(v[j], e);
-            cw |= c << (8 * j);
-            rr[j] = __fsub_rn(v[j], fq8_value(c, e));   // the residual, exact
-            rmax = fmaxf(rmax, fabsf(rr[j]));
-        }
+        const uint32_t cw = fq8_code4_hw(v[0], v[1], v[2], v[3], e);
+        float rr[4] = {__fsub_rn(v[0], fq8_value_hw<0>(cw, e)), __fsub_rn(v[1], fq8_value_hw<1>(cw, e)),   // the residuals, exact
+                       __fsub_rn(v[2], fq8_value_hw<2>(cw, e)), __fsub_rn(v[3], fq8_value_hw<3>(cw, e))};
+        float rmax = fmaxf(fmaxf(fabsf(rr[0]), fabsf(rr[1])), fmaxf(fabsf(rr[2]), fabsf(rr[3])));
         rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 8));
         rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 8));
         rmax = fmaxf(rmax, __shfl_xor(rmax, 4, 8));
         const int e2 = lo_exponent(rmax);
-        uint32_t any = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c2 = fq8_code(rr[j], e2);
-            any |= c2 & 0x7Fu;
-            cw2 |= c2 << (8 * j);
-        }
-        nz = any != 0;
+        const uint32_t cw2 = fq8_code4_hw(rr[0], rr[1], rr[2], rr[3], e2);
+        nz = (cw2 & 0x7F7F7F7Fu) != 0;
         *(uint32_t*)(hc + (long long)r * K + k0) = cw;
         *(uint32_t*)(lc + (long long)r * K + k0) = cw2;
         if ((q & 7) == 0) {
@@ -405,13 +394,11 @@ __global__ void __launch_bounds__(256) swiglu_quant_q4_kernel(const void* __rest
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
     const int e = fq8_exponent(amax);
-    uint32_t qc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qc[i] = fq8_code(h[i], e);
-    if (codes) *(uint32_t*)(codes + (long long)r * inter + c0) = qc[0] | (qc[1] << 8) | (qc[2] << 16) | (qc[3] << 24);
+    const uint32_t qw = fq8_code4_hw(h[0], h[1], h[2], h[3], e);
+    if (codes) *(uint32_t*)(codes + (long long)r * inter + c0) = qw;
     if (scales && (q & 7) == 0) scales[(long long)r * (inter >> 5) + (q >> 3)] = (uint8_t)(e + 127);
     if (hb) {
-        float o[4] = {fq8_value(qc[0], e), fq8_value(qc[1], e), fq8_value(qc[2], e), fq8_value(qc[3], e)};
+        float o[4] = {fq8_value_hw<0>(qw, e), fq8_value_hw<1>(qw, e), fq8_value_hw<2>(qw, e), fq8_value_hw<3>(qw, e)};
         if (permute) unpermute_quad(o, (q & 1) != 0);
         *(uint2*)(hb + (long long)r * inter + c0) = uint2{f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16),
                                                           f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16)};

@@ -41,6 +41,9 @@ struct GroupedArgs {
     // TERMS == 2: the second FP8 term of off-grid activations (dsv41_quant_fp8_split), same strides as xc / xs
     const uint8_t* xlc; const uint8_t* xls;
     const int* run_if;                       // optional: the launch does nothing when *run_if == 0
+    // XB: the activations as bf16 rows (xb [x_rows][ldxb], 8-k permuted when xb_perm) instead of codes: the workgroup
+    // splits its staged rows into the two FP8 terms itself (fp8_split16, the codes dsv41_quant_fp8_split writes)
+    const uint16_t* xb; long long ldxb; int xb_perm;
 };
 
 // LDS row stride for staged activation codes: +16 bytes so 16 rows fall in different banks
@@ -59,10 +62,13 @@ __device__ __forceinline__ int lds_stride(int K) { return K + 16; }
 // c < 8 is pair c's hi row, column c + 8 its lo row, so one MFMA per weight tile computes both terms and the epilogue
 // adds lane c + 8's accumulator to lane c's. For FP8-grid activations the lo codes are +0, so column c + 8 holds signed
 // zeros and the sum is the one-term result bit for bit; no flag is read.
-template <int TILED, int PF, int B_LDS, int NKC, int TERMS = 1>
+// XB (with TERMS == 2): the rows arrive as bf16 and are split into the two terms while being staged, after the first
+// weight tiles went out, so no quantiser launch precedes the GEMM (the same codes and bytes as dsv41_quant_fp8_split).
+template <int TILED, int PF, int B_LDS, int NKC, int TERMS = 1, int XB = 0>
 __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     static_assert(TERMS == 1 || B_LDS, "the second term is staged in LDS");
+    static_assert(!XB || TERMS == 2, "bf16 rows are split into two terms");
     if (a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nb = blockIdx.x * 4 + wave;
@@ -153,7 +159,44 @@ __global__ void __launch_bounds__(256) fp4_grouped_kernel(const GroupedArgs a) {
         };
         // the first weight tiles go out before the activations are staged: staging overlaps their latency
         if (active) pipeline_start<PF>(nk, load);
-        if (B_LDS) {
+        if (B_LDS && XB) {
+            __syncthreads();
+            // stage rows base .. base+mp-1 from bf16: thread i takes 16 values (chunk v of row r), a 32-group's two chunks
+            // on adjacent lanes (vpr is even, so a lane pair is in or out of the range together); every load of a round is
+            // issued before the first split
+            const int vpr = K >> 4;
+            constexpr int U = 2;
+            for (int i0 = threadIdx.x; i0 < mp * vpr; i0 += U * (int)blockDim.x) {
+                v4i w0[U], w1[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int i = i0 + u * (int)blockDim.x;
+                    const int r = i / vpr, v = i - r * vpr;
+                    const int t = i < mp * vpr ? a.pair_tok[base + r] : -1;
+                    const bool ok = t >= 0 && t < a.x_rows;
+                    const uint16_t* src = a.xb + (long long)(ok ? t : 0) * a.ldxb + v * 16;
+                    w0[u] = ok ? *(const v4i*)src : v4i{0, 0, 0, 0};
+                    w1[u] = ok ? *(const v4i*)(src + 8) : v4i{0, 0, 0, 0};
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int i = i0 + u * (int)blockDim.x;
+                    if (i < mp * vpr) {
+                        const int r = i / vpr, v = i - r * vpr;
+                        v4i hi, lo;
+                        int e, e2;
+                        fp8_split16(w0[u], w1[u], a.xb_perm, hi, lo, e, e2);
+                        *(v4i*)(smem + r * LS + v * 16) = hi;
+                        *(v4i*)(smem + lo_off + r * LS + v * 16) = lo;
+                        if ((v & 1) == 0) {
+                            lds_s[r * Ks + (v >> 1)] = (uint8_t)(e + 127);
+                            lds_s[lo_off + r * Ks + (v >> 1)] = (uint8_t)(e2 + 127);
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+        } else if (B_LDS) {
             __syncthreads();
             {
                 // stage rows base .. base+mp-1, both terms: each thread issues all loads of a round (16-byte code vectors,
@@ -966,11 +1009,11 @@ __global__ void __launch_bounds__(256) down_reduce_kernel(const DownSumArgs a, c
 // ------------------------------------------------------------------------------------------ C ABI
 #define B_LDS_MAX_BYTES (48 * 1024)
 
-template <int TILED, int B_LDS, int TERMS = 1>
+template <int TILED, int B_LDS, int TERMS = 1, int XB = 0>
 static void launch_grouped(const GroupedArgs& a, int G, size_t lds, hipStream_t st) {
     dim3 grid((unsigned)((a.N / 16 + 3) / 4), (unsigned)G);
     constexpr int PF = B_LDS ? DSV41_PF_UP : 8;
-    fp4_grouped_kernel<TILED, PF, B_LDS, 0, TERMS><<<grid, 256, lds, st>>>(a);
+    fp4_grouped_kernel<TILED, PF, B_LDS, 0, TERMS, XB><<<grid, 256, lds, st>>>(a);
 }
 
 static void launch_grouped_any(const GroupedArgs& a, int G, bool use_lds, int terms, size_t lds, hipStream_t st, int tiled) {
@@ -1033,6 +1076,37 @@ extern "C" int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, con
         b.vec_store = 0;
         launch_grouped_any(b, G, use_lds, 1, use_lds ? lds1 : 0, st, tiled);
     }
+    return (int)hipGetLastError();
+}
+
+// The same GEMM on bf16 activation rows x [x_rows][ldx] (elements; 8-k permuted when `permuted`): each workgroup splits
+// the rows it stages into the two FP8 terms (the codes dsv41_quant_fp8_split writes), so the GEMM needs no quantiser
+// launch before it. Only for passes whose two terms fit the LDS staging (min(max_tokens, 8) rows of K): otherwise
+// DSV41_EINVAL, and the caller quantises first (dsv41_quant_fp8_split) and calls dsv41_fp4_grouped_gemm.
+extern "C" int dsv41_fp4_grouped_gemm_bf16(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
+                                           int N, int K, const uint16_t* x, long long ldx, int x_rows, int permuted,
+                                           const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
+                                           float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
+                                           int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok,
+                                           void* stream) {
+    if (!W || !S || !x || !grp_expert || !grp_start || !pair_tok || !out) return DSV41_EINVAL;
+    if (N <= 0 || (N & 15) || K <= 0 || (K & 127) || G < 0 || ldo < N || ldx < K || max_tokens < 1) return DSV41_EINVAL;
+    if (accum < 0 || accum > 2 || (ldx & 7) || (((uintptr_t)x) & 15) || x_rows < 0 || n_pairs < 0 || out_rows < 0 || shard_n < 0)
+        return DSV41_EINVAL;   // 16-byte row pieces
+    if (stride_we < (long long)N * (K / 2) || stride_se < (long long)N * (K / 32) || stride_we >= OOB || stride_se >= OOB)
+        return DSV41_EINVAL;
+    const int rows2 = max_tokens < 8 ? max_tokens : 8;
+    const size_t one2 = (size_t)rows2 * (K + 16) + (size_t)rows2 * (K / 32);
+    const size_t lds2 = ((one2 + 15) & ~(size_t)15) + one2;
+    if (lds2 > B_LDS_MAX_BYTES) return DSV41_EINVAL;
+    if (G == 0 || n_pairs == 0) return 0;
+    GroupedArgs a{W, stride_we, S, stride_se, N, K, nullptr, 0, nullptr, 0, x_rows, grp_expert, grp_start, pair_tok, n_pairs, out, ldo,
+                  out_rows, out_row, pair_wt, shard_start, shard_n, zero_out, min_tok, max_tok, 0, accum, rows2, nullptr, nullptr, nullptr,
+                  x, ldx, permuted ? 1 : 0};
+    a.vec_store = ((ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0) ? 1 : 0;
+    hipStream_t st = (hipStream_t)stream;
+    if (tiled) launch_grouped<1, 1, 2, 1>(a, G, lds2, st);
+    else launch_grouped<0, 1, 2, 1>(a, G, lds2, st);
     return (int)hipGetLastError();
 }
 

@@ -287,9 +287,7 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
                     const int c0 = cb * 128 + 32 * cg;
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        uint32_t codes = 0;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
+                        const uint32_t codes = fq8_code4_hw(h[j][0], h[j][1], h[j][2], h[j][3], ex);
                         *(gmem_u32*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
                     }
                     if (kb == 0) *(gmem_u8*)(a.hs + p * a.ldhs + (c0 >> 5)) = (uint8_t)(ex + 127);
@@ -677,9 +675,7 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
                     const int c0 = cb * 128 + 32 * cg;
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        uint32_t codes = 0;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) codes |= fq8_code(h[j][i], ex) << (8 * i);
+                        const uint32_t codes = fq8_code4_hw(h[j][0], h[j][1], h[j][2], h[j][3], ex);
                         *(gmem_u32*)(a.hc + p * a.ldhc + c0 + 16 * j + 4 * kb) = codes;
                     }
                     if (kb == 0) *(gmem_u8*)(a.hs + p * a.ldhs + (c0 >> 5)) = (uint8_t)(ex + 127);

@@ -106,3 +106,29 @@ extern "C" int dsv41_selftest_stream(const uint8_t* src, long long tiles, int bl
     }
     return (int)hipGetLastError();
 }
+
+// FP8 conversion check: for input i, the code of v[i] at scale 2^e[i] by bit arithmetic (fq8_code_sw) and by the
+// hardware conversion (fq8_code2_hw, both halves of the pair), and the decoded value of the software code both ways.
+// out[5 i ..]: sw code, hw code (low byte of the pair), hw code (high byte), bits of the sw decode, bits of the hw decode.
+__global__ void __launch_bounds__(256) selftest_fp8_cvt_kernel(const float* v, const int* e, int n, uint32_t* out) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float x = v[i];
+    const int ex = e[i];
+    const uint32_t sw = fq8_code_sw(x, ex);
+    const uint32_t hw = fq8_code2_hw(x, -x, ex);
+    uint32_t* o = out + 5ll * i;
+    o[0] = sw;
+    o[1] = hw & 0xFFu;
+    o[2] = (fq8_code4_hw(0.f, 0.f, -x, x, ex) >> 24) & 0xFFu;   // the second pair's high byte: x again
+    o[3] = __float_as_uint(fq8_value(sw, ex));
+    o[4] = __float_as_uint(fq8_value_hw<0>(sw, ex));
+    (void)hw;
+}
+
+extern "C" int dsv41_selftest_fp8_cvt(const float* v, const int* e, int n, uint32_t* out, void* stream) {
+    if (!v || !e || !out || n < 0) return DSV41_EINVAL;
+    if (n == 0) return 0;
+    selftest_fp8_cvt_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(v, e, n, out);
+    return (int)hipGetLastError();
+}

@@ -30,6 +30,7 @@ SIGNATURES = {
     "dsv41_swiglu_quant": [P, I, LL, P, I, I, F, P, P, P, I, P],
     "dsv41_quant_fp8_split": [P, LL, I, LL, I, P, P, P, P, P, P],
     "dsv41_fp4_grouped_gemm": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
+    "dsv41_fp4_grouped_gemm_bf16": [P, LL, P, LL, I, I, I, P, LL, I, I, P, P, I, P, I, P, LL, I, P, P, I, I, I, I, I, I, I, P],
     "dsv41_moe_decode_up": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P, P,
                             P, LL, I, P, LL, P, LL, P],
     "dsv41_moe_decode_up_pairs": [P, LL, I, LL, P, F, F, I, I, P, P, I, I, I, P, LL, P, LL, P, LL, I, I, I, F, P, LL, P, LL, P, P, P, P, P,
@@ -59,6 +60,7 @@ SIGNATURES = {
     "dsv41_selftest_mfma_rate": [I, I, I, P, P],
     "dsv41_selftest_stream": [P, LL, I, I, I, P, P],
     "dsv41_selftest_mfma_bf16": [P, P, P, P],
+    "dsv41_selftest_fp8_cvt": [P, P, I, P, P],
 }
 
 _lib = None

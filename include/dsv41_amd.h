@@ -71,6 +71,19 @@ int dsv41_fp4_grouped_gemm(const uint8_t* W, long long stride_we, const uint8_t*
                            float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
                            int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
 
+/* dsv41_fp4_grouped_gemm on bf16 activations x [x_rows][ldx] (ldx in elements, a multiple of 8; x 16-byte aligned;
+ * 8-k permuted rows when permuted, as fp4_gemm_tc takes them, cukern.py:224-227): the kernel splits each staged row
+ * into the two FP8 terms of dsv41_quant_fp8_split itself, so the reference's bf16-activation call
+ * (cukern.fp4_gemm_tc / fp4_gemv_pairs, cukern.py:60-77, 238-276) runs as one launch. Only where both terms of
+ * min(max_tokens, 8) rows fit the kernel's 48 KiB of LDS staging, 2 (min(max_tokens, 8) (K + 16 + K / 32)) bytes
+ * rounded up to 16: otherwise -1 (the caller quantises with dsv41_quant_fp8_split and calls
+ * dsv41_fp4_grouped_gemm). */
+int dsv41_fp4_grouped_gemm_bf16(const uint8_t* W, long long stride_we, const uint8_t* S, long long stride_se, int tiled,
+                                int N, int K, const uint16_t* x, long long ldx, int x_rows, int permuted,
+                                const int* grp_expert, const int* grp_start, int G, const int* pair_tok, int n_pairs,
+                                float* out, long long ldo, int out_rows, const int* out_row, const float* pair_wt, int accum,
+                                int max_tokens, int shard_start, int shard_n, int zero_out, int min_tok, int max_tok, void* stream);
+
 /* Decode routing + up projection + SwiGLU in one launch (M <= 16 tokens, topk <= 16, E <= 512):
  * routing from fp32 logits [M][ldl] (gate_topk semantics, score_func 0 sqrt(softplus) / 1 sigmoid / 2 softmax;
  * bias may be NULL; the logits may be nparts partial sums part_stride floats apart, added in ascending order) or, with logits = NULL, from given eid_in / wt_in [M][topk]; the (token, expert) pairs are
@@ -322,6 +335,12 @@ int dsv41_selftest_mfma_rate(int mode, int blocks, int iters, float* out, void* 
  * workgroup barrier after every second tile (the prefill kernels' per-k-step synchronisation). out: one word, written only
  * if the bytes read XOR to one particular word (keeps the loads live). Bytes read per launch = 1024 tiles. */
 int dsv41_selftest_stream(const uint8_t* src, long long tiles, int blocks, int waves, int sync, unsigned* out, void* stream);
+
+/* FP8 conversion check (no counterpart in the reference: it validates this build's use of the gfx950 conversion
+ * instructions against the bit-arithmetic rounding of quant.py:45-54): for each of the n inputs, the E4M3 code of
+ * v[i] / 2^e[i] (clamped to +-448, round to nearest even) by bit arithmetic and by v_cvt_pk_fp8_f32 (both halves of a
+ * pair), and the value of the first code decoded by bit arithmetic and by v_cvt_f32_fp8. out: [n][5] words. */
+int dsv41_selftest_fp8_cvt(const float* v, const int* e, int n, uint32_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -166,6 +166,50 @@ def test_fp8_grid_input_is_bit_identical_to_one_term():
         assert torch.equal(got, one), name
 
 
+@pytest.mark.parametrize("permuted", [False, True])
+@pytest.mark.parametrize("K,max_tokens", [(3072, 1), (3072, 4), (7168, 1), (7168, 3)])
+def test_bf16_entry_splits_rows_like_the_quantiser(permuted, K, max_tokens):
+    """dsv41_fp4_grouped_gemm_bf16 (the kernel splits its staged bf16 rows into the two FP8 terms) equals the split
+    quantiser's codes through dsv41_fp4_grouped_gemm bit for bit: the same staged operands, the same MFMAs. Raw randn
+    rows with a few tiny and huge ones, pairs whose token row is outside the input (zeros), a group of an expert
+    outside the shard (rows zeroed), atomic accumulation into repeated output rows."""
+    from dsv41_amd import hipkern, quant
+    from test_gpu_moe import make_experts
+    E, N = 8, 256
+    w, s, _, _ = make_experts(E, K, N // 2, 17 + K + max_tokens)
+    wt_, st_ = quant.tile_fp4(w), quant.tile_fp4_scales(s)
+    X = 24
+    g = torch.Generator(device=DEV).manual_seed(5 + max_tokens)
+    x = torch.randn(X, K, generator=g, device=DEV)
+    x[3] *= 1e-4
+    x[4] *= 3e4
+    x = x.to(torch.bfloat16)
+    xin = hipkern.permute_x(x) if permuted else x
+    rng = np.random.default_rng(K + max_tokens)
+    sizes = [min(max_tokens, 1 + i % max_tokens) for i in range(6)]
+    ge, gs, tok, P = _groups(rng, sizes, E, X)
+    tok[0] = -1
+    tok[P - 1] = X + 3
+    assert hipkern.bf16_in_kernel(xin, K, max_tokens)
+    hc, hs, lc, ls, _ = quant.quant_fp8_split(xin, permuted=permuted, flag=False)
+    for shard_start, shard_n in ((0, 1 << 30), (1, E - 2)):
+        got = torch.full((P, N), 7.0, device=DEV)
+        ref = torch.full((P, N), 7.0, device=DEV)
+        hipkern.grouped_gemm_bf16(xin, permuted, wt_, st_, ge, gs, tok, got, max_tokens, True, shard_start=shard_start, shard_n=shard_n,
+                                  zero_out=True, n_pairs=P)
+        hipkern.grouped_gemm_codes(hc, hs, wt_, st_, ge, gs, tok, ref, max_tokens, True, shard_start=shard_start, shard_n=shard_n,
+                                   zero_out=True, n_pairs=P, lo=(lc, ls, None))
+        assert torch.equal(got, ref), f"shard {shard_start}"
+    wt = torch.from_numpy(rng.random(P).astype(np.float32)).to(DEV)
+    orow = torch.from_numpy((np.arange(P) % 3).astype(np.int32)).to(DEV)
+    got = torch.zeros(3, N, device=DEV)
+    ref = torch.zeros(3, N, device=DEV)
+    hipkern.grouped_gemm_bf16(xin, permuted, w, s, ge, gs, tok, got, max_tokens, False, pair_wt=wt, out_row=orow, accum=2, n_pairs=P)
+    hipkern.grouped_gemm_codes(hc, hs, w, s, ge, gs, tok, ref, max_tokens, False, pair_wt=wt, out_row=orow, accum=2, n_pairs=P,
+                               lo=(lc, ls, None))
+    torch.testing.assert_close(got, ref, rtol=1e-6, atol=1e-6 * float(ref.abs().max()))   # atomics: order may differ
+
+
 def test_swiglu_result_carries_its_fp8_operand():
     """fused.swiglu_quant writes the FP8 codes and E8M0 bytes of its result in the same launch and records them on the
     result: they equal the split quantiser's hi term of the result (lo codes all zero, flag 0) in both store orders.
