@@ -211,28 +211,29 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
     for (int u = 0; u < 4; ++u) tb_on[u] = 64 * ph + 16 * u < m;
     v4i OA[2][4], OB0[2][4], OB1[2][4];
     uint32_t OSA[2], OSB[2];   // E8M0 bytes of the 4 weight slots / 4 token blocks, byte j each (MFMA byte select)
+    // Every read of a step is issued before any is used: the token blocks unconditionally (a block without pairs reads
+    // stale bytes of its slot, which no MFMA takes) and each E8M0 byte into a register of its own, packed after the
+    // last read; a byte packed right behind its read would make each block wait for its own LDS round trip.
     auto read_ops = [&](int kk, int r, auto full_c) {
         constexpr bool full = decltype(full_c)::value;
         const uint8_t* st = smem + (kk % PV_NS) * PV_STAGE;
         if (full || tb_on[0]) {   // wave-uniform: a wave whose half of the group is empty runs no MFMA
-            uint32_t sa = 0;
+            uint32_t ab[4], bb[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 OA[r][j] = *(const v4i*)(st + PV_A + slot_of[j] * 1024 + lofs);
-                sa |= (uint32_t)st[PV_AS + slot_of[j] * 64 + col * 4 + kb] << (8 * j);
+                ab[j] = st[PV_AS + slot_of[j] * 64 + col * 4 + kb];
             }
-            OSA[r] = sa;
-        }
-        uint32_t sb = 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (!full && !tb_on[u]) continue;
-            const uint8_t* bt = st + PV_B + (4 * ph + u) * 2048 + lofs;
-            OB0[r][u] = *(const v4i*)bt;
-            OB1[r][u] = *(const v4i*)(bt + 1024);
-            sb |= (uint32_t)st[PV_BS + (64 * ph + 16 * u + col) * 4 + kb] << (8 * u);
+            for (int u = 0; u < 4; ++u) {
+                const uint8_t* bt = st + PV_B + (4 * ph + u) * 2048 + lofs;
+                OB0[r][u] = *(const v4i*)bt;
+                OB1[r][u] = *(const v4i*)(bt + 1024);
+                bb[u] = st[PV_BS + (64 * ph + 16 * u + col) * 4 + kb];
+            }
+            OSA[r] = ab[0] | (ab[1] << 8) | (ab[2] << 16) | (ab[3] << 24);
+            OSB[r] = bb[0] | (bb[1] << 8) | (bb[2] << 16) | (bb[3] << 24);
         }
-        OSB[r] = sb;
     };
     v4f acc[4][4];
 #pragma unroll
@@ -602,29 +603,31 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
     // per-lane LDS offsets within a stage: weight slots relative to slot_of[0], token blocks of this half, scales
     const uint32_t lofs_a = (uint32_t)(P2_A + slot_of[0] * 1024 + lofs), lofs_b = (uint32_t)(P2_B + ph * 2048 + lofs);
     const uint32_t lofs_as = (uint32_t)(P2_AS + slot_of[0] * 64 + col * 4 + kb), lofs_bs = (uint32_t)(P2_BS + 16 * ph * 4 + col * 4 + kb);
+    // Every read of a step is issued before any of them is used: the token blocks unconditionally (a block without
+    // pairs reads stale bytes of its slot, which no MFMA takes) and each E8M0 byte into a register of its own, packed
+    // after the last read. (Packing each byte right behind its read made every block wait for its own LDS round trip:
+    // eight serial round trips per step, the longest part of the step.)
     auto read_ops = [&](int st) {
         const uint32_t so = (uint32_t)st * P2_STAGE;
         const uint32_t oa = lofs_a + so, ob = lofs_b + so, osa = lofs_as + so, osb = lofs_bs + so;
+        uint32_t ab[4], bb[8];
         if (any_on) {   // wave-uniform: a wave whose half of the group is empty reads and computes nothing
-            uint32_t sa = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int dj = MODE == 0 ? (j < 2 ? j : 8 + (j - 2)) : j;   // slot_of[j] - slot_of[0]
                 OA[j] = *(const v4i*)(smem + oa + dj * 1024);
-                sa |= (uint32_t)smem[osa + dj * 64] << (8 * j);
+                ab[j] = smem[osa + dj * 64];
             }
-            OSA = sa;
-        }
-        uint32_t sb[2] = {0u, 0u};
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            if (!tb_on[u]) continue;
-            OB0[u] = *(const v4i*)(smem + ob + u * 4096);
-            OB1[u] = *(const v4i*)(smem + ob + u * 4096 + 1024);
-            sb[u >> 2] |= (uint32_t)smem[osb + u * 128] << (8 * (u & 3));
+            for (int u = 0; u < 8; ++u) {
+                OB0[u] = *(const v4i*)(smem + ob + u * 4096);
+                OB1[u] = *(const v4i*)(smem + ob + u * 4096 + 1024);
+                bb[u] = smem[osb + u * 128];
+            }
+            OSA = ab[0] | (ab[1] << 8) | (ab[2] << 16) | (ab[3] << 24);
+            OSB[0] = bb[0] | (bb[1] << 8) | (bb[2] << 16) | (bb[3] << 24);
+            OSB[1] = bb[4] | (bb[5] << 8) | (bb[6] << 16) | (bb[7] << 24);
         }
-        OSB[0] = sb[0];
-        OSB[1] = sb[1];
     };
     v4f acc[4][8];
 #pragma unroll
