@@ -349,8 +349,10 @@ __device__ __forceinline__ v4i buffer_load_tile(__amdgpu_buffer_rsrc_t r, uint32
 __device__ __forceinline__ int buffer_load_byte(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (int)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
 }
+// weight tiles in flight per wave in the grouped kernel with LDS-staged activation rows (decode-sized groups): 4 was
+// faster and steadier than 6, 8, 12 or 16 on the configs[1] drop-in sequences (alternating builds on one box)
 #ifndef DSV41_PF_UP
-#define DSV41_PF_UP 8
+#define DSV41_PF_UP 4
 #endif
 
 // ------------------------------------------------------------------------------------------ E4M3 weights -> bf16 MFMA operands
