@@ -33,10 +33,10 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 E, H, I, TOPK = 384, 7168, 1664, 8
 LIMIT = 10.0               # swiglu_limit of the reference tests (test_cpumoe.py:23)
 N_COPIES = 4
-# HBM bytes per launch of the dominant kernel (moe_decode_up_kernel, M = 1): rocprofv3 FETCH_SIZE 49,722.4 KiB and
+# HBM bytes per launch of the dominant kernel (moe_decode_up_kernel, M = 1): rocprofv3 FETCH_SIZE 49,706.1 KiB and
 # WRITE_SIZE 16.5 KiB per dispatch (medians of 2048), scaled by what the same counters read for a plain 512 MiB device
 # copy (FETCH x 2.000, WRITE x 1.000); summary and commands in profiles/moe_decode_up_kernel__configs1_decode_m1.txt
-UP_TRAFFIC_BYTES = int(round((49722.4 * 2.0 + 16.5 * 1.0) * 1024))
+UP_TRAFFIC_BYTES = int(round((49706.0625 * 2.0 + 16.46875 * 1.0) * 1024))
 
 
 def expert_bytes():
