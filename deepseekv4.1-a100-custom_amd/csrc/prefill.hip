@@ -42,7 +42,16 @@ struct PrefillArgs {
     int n_pairs;                              // group ranges are clamped to [0, n_pairs)
     int cbw, n_it;                            // column blocks per workgroup, workgroups per group (ceil(n_cb / cbw))
     const int* run_if;                        // MODE 2, optional: the launch does nothing when *run_if == 0
+    const int* grp_order;                     // optional: the order the items take the groups in (dsv41_group_order)
 };
+
+// The group an item's group index stands for: the index itself, or its place in grp_order (largest groups first, so no
+// long item starts near the end of the launch). An order entry outside [0, G) maps to G, which no item computes.
+__device__ __forceinline__ int item_group(const PrefillArgs& a, int g) {
+    if (!a.grp_order || g >= a.G) return g;
+    const int o = a.grp_order[g];
+    return (o >= 0 && o < a.G) ? o : a.G;
+}
 
 // ------------------------------------------------------------------------------------------ direct-to-LDS variant
 // A 256-row x 128-pair tile (MODE 0: 128 gate rows + the matching 128 up rows = 128 SwiGLU columns; MODE 1: 256
@@ -114,7 +123,7 @@ __device__ __forceinline__ void prefill_item128(const PrefillArgs& a, const int 
     __shared__ int s_row[PG_T];
 
     const int jx = L >> 3, gi = jx / a.n_it;
-    const int g = gi * 8 + (L & 7), cbi = jx - gi * a.n_it;
+    const int g = item_group(a, gi * 8 + (L & 7)), cbi = jx - gi * a.n_it;
     if (g >= a.G || cbi >= a.n_it) return;
     // this workgroup's column blocks cb0 .. cb0 + ncb - 1 of group g, one after another through one k-pipeline
     const int cb0 = cbi * a.cbw, ncb = CBL ? min(a.cbw, a.n_cb - cb0) : 1;
@@ -531,7 +540,7 @@ __device__ __forceinline__ void prefill_item256(const PrefillArgs& a, const int 
     __shared__ int s_row[P2_T];
 
     const int jx = L >> 3, gi = jx / a.n_it;
-    const int g = gi * 8 + (L & 7), cbi = jx - gi * a.n_it;
+    const int g = item_group(a, gi * 8 + (L & 7)), cbi = jx - gi * a.n_it;
     if (g >= a.G || cbi >= a.n_it) return;
     const int cb0 = cbi * a.cbw, ncb = CBL ? min(a.cbw, a.n_cb - cb0) : 1;
     if (ncb <= 0) return;
@@ -803,7 +812,7 @@ template <int MODE, int TILED>
 __global__ void __launch_bounds__(PG_THREADS) prefill_gemm_mixed_kernel(const PrefillArgs a) {
     if (MODE == 2 && a.run_if && __builtin_amdgcn_readfirstlane(*a.run_if) == 0) return;
     const int L = (int)blockIdx.x;
-    const int jx = L >> 3, g = (jx / a.n_it) * 8 + (L & 7);
+    const int jx = L >> 3, g = item_group(a, (jx / a.n_it) * 8 + (L & 7));
     if (g >= a.G) return;
     const int p0 = min(max(a.grp_start[g], 0), a.n_pairs), m = min(a.grp_start[g + 1], a.n_pairs) - p0;
     if (m > PG_T) prefill_item256<MODE, TILED>(a, L);
@@ -842,7 +851,7 @@ static int launch_prefill(PrefillArgs& a, int mode, int tiled, bool mixed, hipSt
 extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const uint8_t* W13, long long stride_we,
                                 const uint8_t* S13, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                                 const int* grp_start, int G, const int* tok_sorted, const float* wt_sorted, float limit, uint8_t* hc,
-                                long long ldhc, uint8_t* hs, long long ldhs, void* stream) {
+                                long long ldhc, uint8_t* hs, long long ldhs, const int* grp_order, void* stream) {
     if (!xc || !xs || !W13 || !S13 || !grp_expert || !grp_start || !tok_sorted || !wt_sorted || !hc || !hs) return DSV41_EINVAL;
     if (x_rows < 1 || (long long)x_rows * ldx > 0xFFFFFFFFll || (long long)x_rows * ldxs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || H < 128 * PG_PF || (H & 127) || I <= 0 || (I & 127) || G < 0 || ldx < H || (ldx & 15) || (((uintptr_t)xc) & 15) || ldxs < H / 32 ||
@@ -854,12 +863,13 @@ extern "C" int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t*
     if (G == 0) return 0;
     PrefillArgs a{xc, ldx, xs, ldxs, (uint32_t)(x_rows * ldx), (uint32_t)(x_rows * ldxs), W13, stride_we, S13, stride_se, 2 * I, H, E,
                   grp_expert, grp_start, G, tok_sorted, wt_sorted, limit, hc, ldhc, hs, ldhs, nullptr, 0, I / 128, 0, 0x7FFFFFFF};
+    a.grp_order = grp_order;
     return launch_prefill(a, 0, tiled, true, (hipStream_t)stream);
 }
 
 extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, int h_rows, const uint8_t* W2, long long stride_we,
                                   const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
-                                  const int* grp_start, int G, float* y2, long long ldy, void* stream) {
+                                  const int* grp_start, int G, float* y2, long long ldy, const int* grp_order, void* stream) {
     if (!hc || !hs || !W2 || !S2 || !grp_expert || !grp_start || !y2) return DSV41_EINVAL;
     if (h_rows < 1 || (long long)h_rows * ldhc > 0xFFFFFFFFll || (long long)h_rows * ldhs > 0xFFFFFFFFll) return DSV41_EINVAL;
     if (E < 1 || H <= 0 || (H & 255) || I < 128 * PG_PF || (I & 127) || G < 0 || ldhc < I || (ldhc & 15) || (((uintptr_t)hc) & 15) || ldhs < I / 32 ||
@@ -871,7 +881,44 @@ extern "C" int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8
     if (G == 0) return 0;
     PrefillArgs a{hc, ldhc, hs, ldhs, (uint32_t)(h_rows * ldhc), (uint32_t)(h_rows * ldhs), W2, stride_we, S2, stride_se, H, I, E,
                   grp_expert, grp_start, G, nullptr, nullptr, 0.f, nullptr, 0, nullptr, 0, y2, ldy, H / 256, 0, h_rows};
+    a.grp_order = grp_order;
     return launch_prefill(a, 1, tiled, true, (hipStream_t)stream);
+}
+
+// The groups of a dispatch ordered by pair count, largest first (a counting sort over the counts 0 .. 256 in one
+// workgroup; groups without an expert in the table (-1) count 0, and counts above 256 count 256, as the tile kernels
+// compute at most 256 pairs of a group). Within one count the order is whatever the LDS atomics give: the prefill
+// launches write disjoint rows per item, so their results do not depend on it.
+__global__ void __launch_bounds__(1024) group_order_kernel(const int* __restrict__ grp_expert, const int* __restrict__ grp_start, int G,
+                                                           int n_pairs, int* __restrict__ order) {
+    __shared__ int s_bin[258];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 258; i += 1024) s_bin[i] = 0;
+    __syncthreads();
+    auto bin_of = [&](int g) {   // 0 for 256 pairs .. 256 for none
+        if (grp_expert[g] < 0) return 256;
+        const int p0 = min(max(grp_start[g], 0), n_pairs), p1 = min(max(grp_start[g + 1], p0), n_pairs);
+        return 256 - min(p1 - p0, 256);
+    };
+    for (int g = tid; g < G; g += 1024) atomicAdd(&s_bin[bin_of(g)], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int b = 0; b < 257; ++b) {
+            const int c = s_bin[b];
+            s_bin[b] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int g = tid; g < G; g += 1024) order[atomicAdd(&s_bin[bin_of(g)], 1)] = g;
+}
+
+extern "C" int dsv41_group_order(const int* grp_expert, const int* grp_start, int G, int n_pairs, int* order, void* stream) {
+    if (!grp_expert || !grp_start || !order || G < 0 || n_pairs < 0) return DSV41_EINVAL;
+    if (G == 0) return 0;
+    group_order_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(grp_expert, grp_start, G, n_pairs, order);
+    return (int)hipGetLastError();
 }
 
 // The second FP8 term of off-grid activations (xlc / xls / lo_flag of dsv41_quant_fp8_split, all or none): checked like

@@ -38,8 +38,9 @@ SIGNATURES = {
     "dsv41_moe_down_sum": [P, LL, P, LL, I, I, I, P, LL, P, LL, I, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, LL, P, LL, I, F, P, LL,
                            P, P, P, P, LL, P],
     "dsv41_moe_down_sum_split": [P, LL, P, LL, I, I, I, P, LL, P, LL, P, P, P, I, I, P, LL, P, LL, P, LL, I, I, P, P, P, P, LL, P],
-    "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P],
-    "dsv41_prefill_down": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, LL, P],
+    "dsv41_prefill_up": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, P, F, P, LL, P, LL, P, P],
+    "dsv41_prefill_down": [P, LL, P, LL, I, P, LL, P, LL, I, I, I, I, P, P, I, P, LL, P, P],
+    "dsv41_group_order": [P, P, I, I, P, P],
     "dsv41_fp4_grouped_gemm_t128": [P, LL, P, LL, I, P, P, P, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, LL, P],
     "dsv41_rows_distinct": [P, I, P, I, P, P],
     "dsv41_fp4_grouped_gemm_scatter": [P, LL, P, LL, I, P, P, P, P, P, LL, P, LL, I, I, I, I, P, P, I, I, P, P, P, I, P, LL, I, P, LL, P],

@@ -366,7 +366,10 @@ PREFILL_GROUP = 256
 def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: ExpertWeights, limit: float) -> PrefillState:
     """First half of the prefill path: xq bf16 [T, H] on the FP8 grid -> E4M3 codes (exact); (token, expert) pairs
     bucketed by expert in groups of <= PREFILL_GROUP (moe_dispatch, p2p.cu:90-132); the w13 GEMM with the SwiGLU/FP8
-    epilogue: h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) (model.py:584-587, fused.py:284-306)."""
+    epilogue: h[p] = fq8(bf16(w_p * silu(min(g, L)) * clamp(u, +-L))) (model.py:584-587, fused.py:284-306). The w13
+    launch takes the groups largest first (dsv41_group_order), so no long item starts near the end of it: configs[3] w13
+    1149-1151 -> 1082-1087 us on one box. (The w2 launch keeps table order: its items are four times shorter, and
+    largest first made it slower, 720 -> 746 us, in the same A/B.)"""
     from .hipkern import moe_dispatch
     from .quant import quant_fp8_e8m0
     dev = _lib.require_cuda(xq, eid, wt)
@@ -381,9 +384,11 @@ def prefill_up(xq: torch.Tensor, eid: torch.Tensor, wt: torch.Tensor, ex: Expert
     G = min(P, ex.E + (P + gmax - 1) // gmax)   # groups of <= gmax pairs: at most E + P / gmax of them
     hc = torch.empty(P, I, dtype=torch.uint8, device=dev)
     hs = torch.empty(P, I // 32, dtype=torch.uint8, device=dev)
+    order = torch.empty(G, dtype=torch.int32, device=dev)
+    _lib.call("dsv41_group_order", _lib.ptr(grp_expert), _lib.ptr(grp_start), G, P, _lib.ptr(order), _lib.stream(dev))
     _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), T, _lib.ptr(ex.w13), ex.w13.stride(0), _lib.ptr(ex.s13),
               ex.s13.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(grp_expert), _lib.ptr(grp_start), G, _lib.ptr(tok_sorted),
-              _lib.ptr(wt_sorted), float(limit), _lib.ptr(hc), hc.stride(0), _lib.ptr(hs), hs.stride(0), _lib.stream(dev))
+              _lib.ptr(wt_sorted), float(limit), _lib.ptr(hc), hc.stride(0), _lib.ptr(hs), hs.stride(0), _lib.ptr(order), _lib.stream(dev))
     return PrefillState(T=T, k=k, P=P, G=G, tok_sorted=tok_sorted, wt_sorted=wt_sorted, inv=inv, grp_expert=grp_expert,
                         grp_start=grp_start, hc=hc, hs=hs, y2=None)
 
@@ -398,7 +403,7 @@ def prefill_down(st: PrefillState, ex: ExpertWeights, ys: torch.Tensor | None = 
     st.y2 = torch.empty(st.P, H, dtype=torch.float32, device=dev)
     _lib.call("dsv41_prefill_down", _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), st.P, _lib.ptr(ex.w2), ex.w2.stride(0),
               _lib.ptr(ex.s2), ex.s2.stride(0), 1 if ex.tiled else 0, ex.E, H, I, _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), st.G,
-              _lib.ptr(st.y2), st.y2.stride(0), s)
+              _lib.ptr(st.y2), st.y2.stride(0), None, s)
     if out is None and y32 is None:
         y32 = torch.empty(T, H, dtype=torch.float32, device=dev)
     _lib.call("dsv41_combine_pairs", _lib.ptr(st.y2), st.y2.stride(0), _lib.ptr(st.inv), st.k, T, H, _lib.ptr(ys), H if ys is None else ys.stride(0),

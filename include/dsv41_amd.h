@@ -169,18 +169,25 @@ int dsv41_moe_down_sum_split(const uint8_t* W, long long stride_we, const uint8_
  * h[p] = fq8(bf16(wt_sorted[p] * silu(min(g, L)) * clamp(u, +-L))) with gu = x[tok_sorted[p]] . deq(W13[e])^T;
  * x as E4M3 codes xc [x_rows][ldx] + E8M0 xs [x_rows][ldxs] (x_rows * ldx < 2^32); h as FP8 codes hc [P][ldhc]
  * + E8M0 hs [P][ldhs] in sorted pair order. H % 128 == 0, H >= 384, I % 64 == 0. Replaces the w13 grouped_fp4_gemm + swiglu_quant of
- * model.MoE.__call__ (model.py:584-587; moe_kernels.py:127-151; fused.py:283-345). */
+ * model.MoE.__call__ (model.py:584-587; moe_kernels.py:127-151; fused.py:283-345). grp_order (optional, [G]): the order
+ * the launch takes the groups in (dsv41_group_order: largest first); NULL: table order. The result is the same either way. */
 int dsv41_prefill_up(const uint8_t* xc, long long ldx, const uint8_t* xs, long long ldxs, int x_rows, const uint8_t* W13, long long stride_we,
                      const uint8_t* S13, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
                      const int* grp_start, int G, const int* tok_sorted, const float* wt_sorted, float limit, uint8_t* hc,
-                     long long ldhc, uint8_t* hs, long long ldhs, void* stream);
+                     long long ldhc, uint8_t* hs, long long ldhs, const int* grp_order, void* stream);
 
 /* Prefill w2: y2[p] = h[p] . deq(W2[e_g])^T (fp32 [P][ldy], sorted pair order) for the same groups; h_rows = P
  * (h_rows * ldhc < 2^32).
- * I % 128 == 0, I >= 384, H % 128 == 0. Replaces the w2 grouped_fp4_gemm of model.py:588. */
+ * I % 128 == 0, I >= 384, H % 128 == 0. Replaces the w2 grouped_fp4_gemm of model.py:588. grp_order: as in dsv41_prefill_up. */
 int dsv41_prefill_down(const uint8_t* hc, long long ldhc, const uint8_t* hs, long long ldhs, int h_rows, const uint8_t* W2, long long stride_we,
                        const uint8_t* S2, long long stride_se, int tiled, int E, int H, int I, const int* grp_expert,
-                       const int* grp_start, int G, float* y2, long long ldy, void* stream);
+                       const int* grp_start, int G, float* y2, long long ldy, const int* grp_order, void* stream);
+
+/* The groups 0 .. G-1 of a dispatch (moe_dispatch tables) ordered by pair count, largest first, into order [G] (a
+ * permutation; within one count the order is unspecified). Groups whose expert is -1 count 0; pair ranges are clamped to
+ * [0, n_pairs) and counts to 256. No counterpart in the reference: it lets the prefill launches start their longest items
+ * first, so none of them starts near the end of a launch (scheduling only, the results do not change). */
+int dsv41_group_order(const int* grp_expert, const int* grp_start, int G, int n_pairs, int* order, void* stream);
 
 /* The w2 kernel of the prefill path as a general grouped GEMM for groups of up to 128 pairs (the 256-row x 128-pair tile
  * kernel): for each group g (expert grp_expert[g] in [0, E), pairs grp_start[g] .. grp_start[g+1]-1, clamped to

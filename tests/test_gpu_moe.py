@@ -719,6 +719,52 @@ def _e4m3_values(codes, scales):
     return O.e4m3_decode(c) * np.repeat(s, 32, axis=1)
 
 
+def test_prefill_group_order_changes_nothing_but_the_order():
+    """dsv41_group_order: a permutation of the groups by pair count, largest first (padding and dropped groups last). Both
+    prefill launches write the same h codes, E8M0 bytes and y2 rows bit for bit with it as in table order (each item writes
+    its own rows), here with groups of a few pairs up to full 256-pair ones on both tile kernels."""
+    from dsv41_amd import _lib, moe, quant
+    E, I, H, k, T = 64, 384, 512, 6, 700
+    ws = make_experts(E, H, I, 611)
+    ex = to_ex(*ws, True)
+    rng = np.random.default_rng(13)   # Zipf(1.1) popularity: groups from a few pairs up to full 256-pair ones
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    pop = pop[rng.permutation(E)] / pop.sum()
+    eid = np.stack([rng.choice(E, k, replace=False, p=pop) for _ in range(T)]).astype(np.int32)
+    wt = rng.random((T, k)).astype(np.float32)
+    xq = quant.fake_quant_fp8(rand_x(T, H, 12).to(DEV))
+    st = moe.prefill_up(xq, torch.from_numpy(eid).to(DEV), torch.from_numpy(wt).to(DEV), ex, 10.0)   # w13 in size order
+    moe.prefill_down(st, ex)                                                                         # w2 in table order
+    P, G, dev = T * k, st.G, xq.device
+    order = torch.empty(G, dtype=torch.int32, device=dev)
+    _lib.call("dsv41_group_order", _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), G, P, _lib.ptr(order), _lib.stream(dev))
+    o = order.cpu().numpy()
+    ge, gs = st.grp_expert.cpu().numpy()[:G], st.grp_start.cpu().numpy()
+    cnt = np.where(ge >= 0, np.clip(gs[1:G + 1], 0, P) - np.clip(gs[:G], 0, P), 0)
+    assert sorted(o.tolist()) == list(range(G))
+    assert np.all(np.diff(np.minimum(cnt[o], 256)) <= 0), "not largest first"
+    assert cnt.max() > 128 and (cnt[cnt > 0] <= 16).any()
+    hc, hs, y2 = st.hc.clone(), st.hs.clone(), st.y2.clone()
+    xc, xs = quant.quant_fp8_e8m0(xq)
+
+    def up(order_ptr):
+        st.hc.zero_(); st.hs.zero_()
+        _lib.call("dsv41_prefill_up", _lib.ptr(xc), xc.stride(0), _lib.ptr(xs), xs.stride(0), T, _lib.ptr(ex.w13), ex.w13.stride(0),
+                  _lib.ptr(ex.s13), ex.s13.stride(0), 1, E, H, I, _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), G, _lib.ptr(st.tok_sorted),
+                  _lib.ptr(st.wt_sorted), 10.0, _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), order_ptr, _lib.stream(dev))
+
+    def down(order_ptr):
+        st.y2.zero_()
+        _lib.call("dsv41_prefill_down", _lib.ptr(st.hc), st.hc.stride(0), _lib.ptr(st.hs), st.hs.stride(0), P, _lib.ptr(ex.w2), ex.w2.stride(0),
+                  _lib.ptr(ex.s2), ex.s2.stride(0), 1, E, H, I, _lib.ptr(st.grp_expert), _lib.ptr(st.grp_start), G, _lib.ptr(st.y2),
+                  st.y2.stride(0), order_ptr, _lib.stream(dev))
+
+    up(None)                                                  # table order
+    assert torch.equal(st.hc, hc) and torch.equal(st.hs, hs)
+    down(_lib.ptr(order))                                     # size order
+    assert torch.equal(st.y2, y2)
+
+
 @pytest.mark.parametrize("tiled", [True, False])
 @pytest.mark.parametrize("limit", [10.0, 0.0])
 @pytest.mark.parametrize("H", [512, 768])
