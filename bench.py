@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import os
 import statistics
@@ -87,21 +88,49 @@ def make_layers(torch, dev, n, seed):
 REPLAYS = 50   # timed replays of each captured graph; the median is reported (p10 / p90 kept in graph_time.stats)
 
 
+def settle(torch):
+    """Free what the previous measurement left (Python garbage, torch's cached blocks) now, with the device idle: a
+    collection that falls inside the next measurement's timed replays cost it ~1.5 us per step (the drop-in decode
+    sequences after the offload leg: 40.5 instead of 38.9 us)."""
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
 def graph_time(torch, fn_steps, steps, warmup, replays=None):
     """Capture `steps` calls (fn_steps(i) for i in range(steps)) in one graph; replay it for warm-up, then REPLAYS times
     back to back with one HIP event pair around each replay (one synchronisation before and after the set). Returns
     (median seconds per step, graph); graph_time.stats holds the p10 / median / p90 per step and the replay count."""
+    settle(torch)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())   # inputs were produced on the current stream
     with torch.cuda.stream(s):
         for i in range(min(steps, 4)):
             fn_steps(i)                       # eager warm-up: workspaces allocated outside capture
     torch.cuda.synchronize()
+    # a first capture, replayed once and dropped: the first graph captured after another workload ran ~1 us per step slow
+    # through all its replays (the drop-in decode sequences: 40.4-40.9 against 38.9 us; the next capture of the same calls
+    # was not; gc, an emptied allocator cache, 25 ms of warm-up replays and a 10 s idle did not remove it)
+    g0 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g0, stream=s):
+        for i in range(steps):
+            fn_steps(i)
+    g0.replay()
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
             fn_steps(i)
+    del g0
     for _ in range(max(1, warmup // max(1, steps) + 1)):
+        g.replay()
+    # and at least ~25 ms of replays, so the clocks have settled at the load this graph puts on the device (a leg after a
+    # mostly idle one measured ~1.5 us per step slow on its first short warm-up)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    for _ in range(min(200, int(0.025 / max(time.perf_counter() - t0, 1e-6)))):
         g.replay()
     n = replays or REPLAYS
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
@@ -210,6 +239,7 @@ def bench_prefill(torch, dev, ex, T, iters=20, seed=31):
     (median over iters) and returns a dict."""
     import numpy as np
     from dsv41_amd import moe, quant
+    settle(torch)
     eid_np, wt_np = zipf_routing(T, seed)
     eid, wt = torch.from_numpy(eid_np).to(dev), torch.from_numpy(wt_np).to(dev)
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -846,6 +876,9 @@ def main():
         progress("layer with shared expert")
         extra["fp8_dense_gemv"] = bench_fp8_dense(torch, dev, K, W)
         progress("FP8 dense GEMV")
+        # the drop-in surfaces beside the other decode-sized legs (their decode sequences are the headline's shape)
+        extra["drop_in_surfaces"] = bench_surfaces(torch, dev, layers, min(K, 40), W)
+        progress("drop-in surfaces")
         for M in (4, 8, 16):
             t_m, uniq = bench_decode(torch, dev, layers, K, W, M, seed=100 + M)
             extra[f"decode_M{M}"] = {"us": round(t_m * 1e6, 2), "unique_experts": round(uniq, 2),
@@ -874,8 +907,6 @@ def main():
         progress("configs[4] stack and configs[0] GEMV")
         extra["offload"] = bench_offload(torch, dev)
         progress("offload paths")
-        extra["drop_in_surfaces"] = bench_surfaces(torch, dev, layers, min(K, 40), W)
-        progress("drop-in surfaces")
     if args.no_cpu:
         cpu = {"value": None, "note": "skipped"}
     else:
