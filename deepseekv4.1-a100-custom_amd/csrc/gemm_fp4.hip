@@ -1178,7 +1178,8 @@ extern "C" int dsv41_moe_down_sum(const uint8_t* W, long long stride_we, const u
     }
 #undef DS_LAUNCH_SH
     // weight tiles in flight per wave, measured at configs[1] (one token, 8 groups): 4 -> down launch 11.5 us, 12 -> 12.0,
-    // 2 -> 12.2; M = 4 (h rows in LDS, 32 groups) keeps 12 (4 in flight: 103.1 against 101.3 us per layer)
+    // 2 -> 12.2; and per layer 30.9 us with 4 against 31.0 / 31.05 / 31.2 us with 3 / 5 / 6; M = 4 (h rows in LDS, 32
+    // groups) keeps 12 (4 in flight: 103.1 against 101.3 us per layer)
     if (scl) { if (tiled) DS_LAUNCH(1, 4, 0, 1, 1); else DS_LAUNCH(0, 4, 0, 1, 1); }
     else if (h_lds) { if (tiled) DS_LAUNCH(1, 12, 0, 1, 0); else DS_LAUNCH(0, 12, 0, 1, 0); }
     else if (gs) { if (tiled) DS_LAUNCH(1, 6, 0, 0, 2); else DS_LAUNCH(0, 6, 0, 0, 2); }
