@@ -38,6 +38,13 @@ def test_attached_codes_follow_the_tensor_version():
     assert quant.attached_codes(x, False) is not None
     x.add_(1)
     assert quant.attached_codes(x, False) is None
+    # a set_ onto other storage, or a resize, drops it too
+    quant.attach_codes(x, codes, scales)
+    x.set_(torch.randn(4, 64).to(torch.bfloat16))
+    assert quant.attached_codes(x, False) is None
+    quant.attach_codes(x, codes, scales)
+    x.resize_(2, 128)
+    assert quant.attached_codes(x, False) is None
 
 
 def test_inference_tensors_carry_no_record():
