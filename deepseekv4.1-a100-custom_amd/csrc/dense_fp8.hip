@@ -49,19 +49,31 @@ __device__ __forceinline__ void fp8_store(const Fp8Args& a, const v4f (&sum)[MT]
     }
 }
 
-// WPG waves split the workgroup's chunk range; MT 16-token tiles share every weight tile (M <= 16 MT).
-template <int WPG, int PF, int MT, int TILED>
+// WPG waves split the workgroup's chunk range; MT 16-token tiles share every weight tile (M <= 16 MT). RB row blocks
+// per workgroup (16 RB rows): every activation load a wave makes then feeds RB weight tiles instead of one, so the
+// vector memory pipe carries 2 / RB KiB of activations per KiB of weights instead of 2 KiB. Row blocks 2q and 2q + 1
+// of a workgroup share their 32-row scale row (the first is even), and a row block past the last one reads the last
+// one again and stores nothing. RB > 1 needs gc == 0 or gc % (16 RB) == 0 (one x offset for all the blocks).
+template <int WPG, int PF, int MT, int TILED, int RB>
 __global__ void __launch_bounds__(WPG * 64) fp8_gemm_kernel(const Fp8Args a) {
-    __shared__ v4f s_red[WPG][MT][64];
+    __shared__ v4f s_red[WPG][RB * MT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, j = lane >> 4;
-    const int nb = blockIdx.x;
+    const int nbt = (a.N + 15) / 16;
+    const int nb = blockIdx.x * RB;
     const int c0 = a.nk * wave / WPG, c1 = a.nk * (wave + 1) / WPG;
-    const int row = min(nb * 16 + r, a.N - 1);   // rows past N (natural layout) read row N-1, never stored
-    const uint8_t* wp = TILED ? a.W + ((long long)nb * a.nk + c0) * 1024 + lane * 16
-                              : a.W + (long long)row * a.ldw + (long long)c0 * 64 + j * 16;
+    const uint8_t* wp[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+        const int nbr = min(nb + b, nbt - 1);
+        const int row = min(nbr * 16 + r, a.N - 1);   // rows past N (natural layout) read row N-1, never stored
+        wp[b] = TILED ? a.W + ((long long)nbr * a.nk + c0) * 1024 + lane * 16 : a.W + (long long)row * a.ldw + (long long)c0 * 64 + j * 16;
+    }
     constexpr long long wstep = TILED ? 1024 : 64;
-    const uint8_t* sp8 = a.S + (long long)(nb >> 1) * a.lds + 2 * c0 + (j >> 1);
+    constexpr int NS = (RB + 1) / 2;   // 32-row scale rows: row blocks 2q and 2q + 1 of the workgroup share one
+    const uint8_t* sp8[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) sp8[q] = a.S + (long long)(min(nb + 2 * q, nbt - 1) >> 1) * a.lds + 2 * c0 + (j >> 1);
     const long long goff = a.gc ? (long long)((nb * 16) / a.gc) * a.ldx : 0;
     const uint16_t* xp[MT];
 #pragma unroll
@@ -69,15 +81,19 @@ __global__ void __launch_bounds__(WPG * 64) fp8_gemm_kernel(const Fp8Args a) {
         const int t = min(mt * 16 + r, a.M - 1);   // token columns past M read row M-1, never stored
         xp[mt] = a.x + goff + (long long)t * a.ldt + (long long)c0 * 64 + j * 16;
     }
-    v4f acc[MT];
+    v4f acc[RB][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
-    v4i A[PF], X[PF][MT][2];
-    int SB[PF];
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[b][mt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4i A[PF][RB], X[PF][MT][2];
+    int SB[PF][NS];
     pipelined<PF>(c1 - c0,
         [&](int s, int c) {
-            A[s] = __builtin_nontemporal_load((const v4i*)(wp + (long long)c * wstep));
-            SB[s] = sp8[2 * c];
+#pragma unroll
+            for (int b = 0; b < RB; ++b) A[s][b] = __builtin_nontemporal_load((const v4i*)(wp[b] + (long long)c * wstep));
+#pragma unroll
+            for (int q = 0; q < NS; ++q) SB[s][q] = sp8[q][2 * c];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 X[s][mt][0] = *(const v4i*)(xp[mt] + (long long)c * 64);
@@ -85,27 +101,36 @@ __global__ void __launch_bounds__(WPG * 64) fp8_gemm_kernel(const Fp8Args a) {
             }
         },
         [&](int s) {
-            v8bf16_t lo, hi;
-            decode16(A[s], e8m0_to_f32((uint32_t)SB[s]), lo, hi);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf16_t, X[s][mt][0]), acc[mt], 0, 0, 0);
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf16_t, X[s][mt][1]), acc[mt], 0, 0, 0);
+            for (int b = 0; b < RB; ++b) {
+                v8bf16_t lo, hi;
+                decode16(A[s][b], e8m0_to_f32((uint32_t)SB[s][b >> 1]), lo, hi);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, __builtin_bit_cast(v8bf16_t, X[s][mt][0]), acc[b][mt], 0, 0, 0);
+                    acc[b][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, __builtin_bit_cast(v8bf16_t, X[s][mt][1]), acc[b][mt], 0, 0, 0);
+                }
             }
         });
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) s_red[wave][mt][lane] = acc[mt];
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) s_red[wave][b * MT + mt][lane] = acc[b][mt];
     __syncthreads();
     if (wave != 0) return;
-    v4f sum[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        sum[mt] = s_red[0][mt][lane];
+    for (int b = 0; b < RB; ++b) {
+        if (nb + b >= nbt) break;
+        v4f sum[MT];
 #pragma unroll
-        for (int w = 1; w < WPG; ++w) sum[mt] += s_red[w][mt][lane];
+        for (int mt = 0; mt < MT; ++mt) {
+            sum[mt] = s_red[0][b * MT + mt][lane];
+#pragma unroll
+            for (int w = 1; w < WPG; ++w) sum[mt] += s_red[w][b * MT + mt][lane];
+        }
+        const int n0 = (nb + b) * 16 + 4 * j;   // the accumulator of lane l holds rows 4 (l / 16) .. +3, token l % 16
+        fp8_store<MT>(a, sum, n0, r);
     }
-    const int n0 = nb * 16 + 4 * j;   // the accumulator of lane l holds rows 4 (l / 16) .. +3, token l % 16
-    fp8_store<MT>(a, sum, n0, r);
 }
 
 // M <= 4 tokens (every wave owning at least one chunk): each wave first copies its own k range of the activations and of its row block's scale bytes into a
@@ -250,15 +275,15 @@ __global__ void dequant_fp8_kernel(const uint8_t* __restrict__ W, long long ldw,
 }
 
 // ------------------------------------------------------------------------------------------ entry points
-template <int MT, int PF>
+template <int MT, int PF, int RB = 1>
 static void fp8_launch_pf(const Fp8Args& a, int tiled, bool wide, hipStream_t st) {
-    const dim3 grid((a.N + 15) / 16);
+    const dim3 grid(((a.N + 15) / 16 + RB - 1) / RB);
     if (wide) {
-        if (tiled) fp8_gemm_kernel<16, PF, MT, 1><<<grid, 1024, 0, st>>>(a);
-        else fp8_gemm_kernel<16, PF, MT, 0><<<grid, 1024, 0, st>>>(a);
+        if (tiled) fp8_gemm_kernel<16, PF, MT, 1, RB><<<grid, 1024, 0, st>>>(a);
+        else fp8_gemm_kernel<16, PF, MT, 0, RB><<<grid, 1024, 0, st>>>(a);
     } else {
-        if (tiled) fp8_gemm_kernel<8, PF, MT, 1><<<grid, 512, 0, st>>>(a);
-        else fp8_gemm_kernel<8, PF, MT, 0><<<grid, 512, 0, st>>>(a);
+        if (tiled) fp8_gemm_kernel<8, PF, MT, 1, RB><<<grid, 512, 0, st>>>(a);
+        else fp8_gemm_kernel<8, PF, MT, 0, RB><<<grid, 512, 0, st>>>(a);
     }
 }
 
@@ -271,6 +296,17 @@ static void fp8_launch(const Fp8Args& a, int tiled, hipStream_t st) {
     // <= 128 VGPRs: two 8-wave workgroups per CU. One token tile: 6 tiles in flight per wave, 3 when a wave has fewer
     // than 6 chunks (measured at 16 / 8 rows: 32768 x 1280 17.9 -> 15.1 / 14.8 -> 11.0 us; the other reference shapes
     // within 1 %, and 2 / 4 / 8 in flight no better)
+    // one token tile over >= 256 row blocks: two row blocks per 8-wave workgroup (every activation load feeds two
+    // weight tiles), 4 tiles in flight per wave, 3 when a wave has fewer than 4 chunks. Measured at 16 / 8 rows (median
+    // of 50 graph replays, against one row block per workgroup): 5120 x 8192 20.4 -> 14.4 / 14.9 -> 12.0 us,
+    // 4608 x 5120 14.3 -> 10.6 / 10.7 -> 9.0, 32768 x 1280 15.6 -> 12.1 / 11.4 -> 10.5, 5120 x 2304 7.6 -> 6.5 / 6.1 ->
+    // 6.0; 16-wave workgroups were level or slower, four row blocks per workgroup slower (5120 x 8192: 19.8 / 17.4), and
+    // fewer row blocks (1280 x 5120: 40 workgroups) slower (8.2 -> 9.9 at 16 rows), so they keep one block each
+    if (MT == 1 && nb >= 256 && (a.gc == 0 || a.gc % 32 == 0)) {
+        if (a.nk < 32) fp8_launch_pf<1, 3, 2>(a, tiled, false, st);
+        else fp8_launch_pf<1, 4, 2>(a, tiled, false, st);
+        return;
+    }
     if (MT == 1 && a.nk < 6 * (wide ? 16 : 8)) fp8_launch_pf<MT, 3>(a, tiled, wide, st);
     else fp8_launch_pf<MT, MT == 1 ? 6 : MT == 2 ? 4 : 2>(a, tiled, wide, st);
 }

@@ -67,18 +67,18 @@ def test_dequant_fp8_every_code_and_scale(tiled):
 
 
 @pytest.mark.parametrize("tiled", [False, True])
-@pytest.mark.parametrize("rows", [4, 16, 64])
-def test_fp8_gemm_decode_one_hot_exact(tiled, rows):
+@pytest.mark.parametrize("rows,N", [(4, 256), (16, 256), (64, 256), (16, 4112)])
+def test_fp8_gemm_decode_one_hot_exact(tiled, rows, N):
     """One-hot activation rows make each output one product: out[t, n] = x[t, k_t] * deq[n, k_t] exactly. Launches of
-    `rows` tokens (4: the LDS-staged kernel; 16 and 64: one and four token tiles) cover every k position of the first
-    256 (every lane group and both MFMA halves) and a spread beyond, over rows holding every E4M3 code, with scale bytes
-    90..160 (products normal in bf16)."""
+    `rows` tokens (4: the LDS-staged kernel; 16 and 64: one and four token tiles; 16 over 257 row blocks: two row
+    blocks per workgroup, the last one alone) cover every k position of the first 256 (every lane group and both MFMA
+    halves) and a spread beyond, over rows holding every E4M3 code, with scale bytes 90..160 (products normal in bf16)."""
     from dsv41_amd import hipkern, w8
-    N, K = 256, 1024
+    K = 1024
     g = torch.Generator().manual_seed(11)
     w = torch.stack([torch.cat([torch.randperm(256, generator=g) for _ in range(K // 256)]) for _ in range(N)]).to(torch.uint8)
     w[(w & 0x7F) == 0x7F] = 0
-    s = torch.randint(90, 161, (N // 32, K // 32), generator=g, dtype=torch.uint8)
+    s = torch.randint(90, 161, ((N + 31) // 32, K // 32), generator=g, dtype=torch.uint8)
     deq = O.bf16_bits_to_f32(O.dequant_fp8_block(w.numpy(), s.numpy()))
     wd = (w8.tile(w) if tiled else w).to(DEV)
     sd = s.to(DEV)
@@ -102,6 +102,10 @@ SHAPES = [(1, 512, 5120, 0), (1, 1280, 5120, 0), (1, 32768, 1280, 0), (6, 5120, 
 SHAPES += [(2, 32768, 1280, 0), (1, 4608, 5120, 0), (3, 512, 5120, 0), (4, 5120, 8192, 0), (4, 1280, 8192, 0)]
 # and of the 5-16-row kernel with 3 tiles in flight (fewer than 6 chunks per wave): 8 and 16 waves per workgroup
 SHAPES += [(12, 32768, 1280, 0), (16, 5120, 2304, 0), (16, 1280, 5120, 0)]
+# the 5-16-row kernel's two-row-block workgroups: an odd row-block count (the last workgroup's second block past the
+# end), 8-wave workgroups (K < 4096), column groups of 32 rows (both blocks share one x offset) and of 16 (one block
+# per workgroup)
+SHAPES += [(16, 4112, 4096, 0), (5, 4112, 1280, 0), (9, 4096, 1024, 32), (7, 4096, 1024, 16)]
 
 
 @pytest.mark.parametrize("M,N,K,gc", SHAPES)
@@ -122,6 +126,32 @@ def test_fp8_gemm_reference_shapes(M, N, K, gc):
     # natural row-major layout: the same sums in the same order
     yn = hipkern.fp8_gemm_tc(x, w.to(DEV), sd, group_cols=gc, out_dtype=torch.float32, tiled=False)
     assert torch.equal(yn, y32)
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 4104, 2048), (6, 4136, 4096), (16, 1000, 2048)])
+def test_fp8_gemm_natural_rows_not_a_multiple_of_16(M, N, K):
+    """Natural layout with N % 16 != 0 on the 5-16-row kernel: the last row block's rows past N are read clamped and
+    never stored, and a two-block workgroup's second block past the last one stores nothing."""
+    from dsv41_amd import hipkern
+    w, s = rand_fp8(N, K, seed=N + K)
+    x = (torch.randn(M, K, generator=torch.Generator().manual_seed(3)) * 2).to(torch.bfloat16).to(DEV)
+    ref = O.linear_fp8w(O.bf16_bits_to_f32(u16(x)), w.numpy(), s.numpy())
+    y = hipkern.fp8_gemm_tc(x, w.to(DEV), s.to(DEV), out_dtype=torch.float32, tiled=False)
+    check_close(y.cpu().numpy(), ref, f"M={M} N={N} K={K}")
+    assert y.shape == (M, N)
+
+
+def test_fp8_gemm_rejects_short_scales():
+    """A scale tensor with fewer than ceil(N / 32) rows or K / 32 columns is refused on the host, before any launch
+    (the kernels read scale row n // 32 of every weight row)."""
+    from dsv41_amd import hipkern
+    N, K = 4112, 1024
+    w, s = rand_fp8(N, K, seed=5)
+    x = torch.randn(16, K).to(torch.bfloat16).to(DEV)
+    with pytest.raises(ValueError):
+        hipkern.fp8_gemm_tc(x, w.to(DEV), s[: N // 32].contiguous().to(DEV), out_dtype=torch.float32)
+    with pytest.raises(ValueError):
+        hipkern.fp8_gemm_tc(x, w.to(DEV), s[:, :-1].contiguous().to(DEV), out_dtype=torch.float32)
 
 
 def test_fp8_gemm_deterministic_wide_and_narrow():
