@@ -293,20 +293,21 @@ static void fp8_launch(const Fp8Args& a, int tiled, hipStream_t st) {
     // few row blocks: 16 waves per workgroup so the K split still fills the CUs (not for 4 token tiles, whose
     // registers do not fit 16 waves per CU)
     const bool wide = MT <= 2 && nb < 256 && a.nk >= 64;
-    // <= 128 VGPRs: two 8-wave workgroups per CU. One token tile: 6 tiles in flight per wave, 3 when a wave has fewer
-    // than 6 chunks (measured at 16 / 8 rows: 32768 x 1280 17.9 -> 15.1 / 14.8 -> 11.0 us; the other reference shapes
-    // within 1 %, and 2 / 4 / 8 in flight no better)
-    // one token tile over >= 256 row blocks: two row blocks per 8-wave workgroup (every activation load feeds two
-    // weight tiles), 4 tiles in flight per wave, 3 when a wave has fewer than 4 chunks. Measured at 16 / 8 rows (median
-    // of 50 graph replays, against one row block per workgroup): 5120 x 8192 20.4 -> 14.4 / 14.9 -> 12.0 us,
+    // >= 256 row blocks: two row blocks per 8-wave workgroup (every activation load feeds two weight tiles); one token
+    // tile: 4 tiles in flight per wave, 3 when a wave has fewer than 4 chunks; two: 3; four: 2. Measured (median of 50
+    // graph replays, against one row block per workgroup): 16 / 8 rows 5120 x 8192 20.4 -> 14.4 / 14.9 -> 12.0 us,
     // 4608 x 5120 14.3 -> 10.6 / 10.7 -> 9.0, 32768 x 1280 15.6 -> 12.1 / 11.4 -> 10.5, 5120 x 2304 7.6 -> 6.5 / 6.1 ->
-    // 6.0; 16-wave workgroups were level or slower, four row blocks per workgroup slower (5120 x 8192: 19.8 / 17.4), and
-    // fewer row blocks (1280 x 5120: 40 workgroups) slower (8.2 -> 9.9 at 16 rows), so they keep one block each
-    if (MT == 1 && nb >= 256 && (a.gc == 0 || a.gc % 32 == 0)) {
-        if (a.nk < 32) fp8_launch_pf<1, 3, 2>(a, tiled, false, st);
-        else fp8_launch_pf<1, 4, 2>(a, tiled, false, st);
+    // 6.0; 32 / 64 rows 5120 x 8192 33.9 -> 21.0 / 63.7 -> 36.4, 32768 x 1280 27.8 -> 20.1 / 52.3 -> 38.4. 16-wave
+    // workgroups were level or slower, four row blocks per workgroup slower (5120 x 8192 at 16 rows: 19.8), and fewer
+    // row blocks (1280 x 5120: 40 workgroups) slower (8.2 -> 9.9 at 16 rows), so they keep one block each
+    if (nb >= 256 && (a.gc == 0 || a.gc % 32 == 0)) {
+        if (MT == 1 && a.nk < 32) fp8_launch_pf<1, 3, 2>(a, tiled, false, st);
+        else fp8_launch_pf<MT, MT == 1 ? 4 : MT == 2 ? 3 : 2, 2>(a, tiled, false, st);
         return;
     }
+    // one row block per workgroup, <= 128 VGPRs: two 8-wave workgroups per CU. One token tile: 6 tiles in flight per
+    // wave, 3 when a wave has fewer than 6 chunks (measured at 16 / 8 rows: 32768 x 1280 17.9 -> 15.1 / 14.8 -> 11.0 us;
+    // the other reference shapes within 1 %, and 2 / 4 / 8 in flight no better)
     if (MT == 1 && a.nk < 6 * (wide ? 16 : 8)) fp8_launch_pf<MT, 3>(a, tiled, wide, st);
     else fp8_launch_pf<MT, MT == 1 ? 6 : MT == 2 ? 4 : 2>(a, tiled, wide, st);
 }
