@@ -875,6 +875,8 @@ def main():
         del shared8
         progress("layer with shared expert")
         extra["fp8_dense_gemv"] = bench_fp8_dense(torch, dev, K, W)
+        # and 16 rows (the 5-16-row kernel, test_fp8_tc.py:19's 16-row case), FP8 only
+        extra["fp8_dense_gemm_16_rows"] = bench_fp8_dense(torch, dev, K, W, rows=16, with_bf16=False)
         progress("FP8 dense GEMV")
         # the drop-in surfaces beside the other decode-sized legs (their decode sequences are the headline's shape)
         extra["drop_in_surfaces"] = bench_surfaces(torch, dev, layers, min(K, 40), W)
