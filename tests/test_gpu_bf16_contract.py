@@ -5,7 +5,9 @@ test cases:
     randn activations, scale bytes 110..134, block_m 16 / 64, row-major weights;
   * test_fp4_tcw.py:10-45 -- fp4_gemm_tc, E 48, N 4608, K 5120, tiled weights, scale bytes 112..127, its seven group
     mixes (groups split at 64 pairs), FP8-grid activations as that test uses, and raw ones;
-  * test_fp4_tc.py:34-46 -- fp4_gemm_tc and fp4_gemv_pairs, E 8, N 4608, K 5120, G experts x M tokens.
+  * test_fp4_tc.py:34-46 -- fp4_gemm_tc and fp4_gemv_pairs, E 8, N 4608, K 5120, G experts x M tokens;
+  * test_kernels.py:12-20 -- its dense FP4 GEMM shapes (M 1 / 7 / 64 / 300, N x K 2304 x 5120 and 5120 x 2304) as
+    one-expert grouped GEMMs, row-major and tiled.
 The reference value is the textbook sum in float64 over the dequantised weights (dsv41_dequant_fp4, bit-exact with the
 reference's quant.dequant_fp4 over every code and scale byte, tests/test_gpu_formats.py; checked against the numpy
 oracle's dense_weights here too), the same computation the reference's tests make. Tolerances: the reference tests'
@@ -446,3 +448,24 @@ def test_reference_test_fp4_tc_cases(tcw_weights, grid):
         check(y, ref, f"test_fp4_tc.py fp4_gemm_tc G={G} M={M} ({grid})")
         y2 = hipkern.fp4_gemv_pairs(x, w8, s8, pair_tok, experts.repeat_interleave(M), torch.ones(P, device=DEV), P)
         check(y2, ref, f"test_fp4_tc.py fp4_gemv_pairs G={G} M={M} ({grid})")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 2304, 5120), (7, 5120, 2304), (64, 2304, 5120), (300, 5120, 2304)])
+@pytest.mark.parametrize("tiled", [False, True])
+def test_reference_test_kernels_fp4_gemm_shapes(M, N, K, tiled):
+    """test_kernels.py:12-20's dense FP4 GEMM cases (M x N x K, random bytes, scale bytes 110..134, raw randn bf16 a,
+    max|err| / max|ref| < 2e-3) as one-expert grouped GEMMs: every row of a is a pair on expert 0 (GroupedPairs with
+    block_m 16 up to 16 rows, else 64, so 300 rows take two 256-pair groups). The dense kernel that test drives is
+    outside this build's scope; the grouped surface computes the same product."""
+    from dsv41_amd import moe_kernels, quant
+    g = torch.Generator(device=DEV).manual_seed(7 * M + N)
+    w = torch.randint(0, 256, (1, N, K // 2), generator=g, dtype=torch.uint8, device=DEV)
+    s = torch.randint(110, 135, (1, N, K // 32), generator=g, dtype=torch.uint8, device=DEV)
+    a = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    ref = a.double() @ Dense(w, s, False)[0].T
+    wk, sk = (quant.tile_fp4(w), quant.tile_fp4_scales(s)) if tiled else (w, s)
+    rows = torch.arange(M, device=DEV)
+    pairs = moe_kernels.GroupedPairs(torch.zeros(M, dtype=torch.int32, device=DEV), rows, rows.clone(),
+                                     torch.ones(M, device=DEV), block_m=16 if M <= 16 else 64)
+    out = moe_kernels.grouped_fp4_gemm(a, wk, sk, pairs, M, tiled=tiled)
+    check(out, ref, f"test_kernels.py fp4_gemm M={M} N={N} K={K} tiled={tiled}")
